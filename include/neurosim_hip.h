@@ -1,0 +1,184 @@
+/*
+ * neurosim_hip.h -- C ABI of the MI355X (gfx950) dendritic tick library.
+ *
+ * This library replaces the pybind11 module `neurosim_gpu_native` that the
+ * reference JIT-builds from csrc/bindings.cpp + csrc/compartmental.cu.  Every
+ * entry point takes plain device pointers, sizes and strides (no framework
+ * types), validates its arguments on the host, returns NS_OK or an error code,
+ * and never synchronises the host.  Kernels are enqueued on the caller's
+ * stream (a hipStream_t passed as void*; NULL means the legacy default
+ * stream).  Nothing here allocates device memory: outputs and workspaces are
+ * owned by the caller.
+ *
+ * Dynamics implemented by the tick (one (neuron n, column b) pair):
+ *   j      = sum_e W[n, col[e]] * s[b, col[e]]            (CSR row n)
+ *   d'     = rho_d*d + (1-rho_d)*tanh(j + dendritic_drive)
+ *   u      = (1-c)*j + c*d' - k*a
+ *   s'     = clamp(alpha*s + (1-alpha)*(gain*tanh(u + drive)), 0, 1)
+ *   a'     = rho_a*a + (1-rho_a)*s'
+ * with the parameter order of the reference (native_compartmental.py:20-23):
+ *   [alpha, gain, dendrite_decay (rho_d), adaptation_decay (rho_a),
+ *    coupling (c), adaptation_strength (k)].
+ */
+#ifndef NEUROSIM_HIP_H
+#define NEUROSIM_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NS_ABI_VERSION 1
+
+/* Return codes. */
+#define NS_OK 0
+#define NS_ERR_INVALID 1   /* argument validation failed; nothing was launched */
+#define NS_ERR_LAUNCH 2    /* the HIP runtime rejected a launch */
+
+/* CSR weight encodings (reference: csrc/compartmental.cu:92-119). */
+#define NS_WEIGHT_F32 0    /* float32[M] */
+#define NS_WEIGHT_F16 1    /* IEEE binary16[M] */
+#define NS_WEIGHT_E4M3 2   /* OCP fp8 e4m3fn codes uint8[M] x float32 global scale */
+#define NS_WEIGHT_NVFP4 3  /* e2m1 nibbles uint8[ceil(M/2)] (even edge in the low nibble),
+                              e4m3fn block scales uint8[ceil(M/16)] (16 edges per block, in
+                              CSR order), float32 global scale */
+
+/* A [B,N] float32 operand read as data[b*stride_b + n*stride_n].  A NULL
+ * `data` means every element equals `scalar` (the reference's
+ * `input=None, input_scalar=x` convention, compartmental.cu:41-45). */
+typedef struct ns_plane {
+  const float* data;
+  int64_t stride_b;
+  int64_t stride_n;
+  float scalar;
+} ns_plane;
+
+/* A [B,N] float32 output written as data[b*stride_b + n*stride_n]. */
+typedef struct ns_out_plane {
+  float* data;
+  int64_t stride_b;
+  int64_t stride_n;
+} ns_out_plane;
+
+/* An [N] float32 vector read as data[n*stride]; stride 0 broadcasts one value. */
+typedef struct ns_vector {
+  const float* data;
+  int64_t stride;
+} ns_vector;
+
+/* Destination-major CSR matrix W[N,N] (row = target neuron, col = source). */
+typedef struct ns_csr {
+  int64_t n_rows;              /* N */
+  int64_t n_edges;             /* M */
+  const int32_t* rowptr;       /* [N+1], rowptr[0] = 0, rowptr[N] = M, non-decreasing */
+  const int32_t* col;          /* [M], each in [0, N) */
+  const void* weight;          /* encoding given by `format` */
+  int32_t format;              /* NS_WEIGHT_* */
+  const uint8_t* block_scales; /* NVFP4 only, else NULL */
+  const float* global_scale;   /* device float32[1]; E4M3/NVFP4 only, else NULL */
+} ns_csr;
+
+/* Row blocks produced by ns_plan_row_blocks and copied to the device:
+ * `bounds` holds (row, edge) int32 pairs for block boundaries 0..n_blocks,
+ * bounds[2k] = first row of block k, bounds[2k+1] = rowptr[that row]. */
+typedef struct ns_row_plan {
+  const int32_t* bounds;       /* device int32[2*(n_blocks+1)] */
+  int64_t n_blocks;
+  int32_t block_edges;         /* edge capacity the plan was built for */
+  int32_t reserved;
+} ns_row_plan;
+
+/* Arguments of one fused matrix tick. */
+typedef struct ns_step_args {
+  int64_t n_neurons;           /* N > 0 */
+  int64_t batch;               /* B >= 0; B == 0 launches nothing */
+  ns_plane state;              /* s_t   (data required) */
+  ns_plane dendrite;           /* d_t   (data required) */
+  ns_plane adaptation;         /* a_t   (data required) */
+  ns_plane drive;              /* somatic drive u        (data or scalar) */
+  ns_plane dendritic_drive;    /* dendritic drive v      (data or scalar) */
+  ns_vector params[6];         /* alpha, gain, rho_d, rho_a, coupling, strength */
+  ns_csr matrix;
+  ns_row_plan plan;
+  ns_out_plane out_state;      /* s_{t+1}; must not overlap any input */
+  ns_out_plane out_dendrite;   /* d_{t+1} */
+  ns_out_plane out_adaptation; /* a_{t+1} */
+} ns_step_args;
+
+/* Arguments of one PELS event tick (advance + emit, then scatter). */
+typedef struct ns_event_args {
+  int64_t n_neurons;
+  int64_t batch;
+  ns_plane state, dendrite, adaptation;
+  ns_plane drive, dendritic_drive;
+  ns_vector params[6];
+  float* current;              /* persistent synaptic current, [B,N] read as
+                                  current[b*current_stride_b + n*current_stride_n];
+                                  read by the advance, then updated in place */
+  int64_t current_stride_b;
+  int64_t current_stride_n;
+  ns_plane emitted;            /* last emitted somatic state (data required) */
+  ns_vector theta;             /* per-neuron emission threshold */
+  const int32_t* out_rowptr;   /* source-major CSR: [N+1] */
+  const int32_t* dst;          /* [M] target of each source-major edge */
+  const int32_t* weight_index; /* [M] position of that edge in `weight` */
+  const float* weight;         /* [M] destination-major float32 weights */
+  int64_t n_edges;
+  ns_out_plane out_state, out_dendrite, out_adaptation, out_emitted;
+  float* delta;                /* workspace float32[B*N], overwritten */
+} ns_event_args;
+
+/* Arguments of a plain CSR product J = W @ S (no neuron update). */
+typedef struct ns_spmm_args {
+  int64_t n_neurons;
+  int64_t batch;
+  ns_plane source;             /* S, [B,N] (data required) */
+  ns_csr matrix;
+  ns_row_plan plan;
+  ns_out_plane out;            /* J, [B,N]; must not overlap `source` */
+} ns_spmm_args;
+
+/* ABI version of the loaded library (NS_ABI_VERSION). */
+int ns_abi_version(void);
+
+/* Message of the last failed call on this host thread ("" if none). */
+const char* ns_last_error(void);
+
+/* Edge capacity of one row block used by the tick kernels for batch width
+ * `batch` (a plan passed to ns_dendritic_step/ns_csr_spmm must have been built
+ * with exactly this capacity). */
+int32_t ns_block_edges(int64_t batch);
+
+/* Host-side planner: splits rows [0,N) of a host copy of `rowptr` into blocks
+ * of consecutive rows whose edges fit `block_edges` (with the 4-edge alignment
+ * slack the kernels use) and at most 256 rows; a row too long for one block
+ * gets a block of its own.  Writes 2*(n_blocks+1) int32 into `bounds` when
+ * `capacity` (in int32 elements) suffices; always stores the block count in
+ * *n_blocks.  Validates rowptr (monotone, rowptr[0] == 0). */
+int ns_plan_row_blocks(const int32_t* rowptr_host, int64_t n_rows, int32_t block_edges,
+                       int32_t* bounds, int64_t capacity, int64_t* n_blocks);
+
+/* Fused matrix tick.  Replaces dendritic_step
+ * (reference: csrc/bindings.cpp:3-7,137-142; csrc/compartmental.cu:176-236),
+ * except that the caller supplies the output planes and the row plan. */
+int ns_dendritic_step(const ns_step_args* args, void* stream);
+
+/* PELS event tick: advance + emission threshold, then scatter of each
+ * emitter's out-edges into `current` with float32 atomics.  Replaces
+ * dendritic_event (reference: csrc/bindings.cpp:8-12,143;
+ * csrc/compartmental.cu:238-273), except that the caller supplies the four
+ * output planes and the delta workspace.  The emitted output follows the
+ * reference runtime (runtime.py:241-242): emitted + delta. */
+int ns_dendritic_event(const ns_event_args* args, void* stream);
+
+/* CSR product J = W @ S with the tick's decoding and summation order.
+ * Replaces MatrixRuntime._propagate (reference: runtime.py:78-79) for device
+ * float32 operands, e.g. the persistent current W @ emitted of runtime.py:124,220. */
+int ns_csr_spmm(const ns_spmm_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NEUROSIM_HIP_H */

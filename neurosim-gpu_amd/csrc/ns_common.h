@@ -1,0 +1,107 @@
+// Shared device-side helpers of the gfx950 dendritic tick library.
+//
+// Operand views, the exact weight decoders and the per-(neuron, column)
+// three-state update.  The update follows the operation order of the
+// reference's PyTorch path (compartmental.py:168-183, dynamics.py:305-314)
+// with floating-point contraction disabled, so given the same synaptic input
+// it rounds exactly like the reference's float32 CPU/GPU tensor ops.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "neurosim_hip.h"
+
+namespace ns {
+
+constexpr int kThreads = 256;   // 4 wavefronts of 64 lanes
+constexpr int kMaxRows = 256;   // rows per row block (one lane per row at most density)
+
+struct Plane {
+  const float* data;
+  int64_t sb, sn;
+  float scalar;
+  __device__ __forceinline__ float get(int64_t b, int64_t n) const {
+    return data ? data[b * sb + n * sn] : scalar;
+  }
+};
+
+struct OutPlane {
+  float* data;
+  int64_t sb, sn;
+  __device__ __forceinline__ void put(int64_t b, int64_t n, float x) const {
+    data[b * sb + n * sn] = x;
+  }
+};
+
+struct Vec {
+  const float* data;
+  int64_t stride;
+  __device__ __forceinline__ float get(int64_t n) const { return data[n * stride]; }
+};
+
+struct Params {
+  Vec v[6];  // alpha, gain, rho_d, rho_a, coupling, adaptation_strength
+};
+
+struct NextState {
+  float soma, dendrite, adaptation;
+};
+
+// torch.clamp(x, 0, 1) semantics, including NaN propagation.
+__device__ __forceinline__ float clamp01(float x) {
+  return x < 0.0f ? 0.0f : (x > 1.0f ? 1.0f : x);
+}
+
+// One three-state update.  Each statement is one tensor op of the reference:
+//   d' = rho_d*d + (1-rho_d)*tanh(j + v)
+//   u  = ((1-c)*j + c*d') - k*a
+//   s' = clamp(alpha*s + (1-alpha)*(gain*tanh(u + drive)), 0, 1)
+//   a' = rho_a*a + (1-rho_a)*s'
+__device__ __forceinline__ NextState advance_one(const Params& p, int64_t n, float j, float s,
+                                                 float d, float a, float drive, float ddrive) {
+#pragma clang fp contract(off)
+  const float alpha = p.v[0].get(n);
+  const float gain = p.v[1].get(n);
+  const float rho_d = p.v[2].get(n);
+  const float rho_a = p.v[3].get(n);
+  const float coupling = p.v[4].get(n);
+  const float strength = p.v[5].get(n);
+  NextState out;
+  const float dend_in = tanhf(j + ddrive);
+  out.dendrite = rho_d * d + (1.0f - rho_d) * dend_in;
+  const float mixed = (1.0f - coupling) * j + coupling * out.dendrite;
+  const float current = mixed - strength * a;
+  const float equilibrium = gain * tanhf(current + drive);
+  out.soma = clamp01(alpha * s + (1.0f - alpha) * equilibrium);
+  out.adaptation = rho_a * a + (1.0f - rho_a) * out.soma;
+  return out;
+}
+
+// OCP fp8 e4m3fn -> float32, exact.  The e4m3 bit fields shifted into an IEEE
+// binary16 (1-5-10) give the same significand with an exponent bias of 15
+// instead of 7, so the binary16 value times 2^8 is the e4m3 value; binary16
+// subnormals cover the e4m3 subnormals exactly.  Codes 0x7F/0xFF are NaN.
+__device__ __forceinline__ float e4m3_to_float(uint32_t code) {
+  const uint16_t bits = static_cast<uint16_t>(((code & 0x80u) << 8) | ((code & 0x7Fu) << 7));
+  const _Float16 h = __builtin_bit_cast(_Float16, bits);
+  const float value = static_cast<float>(h) * 256.0f;
+  return (code & 0x7Fu) == 0x7Fu ? __builtin_nanf("") : value;
+}
+
+// e2m1 magnitude of a 3-bit code: 0, 0.5, 1, 1.5, 2, 3, 4, 6.  Twice the
+// magnitude is a small integer; the nibble table below packs those integers.
+__device__ __forceinline__ float e2m1_magnitude(uint32_t code3) {
+  constexpr uint32_t kTwice = 0xC8643210u;
+  return 0.5f * static_cast<float>((kTwice >> (code3 * 4u)) & 15u);
+}
+
+// Decoded weight of an NVFP4 nibble given its block scale already decoded and
+// multiplied by the global scale (one float32 rounding, as in the reference's
+// levels[code & 7] * (block.float() * global); precision.py:109).
+__device__ __forceinline__ float nvfp4_weight(uint32_t nibble, float block_times_global) {
+  const float magnitude = e2m1_magnitude(nibble & 7u) * block_times_global;
+  return (nibble & 8u) ? -magnitude : magnitude;
+}
+
+}  // namespace ns

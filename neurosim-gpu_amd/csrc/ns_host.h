@@ -1,0 +1,62 @@
+// Host-side helpers shared by the C-ABI entry points: thread-local error
+// text, operand conversion and overlap checks.  All validation runs before
+// any launch, so a failing call leaves every buffer untouched.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+
+#include "ns_common.h"
+
+namespace ns {
+
+char* error_buffer();
+
+inline void clear_error() { error_buffer()[0] = '\0'; }
+
+__attribute__((format(printf, 1, 2))) inline int fail(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(error_buffer(), 512, fmt, ap);
+  va_end(ap);
+  return NS_ERR_INVALID;
+}
+
+inline int fail_launch(const char* what, hipError_t err) {
+  snprintf(error_buffer(), 512, "%s launch failed: %s", what, hipGetErrorString(err));
+  return NS_ERR_LAUNCH;
+}
+
+// Byte range [lo, hi) touched by a strided [B,N] float32 view (empty if absent).
+struct Extent {
+  uintptr_t lo, hi;
+};
+
+inline Extent extent_of(const void* data, int64_t sb, int64_t sn, int64_t batch, int64_t n) {
+  if (!data || batch <= 0 || n <= 0) return Extent{0, 0};
+  const uintptr_t lo = reinterpret_cast<uintptr_t>(data);
+  const int64_t last = (batch - 1) * (sb < 0 ? -sb : sb) + (n - 1) * (sn < 0 ? -sn : sn);
+  return Extent{lo, lo + static_cast<uintptr_t>((last + 1) * 4)};
+}
+
+inline Extent extent(const ns_plane& p, int64_t b, int64_t n) {
+  return extent_of(p.data, p.stride_b, p.stride_n, b, n);
+}
+inline Extent extent(const ns_out_plane& p, int64_t b, int64_t n) {
+  return extent_of(p.data, p.stride_b, p.stride_n, b, n);
+}
+
+inline bool overlaps(const Extent& x, const Extent& y) {
+  if (x.lo == x.hi || y.lo == y.hi) return false;
+  return x.lo < y.hi && y.lo < x.hi;
+}
+
+inline Plane plane(const ns_plane& p) { return Plane{p.data, p.stride_b, p.stride_n, p.scalar}; }
+inline OutPlane out_plane(const ns_out_plane& p) {
+  return OutPlane{p.data, p.stride_b, p.stride_n};
+}
+
+}  // namespace ns

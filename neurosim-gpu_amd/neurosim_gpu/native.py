@@ -1,0 +1,423 @@
+"""Loader and tensor-level shim for the gfx950 C-ABI library libneurosim_hip.so.
+
+``load_native_extension()`` returns an object with the reference extension's
+hot-path ops and signatures (csrc/bindings.cpp:3-12,137-143):
+
+    dendritic_step(state, dendrite, adaptation, params, rowptr, source, weight,
+                   input, input_scalar, dendritic_input, dendritic_scalar, width,
+                   block_scales=None, global_scale=None) -> [state', dendrite', adaptation']
+    dendritic_event(state, dendrite, adaptation, params, current, emitted, theta,
+                    out_rowptr, dst, weight_index, weight, input, input_scalar,
+                    dendritic_input, dendritic_scalar)
+                    -> [state', dendrite', adaptation', emitted']   (current updated in place)
+
+plus ``csr_spmm(source, rowptr, col, weight, block_scales=None, global_scale=None)``.
+Validation failures raise RuntimeError before anything is launched, like the
+reference's TORCH_CHECKs.  Outputs are fresh [B,N] tensors stored neuron-major
+(strides (1, B)): the kernels gather s[col, 0:B] as one contiguous run per
+edge.  ``width`` is accepted for compatibility (8, 16 or 32) and does not
+change the kernels, which size their lane groups per row block.
+
+The library is never built or replaced implicitly: a missing library raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+import weakref
+from collections import OrderedDict
+from functools import lru_cache
+from pathlib import Path
+
+import numpy as np
+import torch
+
+_LIB_NAME = "libneurosim_hip.so"
+ABI_VERSION = 1
+
+WEIGHT_F32, WEIGHT_F16, WEIGHT_E4M3, WEIGHT_NVFP4 = 0, 1, 2, 3
+_PLAN_CACHE = 64   # row plans kept per extension (one per live topology and batch width)
+
+_c_i64 = ctypes.c_int64
+_c_ptr = ctypes.c_void_p
+
+
+class _Plane(ctypes.Structure):
+    _fields_ = [("data", _c_ptr), ("stride_b", _c_i64), ("stride_n", _c_i64),
+                ("scalar", ctypes.c_float)]
+
+
+class _OutPlane(ctypes.Structure):
+    _fields_ = [("data", _c_ptr), ("stride_b", _c_i64), ("stride_n", _c_i64)]
+
+
+class _Vector(ctypes.Structure):
+    _fields_ = [("data", _c_ptr), ("stride", _c_i64)]
+
+
+class _Csr(ctypes.Structure):
+    _fields_ = [("n_rows", _c_i64), ("n_edges", _c_i64), ("rowptr", _c_ptr), ("col", _c_ptr),
+                ("weight", _c_ptr), ("format", ctypes.c_int32), ("block_scales", _c_ptr),
+                ("global_scale", _c_ptr)]
+
+
+class _RowPlan(ctypes.Structure):
+    _fields_ = [("bounds", _c_ptr), ("n_blocks", _c_i64), ("block_edges", ctypes.c_int32),
+                ("reserved", ctypes.c_int32)]
+
+
+class _StepArgs(ctypes.Structure):
+    _fields_ = [("n_neurons", _c_i64), ("batch", _c_i64),
+                ("state", _Plane), ("dendrite", _Plane), ("adaptation", _Plane),
+                ("drive", _Plane), ("dendritic_drive", _Plane),
+                ("params", _Vector * 6), ("matrix", _Csr), ("plan", _RowPlan),
+                ("out_state", _OutPlane), ("out_dendrite", _OutPlane),
+                ("out_adaptation", _OutPlane)]
+
+
+class _EventArgs(ctypes.Structure):
+    _fields_ = [("n_neurons", _c_i64), ("batch", _c_i64),
+                ("state", _Plane), ("dendrite", _Plane), ("adaptation", _Plane),
+                ("drive", _Plane), ("dendritic_drive", _Plane),
+                ("params", _Vector * 6),
+                ("current", _c_ptr), ("current_stride_b", _c_i64), ("current_stride_n", _c_i64),
+                ("emitted", _Plane), ("theta", _Vector),
+                ("out_rowptr", _c_ptr), ("dst", _c_ptr), ("weight_index", _c_ptr),
+                ("weight", _c_ptr), ("n_edges", _c_i64),
+                ("out_state", _OutPlane), ("out_dendrite", _OutPlane),
+                ("out_adaptation", _OutPlane), ("out_emitted", _OutPlane),
+                ("delta", _c_ptr)]
+
+
+class _SpmmArgs(ctypes.Structure):
+    _fields_ = [("n_neurons", _c_i64), ("batch", _c_i64), ("source", _Plane),
+                ("matrix", _Csr), ("plan", _RowPlan), ("out", _OutPlane)]
+
+
+def library_path() -> Path:
+    override = os.environ.get("NEUROSIM_HIP_LIB")
+    if override:
+        return Path(override)
+    return Path(__file__).resolve().parent / "_lib" / _LIB_NAME
+
+
+@lru_cache(maxsize=1)
+def load_library() -> ctypes.CDLL:
+    """Open the built library once; raise if it is missing or of another ABI."""
+    path = library_path()
+    if not path.exists():
+        raise RuntimeError(
+            f"native library {path} is missing; build it with "
+            "`python -c 'import __graft_entry__ as g; g.build()'` or "
+            "`make -C neurosim-gpu_amd/csrc`")
+    lib = ctypes.CDLL(str(path))
+    lib.ns_abi_version.restype = ctypes.c_int
+    lib.ns_last_error.restype = ctypes.c_char_p
+    lib.ns_block_edges.restype = ctypes.c_int32
+    lib.ns_block_edges.argtypes = [_c_i64]
+    lib.ns_plan_row_blocks.restype = ctypes.c_int
+    lib.ns_plan_row_blocks.argtypes = [_c_ptr, _c_i64, ctypes.c_int32, _c_ptr, _c_i64,
+                                       ctypes.POINTER(_c_i64)]
+    for name, kind in (("ns_dendritic_step", _StepArgs), ("ns_dendritic_event", _EventArgs),
+                       ("ns_csr_spmm", _SpmmArgs)):
+        fn = getattr(lib, name)
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.POINTER(kind), _c_ptr]
+    version = lib.ns_abi_version()
+    if version != ABI_VERSION:
+        raise RuntimeError(f"{path} has ABI version {version}, expected {ABI_VERSION}")
+    return lib
+
+
+def _raise_on(code: int, lib: ctypes.CDLL) -> None:
+    if code != 0:
+        message = lib.ns_last_error().decode("utf-8", "replace")
+        raise RuntimeError(message or f"native call failed with code {code}")
+
+
+def plan_row_blocks(rowptr: torch.Tensor, batch: int, device: torch.device) -> tuple[torch.Tensor, int, int]:
+    """Row blocks for the tick kernels, built on the host and placed on ``device``.
+
+    Returns (bounds int32 device tensor [2*(blocks+1)], blocks, block capacity).
+    Reads rowptr once on the host (a synchronisation), so call it at set-up.
+    """
+    lib = load_library()
+    capacity = int(lib.ns_block_edges(int(batch)))
+    host = np.ascontiguousarray(rowptr.detach().to("cpu", torch.int32).numpy())
+    n = host.size - 1
+    count = _c_i64(0)
+    _raise_on(lib.ns_plan_row_blocks(host.ctypes.data, n, capacity, None, 0,
+                                     ctypes.byref(count)), lib)
+    bounds = np.empty(2 * (count.value + 1), dtype=np.int32)
+    _raise_on(lib.ns_plan_row_blocks(host.ctypes.data, n, capacity, bounds.ctypes.data,
+                                     bounds.size, ctypes.byref(count)), lib)
+    return torch.from_numpy(bounds).to(device), int(count.value), capacity
+
+
+def _check_float(value: torch.Tensor, state: torch.Tensor, what: str) -> None:
+    if not isinstance(value, torch.Tensor):
+        raise RuntimeError(f"{what} must be a tensor")
+    if value.device != state.device:
+        raise RuntimeError("all tensors must be on the state's CUDA device")
+    if value.dtype != torch.float32:
+        raise RuntimeError("all values must be float32")
+
+
+def _plane(value: torch.Tensor, state: torch.Tensor, what: str) -> _Plane:
+    _check_float(value, state, what)
+    if value.shape != state.shape:
+        raise RuntimeError("state/current/drive shape mismatch")
+    return _Plane(value.data_ptr(), value.stride(0), value.stride(1), 0.0)
+
+
+def _drive(value: torch.Tensor | None, scalar: float, state: torch.Tensor) -> _Plane:
+    if value is None:
+        return _Plane(None, 0, 0, float(scalar))
+    return _plane(value, state, "drive")
+
+
+def _out(value: torch.Tensor) -> _OutPlane:
+    return _OutPlane(value.data_ptr(), value.stride(0), value.stride(1))
+
+
+def _index(value: torch.Tensor, state: torch.Tensor) -> None:
+    if (not isinstance(value, torch.Tensor) or value.device != state.device
+            or value.dtype != torch.int32 or not value.is_contiguous() or value.dim() != 1):
+        raise RuntimeError("indices must be contiguous int32 vectors on the state device")
+
+
+def _check_state(state: torch.Tensor) -> None:
+    if (not isinstance(state, torch.Tensor) or state.device.type != "cuda"
+            or state.dtype != torch.float32):
+        raise RuntimeError("state must be CUDA float32")
+    if state.dim() != 2 or state.size(1) <= 0:
+        raise RuntimeError("state must be [B,N], N > 0")
+
+
+def _params(values, state: torch.Tensor):
+    if not isinstance(values, (list, tuple)) or len(values) != 6:
+        raise RuntimeError("six neuron parameter vectors are required")
+    vectors = (_Vector * 6)()
+    for i, value in enumerate(values):
+        _check_float(value, state, "parameter")
+        if value.dim() != 1 or value.numel() != state.size(1):
+            raise RuntimeError("parameters must have one value per neuron")
+        vectors[i] = _Vector(value.data_ptr(), value.stride(0))
+    return vectors
+
+
+def new_planes(count: int, batch: int, n: int, like: torch.Tensor) -> list[torch.Tensor]:
+    """``count`` fresh [B,N] planes stored neuron-major in one allocation."""
+    storage = torch.empty((count, n, batch), dtype=torch.float32, device=like.device)
+    return [storage[i].T for i in range(count)]
+
+
+class NativeExtension:
+    """Drop-in for the reference's compiled extension (hot-path ops only)."""
+
+    def __init__(self) -> None:
+        self.lib = load_library()
+        # id(rowptr) -> (weakref, _version, {capacity: plan}); identity is re-checked on lookup.
+        self._plans: "OrderedDict[int, tuple]" = OrderedDict()
+        self._lock = threading.Lock()
+
+    # -- row plans ---------------------------------------------------------
+    def plan_tensors(self, rowptr: torch.Tensor, batch: int) -> tuple[torch.Tensor, int, int]:
+        """Cached (bounds, blocks, capacity) of ``rowptr`` for batch width ``batch``."""
+        capacity = int(self.lib.ns_block_edges(int(batch)))
+        key = id(rowptr)
+        with self._lock:
+            entry = self._plans.get(key)
+            if entry is None or entry[0]() is not rowptr or entry[1] != rowptr._version:
+                entry = (weakref.ref(rowptr), rowptr._version, {})
+                self._plans[key] = entry
+            self._plans.move_to_end(key)
+            while len(self._plans) > _PLAN_CACHE:
+                self._plans.popitem(last=False)
+            plan = entry[2].get(capacity)
+        if plan is None:
+            plan = plan_row_blocks(rowptr, batch, rowptr.device)
+            with self._lock:
+                entry[2][capacity] = plan
+        return plan
+
+    def plan_for(self, rowptr: torch.Tensor, batch: int) -> _RowPlan:
+        bounds, blocks, capacity = self.plan_tensors(rowptr, batch)
+        return _RowPlan(bounds.data_ptr(), blocks, capacity, 0)
+
+    # -- weights -----------------------------------------------------------
+    @staticmethod
+    def _csr(state, rowptr, source, weight, block_scales, global_scale) -> _Csr:
+        _index(rowptr, state)
+        _index(source, state)
+        n = state.size(1)
+        edges = source.numel()
+        if rowptr.numel() != n + 1:
+            raise RuntimeError("invalid CSR geometry")
+        if (not isinstance(weight, torch.Tensor) or weight.device != state.device
+                or not weight.is_contiguous() or weight.dim() != 1):
+            raise RuntimeError("CSR weights must be a contiguous vector on the state device")
+        scales_ptr = scale_ptr = None
+        if weight.dtype == torch.uint8:
+            if global_scale is None:
+                raise RuntimeError("quantized CSR weights require a global scale")
+            _check_float(global_scale, state, "global scale")
+            if global_scale.numel() != 1:
+                raise RuntimeError("global scale must have one value")
+            expected = (edges + 1) // 2 if block_scales is not None else edges
+            if weight.numel() != expected:
+                raise RuntimeError("invalid quantized CSR weight count")
+            if block_scales is not None:
+                if (block_scales.device != state.device or block_scales.dtype != torch.uint8
+                        or not block_scales.is_contiguous() or block_scales.dim() != 1
+                        or block_scales.numel() != (edges + 15) // 16):
+                    raise RuntimeError("invalid NVFP4 block scales")
+                fmt = WEIGHT_NVFP4
+                scales_ptr = block_scales.data_ptr()
+            else:
+                fmt = WEIGHT_E4M3
+            scale_ptr = global_scale.data_ptr()
+        else:
+            if (block_scales is not None or global_scale is not None or weight.numel() != edges
+                    or weight.dtype not in (torch.float32, torch.float16)):
+                raise RuntimeError("invalid floating-point CSR weights")
+            fmt = WEIGHT_F32 if weight.dtype == torch.float32 else WEIGHT_F16
+        return _Csr(n, edges, rowptr.data_ptr(), source.data_ptr(), weight.data_ptr(), fmt,
+                    scales_ptr, scale_ptr)
+
+    # -- ops ----------------------------------------------------------------
+    def dendritic_step(self, state, dendrite, adaptation, params, rowptr, source, weight,
+                       input, input_scalar, dendritic_input, dendritic_scalar, width,
+                       block_scales=None, global_scale=None):
+        _check_state(state)
+        args = _StepArgs()
+        args.state = _plane(state, state, "state")
+        args.dendrite = _plane(dendrite, state, "dendrite")
+        args.adaptation = _plane(adaptation, state, "adaptation")
+        args.params = _params(params, state)
+        args.drive = _drive(input, input_scalar, state)
+        args.dendritic_drive = _drive(dendritic_input, dendritic_scalar, state)
+        args.matrix = self._csr(state, rowptr, source, weight, block_scales, global_scale)
+        if width not in (8, 16, 32):
+            raise RuntimeError("width must be 8, 16 or 32")
+        batch, n = state.shape
+        args.n_neurons, args.batch = n, batch
+        args.plan = self.plan_for(rowptr, batch)
+        outs = new_planes(3, batch, n, state)
+        args.out_state, args.out_dendrite, args.out_adaptation = (_out(o) for o in outs)
+        stream = torch.cuda.current_stream(state.device).cuda_stream
+        _raise_on(self.lib.ns_dendritic_step(ctypes.byref(args), stream), self.lib)
+        return outs
+
+    def dendritic_event(self, state, dendrite, adaptation, params, current, emitted, theta,
+                        rowptr, dst, weight_index, weight, input, input_scalar,
+                        dendritic_input, dendritic_scalar, delta=None):
+        _check_state(state)
+        args = _EventArgs()
+        args.state = _plane(state, state, "state")
+        args.dendrite = _plane(dendrite, state, "dendrite")
+        args.adaptation = _plane(adaptation, state, "adaptation")
+        args.params = _params(params, state)
+        args.drive = _drive(input, input_scalar, state)
+        args.dendritic_drive = _drive(dendritic_input, dendritic_scalar, state)
+        _check_float(current, state, "current")
+        if current.shape != state.shape:
+            raise RuntimeError("state/current/drive shape mismatch")
+        args.current = current.data_ptr()
+        args.current_stride_b, args.current_stride_n = current.stride(0), current.stride(1)
+        args.emitted = _plane(emitted, state, "emitted")
+        _check_float(theta, state, "theta")
+        if theta.dim() != 1 or theta.numel() != state.size(1):
+            raise RuntimeError("theta must have N values")
+        args.theta = _Vector(theta.data_ptr(), theta.stride(0))
+        for index in (rowptr, dst, weight_index):
+            _index(index, state)
+        _check_float(weight, state, "weight")
+        if (rowptr.numel() != state.size(1) + 1 or dst.numel() != weight.numel()
+                or dst.numel() != weight_index.numel() or not weight.is_contiguous()
+                or weight.dim() != 1):
+            raise RuntimeError("invalid event topology geometry")
+        args.out_rowptr, args.dst = rowptr.data_ptr(), dst.data_ptr()
+        args.weight_index, args.weight = weight_index.data_ptr(), weight.data_ptr()
+        args.n_edges = weight.numel()
+        batch, n = state.shape
+        args.n_neurons, args.batch = n, batch
+        outs = new_planes(4, batch, n, state)
+        (args.out_state, args.out_dendrite, args.out_adaptation,
+         args.out_emitted) = (_out(o) for o in outs)
+        if delta is None:
+            delta = torch.empty(batch * n, dtype=torch.float32, device=state.device)
+        elif delta.numel() < batch * n or delta.dtype != torch.float32 or not delta.is_contiguous():
+            raise RuntimeError("delta workspace must hold B*N float32")
+        args.delta = delta.data_ptr()
+        stream = torch.cuda.current_stream(state.device).cuda_stream
+        _raise_on(self.lib.ns_dendritic_event(ctypes.byref(args), stream), self.lib)
+        return outs
+
+    def csr_spmm(self, source, rowptr, col, weight, block_scales=None, global_scale=None):
+        _check_state(source)
+        args = _SpmmArgs()
+        args.source = _plane(source, source, "source")
+        args.matrix = self._csr(source, rowptr, col, weight, block_scales, global_scale)
+        batch, n = source.shape
+        args.n_neurons, args.batch = n, batch
+        args.plan = self.plan_for(rowptr, batch)
+        (out,) = new_planes(1, batch, n, source)
+        args.out = _out(out)
+        stream = torch.cuda.current_stream(source.device).cuda_stream
+        _raise_on(self.lib.ns_csr_spmm(ctypes.byref(args), stream), self.lib)
+        return out
+
+
+class TickLauncher:
+    """A prepared fused tick: fixed weights, plan, parameters and drives.
+
+    Only the input/output state planes change between launches, so a
+    multi-tick loop does no validation or allocation per tick and can be
+    captured into one HIP graph.  Keeps every tensor it points at alive.
+    """
+
+    def __init__(self, extension: "NativeExtension", state_like: torch.Tensor, params, rowptr,
+                 col, weight, drive, dendritic_drive, block_scales=None, global_scale=None):
+        _check_state(state_like)
+        self.lib = extension.lib
+        args = _StepArgs()
+        args.params = _params(params, state_like)
+        args.matrix = extension._csr(state_like, rowptr, col, weight, block_scales, global_scale)
+        drive_t = drive if isinstance(drive, torch.Tensor) else None
+        ddrive_t = dendritic_drive if isinstance(dendritic_drive, torch.Tensor) else None
+        if drive_t is not None:
+            drive_t = drive_t.expand_as(state_like)
+        if ddrive_t is not None:
+            ddrive_t = ddrive_t.expand_as(state_like)
+        args.drive = _drive(drive_t, 0.0 if drive_t is not None else float(drive), state_like)
+        args.dendritic_drive = _drive(ddrive_t, 0.0 if ddrive_t is not None
+                                      else float(dendritic_drive), state_like)
+        batch, n = state_like.shape
+        args.n_neurons, args.batch = n, batch
+        bounds, blocks, capacity = extension.plan_tensors(rowptr, batch)
+        args.plan = _RowPlan(bounds.data_ptr(), blocks, capacity, 0)
+        self.args = args
+        self.batch, self.n = batch, n
+        self._keep = (list(params), rowptr, col, weight, drive_t, ddrive_t, block_scales,
+                      global_scale, bounds)
+
+    def __call__(self, source: tuple, target: tuple, stream: int | None = None) -> None:
+        """One tick from planes (s, d, a) into planes (s', d', a') (all [B,N] views)."""
+        args = self.args
+        args.state = _Plane(source[0].data_ptr(), source[0].stride(0), source[0].stride(1), 0.0)
+        args.dendrite = _Plane(source[1].data_ptr(), source[1].stride(0), source[1].stride(1), 0.0)
+        args.adaptation = _Plane(source[2].data_ptr(), source[2].stride(0), source[2].stride(1),
+                                 0.0)
+        args.out_state, args.out_dendrite, args.out_adaptation = (_out(t) for t in target)
+        if stream is None:
+            stream = torch.cuda.current_stream(source[0].device).cuda_stream
+        _raise_on(self.lib.ns_dendritic_step(ctypes.byref(args), stream), self.lib)
+
+
+@lru_cache(maxsize=1)
+def load_native_extension(verbose: bool = False) -> NativeExtension:
+    """The process-wide native extension (library loaded once, never rebuilt)."""
+    return NativeExtension()

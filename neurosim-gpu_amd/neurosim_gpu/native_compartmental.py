@@ -1,0 +1,219 @@
+"""Native (gfx950 HIP) dendritic runtimes with explicit reference fallbacks.
+
+API of the reference's native_compartmental module
+(src/neurosim_gpu/native_compartmental.py:13-177):
+
+* NativeDendriticMatrixRuntime -- one fused kernel per tick: CSR gather-product
+  over the B columns plus the three-state update, with fp32 / fp16 / fp8 e4m3 /
+  nvfp4 weights decoded in-kernel and accumulated in float32.
+* NativeDendriticPELSRuntime -- two kernels per tick: advance + emission
+  threshold, then the emitters' out-edge scatter into the persistent current.
+
+Requests that need autograd (any tensor with requires_grad under grad mode)
+or PELS statistics run the PyTorch reference step instead and say so in
+``last_backend`` ("reference-autograd" / "reference-stats"); reduced weight
+storage is inference-only.  The native library must be present: a missing
+library raises at construction, nothing falls back silently.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .compartmental import DendriticDynamics, DendriticMatrixRuntime, DendriticPELSRuntime
+from .native import NativeExtension, load_native_extension
+from .topology import SparseTopology
+
+
+def _require_gpu_float32(initial_state: torch.Tensor) -> None:
+    if initial_state.device.type != "cuda" or initial_state.dtype != torch.float32:
+        raise ValueError("native compartment runtime requires CUDA float32")
+
+
+class _NativeCompartments:
+    def _init_native(self, initial_state: torch.Tensor, extension) -> None:
+        _require_gpu_float32(initial_state)
+        self.extension = extension if extension is not None else load_native_extension()
+        self.last_backend = "unstepped"
+
+    def _parameters(self) -> list[torch.Tensor]:
+        model = self.compartment_dynamics
+        return [model.soma.alpha, model.soma.gain, model.dendrite_decay,
+                model.adaptation_decay, model.coupling, model.adaptation_strength]
+
+    def _needs_autograd(self, drive, dendritic_drive) -> bool:
+        if not torch.is_grad_enabled():
+            return False
+        values = [self.state, self.dendritic_state, self.adaptation_state,
+                  self.topology.weight, self.topology.in_weight, *self._parameters(),
+                  drive, dendritic_drive]
+        if hasattr(self, "persistent_current"):
+            values += [self.persistent_current, self.emitted_state]
+        return any(isinstance(v, torch.Tensor) and v.requires_grad for v in values)
+
+    def _drive(self, value) -> tuple[torch.Tensor | None, float]:
+        """(broadcast [B,N] view, 0.0) for tensors, (None, value) for numbers."""
+        if not isinstance(value, torch.Tensor):
+            return None, float(value)
+        if value.device != self.state.device or value.dtype != self.state.dtype:
+            raise ValueError("drive must match state device and dtype")
+        try:
+            return value.expand_as(self.state), 0.0
+        except RuntimeError as error:
+            raise ValueError("drive must broadcast to [batch, n_neurons]") from error
+
+    def _native_spmm(self, source: torch.Tensor) -> torch.Tensor:
+        """W @ source on the device (float32 weights), neuron-major output."""
+        topology = self.topology
+        return self.extension.csr_spmm(source.detach(), topology.in_rowptr, topology.in_col,
+                                       topology.in_weight.detach())
+
+
+class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
+    """One HIP launch per tick for CSR propagation plus all three neuron states.
+
+    States, parameters, drives and accumulation are float32 on the GPU.
+    ``weight_dtype=torch.float16`` or ``weight_format='fp8'|'nvfp4'`` stores
+    the CSR weights compressed (re-encoded whenever topology.weight_version
+    changes) and decodes them in-kernel before each float32 multiply.
+    Returned states stay valid after later ticks (every tick allocates fresh
+    outputs).  ``threads_per_row`` is accepted for compatibility.
+    """
+
+    def __init__(self, topology: SparseTopology, dynamics: DendriticDynamics,
+                 initial_state: torch.Tensor, *, threads_per_row: int | None = None,
+                 extension=None, weight_dtype: torch.dtype = torch.float32,
+                 weight_format: str | None = None) -> None:
+        if threads_per_row not in (None, 8, 16, 32):
+            raise ValueError("threads_per_row must be 8, 16, 32 or None")
+        _require_gpu_float32(initial_state)
+        if weight_dtype not in (torch.float32, torch.float16):
+            raise ValueError("weight_dtype must be torch.float32 or torch.float16")
+        if weight_format not in (None, "fp8", "nvfp4"):
+            raise ValueError("weight_format must be None, 'fp8' or 'nvfp4'")
+        if weight_format is not None and weight_dtype != torch.float32:
+            raise ValueError("weight_format and non-default weight_dtype conflict")
+        super().__init__(topology, dynamics, initial_state)
+        degree = topology.n_edges / max(topology.n_neurons, 1)
+        self.threads_per_row = threads_per_row or (8 if degree <= 16 else 16 if degree <= 48 else 32)
+        self._init_native(initial_state, extension)
+        self.weight_dtype = weight_dtype
+        self.weight_format = weight_format
+        self._invalidate_precision_cache()
+
+    def _invalidate_precision_cache(self) -> None:
+        self._packed_weight = None
+        self._packed_weight_version = -1
+
+    @property
+    def checkpoint_precision(self) -> str:
+        if self.weight_format is not None:
+            return self.weight_format
+        return "fp16" if self.weight_dtype == torch.float16 else "fp32"
+
+    @property
+    def precision_execution(self) -> str:
+        return f"cuda-fused-{self.checkpoint_precision}-weights-fp32-fma"
+
+    @property
+    def weight_storage_bytes(self) -> int:
+        """Logical inference payload in bytes, excluding the original topology."""
+        edges = self.topology.n_edges
+        if self.weight_format == "nvfp4":
+            return (edges + 1) // 2 + (edges + 15) // 16 + 4
+        if self.weight_format == "fp8":
+            return edges + 4
+        return edges * (2 if self.weight_dtype == torch.float16 else 4)
+
+    def _weights(self) -> tuple[torch.Tensor, tuple, str]:
+        """(weight payload, scale arguments, backend label) for this tick."""
+        weight = self.topology.in_weight
+        if self.weight_format is None and self.weight_dtype == torch.float32:
+            return weight, (), "native"
+        if self._packed_weight_version != self.topology.weight_version:
+            with torch.no_grad():
+                if self.weight_format is None:
+                    self._packed_weight = (weight.detach().to(torch.float16),)
+                else:
+                    from .precision import encode_sparse_weights
+                    self._packed_weight = encode_sparse_weights(weight.detach(), self.weight_format)
+            self._packed_weight_version = self.topology.weight_version
+        payload, *scales = self._packed_weight
+        return payload, tuple(scales), f"native-{self.weight_format or 'fp16'}-weight"
+
+    def step(self, drive: torch.Tensor | float = 0.0, *,
+             dendritic_drive: torch.Tensor | float = 0.0) -> torch.Tensor:
+        if self._needs_autograd(drive, dendritic_drive):
+            if self.weight_format is not None or self.weight_dtype == torch.float16:
+                raise RuntimeError("native reduced-precision weight storage is inference-only")
+            self.last_backend = "reference-autograd"
+            return super().step(drive, dendritic_drive=dendritic_drive)
+        u, us = self._drive(drive)
+        v, vs = self._drive(dendritic_drive)
+        weight, scales, backend = self._weights()
+        self.state, self.dendritic_state, self.adaptation_state = self.extension.dendritic_step(
+            self.state, self.dendritic_state, self.adaptation_state, self._parameters(),
+            self.topology.in_rowptr, self.topology.in_col, weight,
+            u, us, v, vs, self.threads_per_row, *scales)
+        self.last_backend = backend
+        return self.state
+
+
+class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
+    """Two HIP launches per tick: advance/emission, then out-edge scatter.
+
+    The scan covers all B*N (neuron, column) pairs on the device; only pairs
+    with a nonzero delta walk their out-edges.  Float32 atomics make the
+    scatter's summation order, and therefore the last bits of the current,
+    run-dependent.  Statistics and autograd requests use the reference step.
+    """
+
+    @property
+    def precision_execution(self) -> str:
+        return "cuda-fused-pels-fp32"
+
+    def __init__(self, topology: SparseTopology, dynamics: DendriticDynamics,
+                 initial_state: torch.Tensor, *, theta: float | torch.Tensor,
+                 extension=None) -> None:
+        _require_gpu_float32(initial_state)
+        self.extension = extension if extension is not None else load_native_extension()
+        super().__init__(topology, dynamics, initial_state, theta=theta, propagation="event")
+        self._init_native(initial_state, self.extension)
+        batch, n = initial_state.shape
+        self._delta = torch.empty(batch * n, dtype=torch.float32, device=initial_state.device)
+
+    def _initial_current(self) -> torch.Tensor:
+        if torch.is_grad_enabled() and (self.emitted_state.requires_grad
+                                        or self.topology.in_weight.requires_grad):
+            return super()._initial_current()
+        return self._native_spmm(self.emitted_state)
+
+    def _refresh_current(self) -> None:
+        if self._weight_version != self.topology.weight_version:
+            if torch.is_grad_enabled() and (self.emitted_state.requires_grad
+                                            or self.topology.in_weight.requires_grad):
+                self.persistent_current = self._propagate(self.emitted_state).contiguous()
+            else:
+                self.persistent_current = self._native_spmm(self.emitted_state)
+            self._weight_version = self.topology.weight_version
+
+    def step(self, drive: torch.Tensor | float = 0.0, *,
+             dendritic_drive: torch.Tensor | float = 0.0, collect_stats: bool = False):
+        if collect_stats or self._needs_autograd(drive, dendritic_drive):
+            self.last_backend = "reference-stats" if collect_stats else "reference-autograd"
+            return super().step(drive, dendritic_drive=dendritic_drive,
+                                collect_stats=collect_stats)
+        u, us = self._drive(drive)
+        v, vs = self._drive(dendritic_drive)
+        self._refresh_current()
+        extra = {"delta": self._delta} if isinstance(self.extension, NativeExtension) else {}
+        # The current is updated in place only after the advance kernel has read it.
+        self.state, self.dendritic_state, self.adaptation_state, self.emitted_state = (
+            self.extension.dendritic_event(
+                self.state, self.dendritic_state, self.adaptation_state, self._parameters(),
+                self.persistent_current, self.emitted_state, self.theta,
+                self.topology.out_rowptr, self.topology.dst, self.topology.out_weight_index,
+                self.topology.in_weight, u, us, v, vs, **extra))
+        self._tick += 1
+        self.last_backend = "native"
+        return self.state

@@ -1,0 +1,59 @@
+"""Extract the reference-held result data used as golden vectors.
+
+Reads two result files of the reference checkout (data, not code) and writes
+compact fixtures next to this script:
+
+* probe_cpu.json  <- results/compartmental_probe_cpu.json: FP64, N=32, M=0,
+  B=2, 400 ticks, five variants, per-tick population means of soma /
+  dendrite / adaptation, plus the summary metrics.
+* brainwaves.npz + brainwaves_meta.json <- results/compartmental_brainwaves.json:
+  N=1024 graph from random_topology(1024, 20480, seed=23) (20295 edges), the
+  shared state means after 512 warm-up ticks, the post-warm-up group inputs,
+  and the 4096-tick population-mean soma traces of both rows (row 0 keeps
+  its inputs, row 1 has both drives withdrawn).
+
+Usage: python tests/golden/make_fixtures.py [/root/reference]
+"""
+
+from __future__ import annotations
+
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+
+
+def main(reference: Path) -> None:
+    probe = json.loads((reference / "results/compartmental_probe_cpu.json").read_text())
+    compact = {
+        "config": probe["config"],
+        "metrics": probe["metrics"],
+        "traces": {name: {key: [row[key] for row in rows]
+                          for key in ("drive", "dendritic_drive", "soma", "dendrite", "adaptation")}
+                   for name, rows in probe["traces"].items()},
+    }
+    (HERE / "probe_cpu.json").write_text(json.dumps(compact) + "\n")
+
+    waves = json.loads((reference / "results/compartmental_brainwaves.json").read_text())
+    sim = waves["simulation"]
+    meta = {key: sim[key] for key in ("neurons", "actual_edges", "candidate_edges", "graph_seed",
+                                      "input_seed", "warmup_ticks", "ticks_per_condition",
+                                      "groups", "parameters", "shared_initial_state_means",
+                                      "topology_sha256")}
+    meta["mean_last_512_ticks"] = {k: waves["measurements"][k]["mean_last_512_ticks"]
+                                   for k in ("driven", "zero_input")}
+    (HERE / "brainwaves_meta.json").write_text(json.dumps(meta, indent=1) + "\n")
+    inputs = waves["continued_input_group_traces"]
+    np.savez_compressed(
+        HERE / "brainwaves.npz",
+        somatic=np.asarray(inputs["somatic"], dtype=np.float32),
+        dendritic=np.asarray(inputs["dendritic"], dtype=np.float32),
+        driven_mean=np.asarray(waves["measurements"]["driven"]["population_mean_trace"]),
+        zero_mean=np.asarray(waves["measurements"]["zero_input"]["population_mean_trace"]))
+
+
+if __name__ == "__main__":
+    main(Path(sys.argv[1] if len(sys.argv) > 1 else "/root/reference"))

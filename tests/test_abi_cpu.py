@@ -1,0 +1,144 @@
+"""The C-ABI library loads on a host without a GPU, exports every declared
+symbol, plans rows correctly and rejects invalid arguments before launching.
+No kernel runs here: every call either is host-only or fails validation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from neurosim_gpu import native
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "neurosim_hip.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return native.load_library()
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    return re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(ns_\w+)\s*\(", text, flags=re.M)
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared_functions()
+    assert set(names) == {"ns_abi_version", "ns_last_error", "ns_block_edges",
+                          "ns_plan_row_blocks", "ns_dendritic_step", "ns_dendritic_event",
+                          "ns_csr_spmm"}
+    for name in names:
+        assert hasattr(lib, name), name
+    assert lib.ns_abi_version() == native.ABI_VERSION
+
+
+def test_block_capacity_per_batch(lib):
+    caps = {b: lib.ns_block_edges(b) for b in (0, 1, 2, 3, 4, 8, 16, 64)}
+    assert caps[1] == caps[0] == 2048 and caps[2] == 2048
+    assert caps[3] == caps[4] == caps[8] == caps[16] == caps[64] == 1024
+
+
+def plan(lib, rowptr, capacity):
+    rowptr = np.ascontiguousarray(rowptr, dtype=np.int32)
+    count = ctypes.c_int64()
+    rc = lib.ns_plan_row_blocks(rowptr.ctypes.data, rowptr.size - 1, capacity, None, 0,
+                                ctypes.byref(count))
+    assert rc == 0, lib.ns_last_error()
+    bounds = np.empty(2 * (count.value + 1), np.int32)
+    rc = lib.ns_plan_row_blocks(rowptr.ctypes.data, rowptr.size - 1, capacity,
+                                bounds.ctypes.data, bounds.size, ctypes.byref(count))
+    assert rc == 0, lib.ns_last_error()
+    return bounds.reshape(-1, 2)
+
+
+@pytest.mark.parametrize("degrees", [
+    [20] * 1000, [0] * 700, [150] * 300, [5000, 3, 0, 2100, 1] + [7] * 50,
+    list(np.random.default_rng(1).poisson(30, 2000)), [2045, 2046, 2047, 2048, 2049, 1]])
+def test_planner_blocks_cover_rows_and_fit(lib, degrees):
+    capacity = 2048
+    rowptr = np.concatenate([[0], np.cumsum(degrees)]).astype(np.int32)
+    bounds = plan(lib, rowptr, capacity)
+    rows = bounds[:, 0]
+    assert rows[0] == 0 and rows[-1] == len(degrees)
+    assert np.all(np.diff(rows) >= 1)
+    assert np.array_equal(bounds[:, 1], rowptr[rows])
+    for r0, r1 in zip(rows[:-1], rows[1:]):
+        span = rowptr[r1] - (rowptr[r0] & ~3)
+        assert (r1 - r0 <= 256 and span <= capacity) or r1 - r0 == 1
+        if r1 < len(degrees) and r1 - r0 < 256 and span <= capacity:
+            # greedy: the next row would not have fit
+            assert rowptr[r1 + 1] - (rowptr[r0] & ~3) > capacity
+
+
+def test_planner_rejects_bad_rowptr(lib):
+    count = ctypes.c_int64()
+    bad = np.array([0, 5, 3], np.int32)
+    assert lib.ns_plan_row_blocks(bad.ctypes.data, 2, 2048, None, 0, ctypes.byref(count)) != 0
+    assert b"non-decreasing" in lib.ns_last_error()
+    bad = np.array([1, 5], np.int32)
+    assert lib.ns_plan_row_blocks(bad.ctypes.data, 1, 2048, None, 0, ctypes.byref(count)) != 0
+    small = np.array([0, 5, 9], np.int32)
+    bounds = np.empty(2, np.int32)
+    assert lib.ns_plan_row_blocks(small.ctypes.data, 2, 2048, bounds.ctypes.data, 2,
+                                  ctypes.byref(count)) != 0
+    assert b"capacity" in lib.ns_last_error()
+
+
+def fake_step_args(n=8, batch=2):
+    """Host-memory pointers: valid for validation only (never launched)."""
+    keep = [np.zeros((batch, n), np.float32) for _ in range(6)]
+    params = [np.ones(n, np.float32) for _ in range(6)]
+    rowptr = np.zeros(n + 1, np.int32)
+    args = native._StepArgs()
+    args.n_neurons, args.batch = n, batch
+    planes = [native._Plane(k.ctypes.data, n, 1, 0.0) for k in keep[:3]]
+    args.state, args.dendrite, args.adaptation = planes
+    args.drive = native._Plane(None, 0, 0, 0.2)
+    args.dendritic_drive = native._Plane(None, 0, 0, 0.1)
+    for i, p in enumerate(params):
+        args.params[i] = native._Vector(p.ctypes.data, 1)
+    args.matrix = native._Csr(n, 0, rowptr.ctypes.data, None, None, native.WEIGHT_F32, None, None)
+    bounds = np.array([0, 0, n, 0], np.int32)
+    args.plan = native._RowPlan(bounds.ctypes.data, 1, 2048, 0)
+    outs = [native._OutPlane(k.ctypes.data, n, 1) for k in keep[3:]]
+    args.out_state, args.out_dendrite, args.out_adaptation = outs
+    return args, (keep, params, rowptr, bounds)
+
+
+def call(lib, args):
+    rc = lib.ns_dendritic_step(ctypes.byref(args), None)
+    return rc, lib.ns_last_error().decode()
+
+
+def test_step_validation_messages(lib):
+    args, keep = fake_step_args()
+    args.params[3] = native._Vector(None, 1)
+    assert call(lib, args) == (1, "six neuron parameter vectors are required")
+    args, keep = fake_step_args()
+    args.n_neurons = 0
+    assert "N > 0" in call(lib, args)[1]
+    args, keep = fake_step_args()
+    args.plan.block_edges = 1024
+    assert "capacity" in call(lib, args)[1]
+    args, keep = fake_step_args()
+    args.out_dendrite = native._OutPlane(args.state.data, 8, 1)
+    assert "overlap" in call(lib, args)[1]
+    args, keep = fake_step_args()
+    args.matrix.format = 9
+    assert "format" in call(lib, args)[1]
+    args, keep = fake_step_args()
+    args.matrix.format = native.WEIGHT_E4M3
+    assert "global scale" in call(lib, args)[1]
+    args, keep = fake_step_args()
+    args.matrix.n_rows = 7
+    assert "row count" in call(lib, args)[1]
+
+
+def test_empty_batch_is_a_no_op(lib):
+    args, keep = fake_step_args(batch=0)
+    assert call(lib, args) == (0, "")

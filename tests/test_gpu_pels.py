@@ -1,0 +1,117 @@
+"""Native PELS event tick vs the CPU oracle (MI355X).
+
+Tolerances: theta=0 within 1e-5 of the oracle (which is then the matrix
+tick); theta>0 within 1e-3 of the oracle PELS at the same theta (float32
+atomics reorder the current's sums, which can move an emission by a tick near
+the threshold; the reference accepts 2e-3 for the same comparison).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from cases import make_case, max_err
+from oracle import runtime as ort
+from neurosim_gpu import NativeDendriticPELSRuntime
+
+pytestmark = pytest.mark.gpu
+FIELDS = ("state", "dendritic_state", "adaptation_state")
+
+
+def state_error(native, oracle) -> float:
+    return max(max_err(getattr(native, f), getattr(oracle, f)) for f in FIELDS)
+
+
+def test_theta_zero_long_rollout_matches_matrix(gpu):
+    """Reference test_native_compartmental.py:99-110 (N=1024, B=2, 16000 edges, 500 ticks)."""
+    case = make_case(1024, 16000, 83, gpu, kind="reference")
+    state = torch.full((2, 1024), 0.2)
+    native = NativeDendriticPELSRuntime(case.topology, case.model, state.to(gpu), theta=0)
+    matrix = ort.MatrixOracle(case.graph, case.params, state)
+    for t in range(500):
+        value = 0.2 if t % 70 < 35 else 0.05
+        native.step(value, dendritic_drive=0.1)
+        matrix.step(value, 0.1)
+    assert state_error(native, matrix) <= 8e-6
+    current = ort.propagate(ort.csr_matrix(case.graph), native.emitted_state.cpu())
+    assert max_err(native.persistent_current, current) <= 1e-5
+
+
+def test_nonzero_theta_emission_and_weight_mutation(gpu):
+    """Reference test_native_compartmental.py:142-164 (theta .02, weights x0.7 at tick 25)."""
+    from oracle import topology as otop
+
+    case = make_case(97, 600, 83, gpu, kind="reference")
+    state = torch.full((3, 97), 0.2)
+    native = NativeDendriticPELSRuntime(case.topology, case.model, state.to(gpu), theta=0.02)
+    oracle = ort.PelsOracle(case.graph, case.params, state, theta=0.02)
+    for t in range(50):
+        if t == 25:
+            case.topology.apply_source_weights_(case.topology.weight * 0.7)
+            new_graph = otop.with_weights(case.graph, case.topology.weight.cpu().numpy())
+            oracle.matrix = ort.csr_matrix(new_graph)
+            oracle.persistent_current = ort.propagate(oracle.matrix, oracle.emitted_state)
+            case = case.__class__(new_graph, case.topology, case.model, case.params)
+        native.step(0.3, dendritic_drive=0.1)
+        oracle.step(0.3, 0.1)
+        assert float((native.state - native.emitted_state).abs().max()) < 0.020001
+        exact = ort.propagate(ort.csr_matrix(case.graph), native.emitted_state.cpu())
+        assert max_err(native.persistent_current, exact) <= 1e-5
+    assert state_error(native, oracle) <= 1e-3
+    _, stats = native.step(0.3, collect_stats=True)
+    oracle.step(0.3)
+    assert native.last_backend == "reference-stats" and stats.active_edges >= 0
+    native.step(0.3)
+    oracle.step(0.3)
+    assert native.last_backend == "native"
+    assert state_error(native, oracle) <= 1e-3
+
+
+def test_idle_updates_traces_and_retains_returned_state(gpu):
+    """Reference test_native_compartmental.py:166-178 (theta 2: nothing emits)."""
+    case = make_case(97, 600, 83, gpu, kind="reference")
+    native = NativeDendriticPELSRuntime(case.topology, case.model,
+                                        torch.full((3, 97), 0.2, device=gpu), theta=2)
+    previous = native.step(0.5)
+    saved = previous.clone()
+    current = native.persistent_current.clone()
+    first_adaptation = native.adaptation_state.clone()
+    for _ in range(10):
+        native.step(0.5)
+    assert torch.equal(previous, saved)
+    assert torch.equal(native.persistent_current, current)
+    assert not torch.equal(first_adaptation, native.adaptation_state)
+
+
+@pytest.mark.parametrize("theta", [0.0, 0.02])
+def test_cfg4_event_path_warmup_then_withdrawn(gpu, theta):
+    """N=50000, M~1M, B=1: 512 ticks drive .2/.1, then 4096 ticks with inputs withdrawn."""
+    print(f"case cfg4 N=50000 M=1000000 theta={theta}", flush=True)
+    case = make_case(50_000, 1_000_000, 0, gpu)
+    native = NativeDendriticPELSRuntime(case.topology, case.model,
+                                        torch.zeros(1, 50_000, device=gpu), theta=theta)
+    oracle = ort.PelsOracle(case.graph, case.params, torch.zeros(1, 50_000), theta=theta)
+    bar = 1e-5 if theta == 0 else 1e-3
+    worst = worst_current = 0.0
+    mismatches = checked = 0
+    for tick in range(512 + 4096):
+        drive, ddrive = (0.2, 0.1) if tick < 512 else (0.0, 0.0)
+        before_native, before_oracle = native.emitted_state, oracle.emitted_state
+        native.step(drive, dendritic_drive=ddrive)
+        oracle.step(drive, ddrive)
+        if tick % 64 == 63 or tick == 511:
+            worst = max(worst, state_error(native, oracle))
+            worst_current = max(worst_current,
+                                max_err(native.persistent_current, oracle.persistent_current))
+            emitted_native = (native.emitted_state != before_native).cpu()
+            emitted_oracle = oracle.emitted_state != before_oracle
+            mismatches += int((emitted_native != emitted_oracle).sum())
+            checked += emitted_oracle.numel()
+    print(f"cfg4 theta={theta}: state {worst:.3e} current {worst_current:.3e} "
+          f"emit-mask mismatches {mismatches}/{checked}")
+    assert worst <= bar
+    assert worst_current <= bar
+    assert max_err(native.emitted_state, oracle.emitted_state) <= bar
+    assert mismatches <= 1e-3 * checked

@@ -1,0 +1,102 @@
+"""Pins of the oracle graph builder, and product == oracle on the same draws.
+
+Reference-held pin: random_topology(1024, 20480, seed=23) on the CPU has
+20295 unique edges (results/compartmental_brainwaves.json, simulation.
+actual_edges).  The reference's topology_sha256 of that graph also covers the
+weight bits, which torch's CPU normal sampler produces through the host
+platform's libm/SIMD path; it is therefore not reproducible off the
+reference's machine and is not asserted here.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle import topology as otop
+from neurosim_gpu import SparseTopology, random_topology
+
+
+def brute_force(n, src, dst, weight):
+    """Dictionary coalescer: the definition, not an algorithm."""
+    sums = {}
+    for s, d, w in zip(src.tolist(), dst.tolist(), weight.tolist()):
+        sums[(s, d)] = np.float32(sums.get((s, d), np.float32(0.0)) + np.float32(w))
+    return sums
+
+
+def test_brainwaves_graph_edge_count():
+    graph = otop.random_graph(1024, 20480, seed=23)
+    assert graph.n_edges == 20295
+
+
+def test_coalescing_matches_brute_force_and_invariants():
+    for n, m, seed in ((12, 48, 17), (97, 600, 83), (5, 200, 3), (1, 0, 0), (40, 1, 9)):
+        src, dst, weight = otop.random_edges(n, m, seed=seed)
+        graph = otop.build(n, src, dst, weight)
+        expected = brute_force(n, src, dst, weight)
+        assert graph.n_edges == len(expected)
+        keys = graph.src.astype(np.int64) * n + graph.dst
+        assert np.all(np.diff(keys) > 0)                      # strictly source-major
+        for s, d, w in zip(graph.src, graph.dst, graph.weight):
+            assert expected[(int(s), int(d))] == w
+        # destination view: rows sorted, columns ascending within a row
+        rows = np.repeat(np.arange(n), np.diff(graph.in_rowptr))
+        in_keys = rows.astype(np.int64) * n + graph.in_col
+        assert np.all(np.diff(in_keys) > 0)
+        # out_weight_index is the permutation canonical -> destination slot
+        assert np.array_equal(np.sort(graph.out_weight_index), np.arange(graph.n_edges))
+        assert np.array_equal(graph.in_weight[graph.out_weight_index], graph.weight)
+        assert np.array_equal(graph.in_col[graph.out_weight_index], graph.src)
+        assert np.array_equal(rows[graph.out_weight_index], graph.dst)
+        assert graph.in_rowptr[-1] == graph.out_rowptr[-1] == graph.n_edges
+
+
+def test_long_duplicate_run_sums_in_input_order():
+    values = np.array([1e8, 1.0, -1e8, 1.0, 3.0, -2.0, 1e-3, 5.0, 1e8, -1e8, 0.5], np.float32)
+    graph = otop.build(2, np.zeros(values.size, np.int64), np.ones(values.size, np.int64), values)
+    total = np.float32(0)
+    for v in values:
+        total = np.float32(total + v)
+    assert graph.weight[0] == total
+
+
+def test_duplicates_sum_in_input_order():
+    # 1e8 + 1 - 1e8 in float32 depends on the order; the reference sums in input order.
+    src = np.array([0, 0, 0], np.int64)
+    dst = np.array([1, 1, 1], np.int64)
+    weight = np.array([1e8, 1.0, -1e8], np.float32)
+    graph = otop.build(2, src, dst, weight)
+    expected = np.float32(np.float32(np.float32(0) + np.float32(1e8)) + np.float32(1.0)) - np.float32(1e8)
+    assert graph.weight[0] == expected
+
+
+def test_product_topology_equals_oracle_bitwise():
+    for n, m, seed in ((97, 600, 83), (1024, 20480, 23), (50, 3000, 1)):
+        product = random_topology(n, m, device="cpu", seed=seed)
+        graph = otop.random_graph(n, m, seed=seed)
+        for name in ("src", "dst", "weight", "out_rowptr", "in_rowptr", "in_col",
+                     "out_weight_index", "in_weight"):
+            assert np.array_equal(getattr(product, name).numpy(), getattr(graph, name)), name
+        assert product.n_edges == graph.n_edges
+
+
+def test_product_apply_source_weights_matches_oracle():
+    product = random_topology(60, 500, device="cpu", seed=5)
+    graph = otop.random_graph(60, 500, seed=5)
+    new = product.weight * 0.7
+    product.apply_source_weights_(new)
+    updated = otop.with_weights(graph, new.numpy())
+    assert product.weight_version == 1
+    assert np.array_equal(product.in_weight.numpy(), updated.in_weight)
+
+
+def test_from_edges_rejects_bad_input():
+    import pytest
+
+    with pytest.raises(ValueError, match="out of range"):
+        SparseTopology.from_edges(3, torch.tensor([0, 3]), torch.tensor([1, 1]), torch.ones(2))
+    with pytest.raises(ValueError, match="int32 or torch.int64"):
+        SparseTopology.from_edges(3, torch.tensor([0.0]), torch.tensor([1]), torch.ones(1))
+    with pytest.raises(ValueError, match="equal length"):
+        SparseTopology.from_edges(3, torch.tensor([0, 1]), torch.tensor([1]), torch.ones(2))
