@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 1
+#define NS_ABI_VERSION 2
 
 /* Return codes. */
 #define NS_OK 0
@@ -89,6 +89,43 @@ typedef struct ns_row_plan {
   int32_t reserved;
 } ns_row_plan;
 
+/* Column-panel layout of a CSR matrix for batch widths 1 and 2, built by
+ * ns_plan_panels.  Columns are cut into `n_panels` panels of `panel_width`
+ * neurons (the panel's slice of the state is staged in LDS); rows into
+ * `n_stripes` stripes.  For every (panel p, stripe s) the stripe's rows, with
+ * their edges whose source lies in panel p, are cut into chunks of at most
+ * `chunk_edges` = 512*pad edges and 511 rows, each padded to whole lanes of
+ * `pad` slots.  A tile is one workgroup's work: one panel and a run of
+ * consecutive stripes (its chunks are contiguous).  Edge slot k is original
+ * CSR edge perm[k] (or padding). */
+typedef struct ns_panel_plan {
+  int32_t panel_width;
+  int32_t n_panels;
+  int32_t n_stripes;
+  int32_t n_tiles;
+  int32_t n_chunks;
+  int32_t chunk_edges;
+  int32_t pad;
+  int32_t reserved;
+  int64_t n_slots;             /* edge slots including padding */
+  const int32_t* tiles;        /* [n_tiles][4]: panel, first chunk, end chunk, group */
+  const int32_t* chunks;       /* [n_chunks][8]: first slot, edges, first row, rows,
+                                  first row offset, flags (1: first row continues the
+                                  previous chunk's last row, 2: last row continues,
+                                  4: last chunk of its (panel, stripe)),
+                                  lane table index, stripe */
+  const uint16_t* row_offsets; /* per chunk rows+1 offsets of each row's first edge */
+  const uint16_t* lane_rows;   /* [n_chunks][512]: chunk-local row of each lane's first
+                                  slot (lane l covers slots l*pad .. l*pad+pad-1) */
+  const int32_t* stripes;      /* [n_stripes+1] first row of each stripe */
+  const uint16_t* col;         /* [n_slots] source index minus the panel's first neuron */
+  const void* weight;          /* [n_slots] weights in slot order, encoding of the matrix:
+                                  F32/F16 values, E4M3 codes, NVFP4 nibbles (two per byte) */
+  const uint8_t* slot_scales;  /* NVFP4: e4m3 block-scale code of each slot's edge */
+  float* partials;             /* workspace [n_panels][N][batch] (n_panels > 1): per-panel
+                                  row sums, added in panel order by a second kernel */
+} ns_panel_plan;
+
 /* Arguments of one fused matrix tick. */
 typedef struct ns_step_args {
   int64_t n_neurons;           /* N > 0 */
@@ -101,6 +138,8 @@ typedef struct ns_step_args {
   ns_vector params[6];         /* alpha, gain, rho_d, rho_a, coupling, strength */
   ns_csr matrix;
   ns_row_plan plan;
+  const ns_panel_plan* panels; /* optional (batch <= 2): column-panel layout to use
+                                  instead of the row plan; NULL selects the row plan */
   ns_out_plane out_state;      /* s_{t+1}; must not overlap any input */
   ns_out_plane out_dendrite;   /* d_{t+1} */
   ns_out_plane out_adaptation; /* a_{t+1} */
@@ -158,6 +197,30 @@ int32_t ns_block_edges(int64_t batch);
  * *n_blocks.  Validates rowptr (monotone, rowptr[0] == 0). */
 int ns_plan_row_blocks(const int32_t* rowptr_host, int64_t n_rows, int32_t block_edges,
                        int32_t* bounds, int64_t capacity, int64_t* n_blocks);
+
+/* Host-side panel planner for a host copy of (rowptr, col).  Panel width is
+ * the largest that fits `max_panel_width` neurons, equalised over panels and
+ * rounded to a multiple of 4; stripes split rows by edge count; each panel's
+ * stripes are dealt to `n_groups` tiles in consecutive runs.  Call once
+ * with all output pointers NULL to get the sizes in *plan (n_panels,
+ * n_stripes, n_tiles, n_chunks, n_slots, chunk_edges, pad, panel_width) and
+ * *n_row_offsets, then again with arrays of those sizes:
+ * tiles int32[4*n_tiles], chunks int32[8*n_chunks], row_offsets
+ * uint16[n_row_offsets], lane_rows uint16[512*n_chunks], stripes int32[n_stripes+1],
+ * perm int32[n_slots]
+ * (-1 for padding), col uint16[n_slots].  Pointer fields of *plan are not
+ * touched. */
+int ns_plan_panels(const int32_t* rowptr_host, const int32_t* col_host, int64_t n_rows,
+                   int32_t max_panel_width, int32_t n_stripes, int32_t n_groups,
+                   int32_t chunk_edges, int32_t pad,
+                   ns_panel_plan* plan, int64_t* n_row_offsets, int32_t* tiles, int32_t* chunks,
+                   uint16_t* row_offsets, uint16_t* lane_rows, int32_t* stripes, int32_t* perm,
+                   uint16_t* col);
+
+/* Panel geometry the tick kernels use for batch width `batch` (1 or 2):
+ * largest panel width, chunk edges and padding (any NULL output is skipped). */
+int ns_panel_geometry(int64_t batch, int32_t* max_panel_width, int32_t* chunk_edges,
+                      int32_t* pad);
 
 /* Fused matrix tick.  Replaces dendritic_step
  * (reference: csrc/bindings.cpp:3-7,137-142; csrc/compartmental.cu:176-236),

@@ -17,6 +17,11 @@ namespace ns {
 constexpr int kThreads = 256;   // 4 wavefronts of 64 lanes
 constexpr int kMaxRows = 256;   // rows per row block (one lane per row at most density)
 
+// Column-panel kernels (batch widths 1 and 2): 512 lanes; a chunk holds at most
+// 511 rows so its rows+1 offsets fit one per lane.
+constexpr int kPanelThreads = 512;
+constexpr int kPanelMaxRows = kPanelThreads - 1;
+
 struct Plane {
   const float* data;
   int64_t sb, sn;

@@ -334,8 +334,10 @@ hipError_t launch_tick(const TickArgs& A, int fmt, hipStream_t stream) {
   }
 }
 
+int panel_step(const ns_step_args& a, hipStream_t stream);
+
 // Host-side validation shared by the tick and the plain product.
-int check_matrix(const ns_csr& m, int64_t n, const ns_row_plan& plan, int64_t batch) {
+int check_csr(const ns_csr& m, int64_t n) {
   if (m.n_rows != n) return fail("CSR row count %lld does not match N=%lld",
                                  (long long)m.n_rows, (long long)n);
   if (m.n_edges < 0 || m.n_edges >= (int64_t{1} << 31))
@@ -359,6 +361,11 @@ int check_matrix(const ns_csr& m, int64_t n, const ns_row_plan& plan, int64_t ba
     default:
       return fail("unknown CSR weight format %d", m.format);
   }
+  return NS_OK;
+}
+
+int check_matrix(const ns_csr& m, int64_t n, const ns_row_plan& plan, int64_t batch) {
+  if (int rc = check_csr(m, n)) return rc;
   if (!plan.bounds || plan.n_blocks < 1) return fail("a row plan is required");
   if (plan.n_blocks > 0x7FFFFFFF) return fail("row plan has too many blocks");
   if (plan.block_edges != capacity_for(batch))
@@ -403,7 +410,11 @@ extern "C" int ns_dendritic_step(const ns_step_args* args, void* stream) {
   if (a.n_neurons >= (int64_t{1} << 31)) return fail("N must be below 2^31");
   for (int i = 0; i < 6; ++i)
     if (!a.params[i].data) return fail("six neuron parameter vectors are required");
-  if (int rc = check_matrix(a.matrix, a.n_neurons, a.plan, a.batch)) return rc;
+  if (a.panels) {
+    if (int rc = check_csr(a.matrix, a.n_neurons)) return rc;
+  } else if (int rc = check_matrix(a.matrix, a.n_neurons, a.plan, a.batch)) {
+    return rc;
+  }
   if (a.batch == 0) return NS_OK;  // empty planes may carry null pointers
   if (!a.state.data || !a.dendrite.data || !a.adaptation.data)
     return fail("state, dendrite and adaptation data are required");
@@ -423,7 +434,7 @@ extern "C" int ns_dendritic_step(const ns_step_args* args, void* stream) {
     for (int p = o + 1; p < 3; ++p)
       if (overlaps(outs[o], outs[p])) return fail("output planes must not overlap each other");
   }
-  if (a.batch == 0) return NS_OK;
+  if (a.panels) return panel_step(a, static_cast<hipStream_t>(stream));
 
   TickArgs A{};
   A.N = a.n_neurons; A.B = a.batch; A.M = a.matrix.n_edges;

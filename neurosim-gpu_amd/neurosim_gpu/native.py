@@ -35,7 +35,7 @@ import numpy as np
 import torch
 
 _LIB_NAME = "libneurosim_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 WEIGHT_F32, WEIGHT_F16, WEIGHT_E4M3, WEIGHT_NVFP4 = 0, 1, 2, 3
 _PLAN_CACHE = 64   # row plans kept per extension (one per live topology and batch width)
@@ -68,11 +68,22 @@ class _RowPlan(ctypes.Structure):
                 ("reserved", ctypes.c_int32)]
 
 
+class _PanelPlan(ctypes.Structure):
+    _fields_ = [("panel_width", ctypes.c_int32), ("n_panels", ctypes.c_int32),
+                ("n_stripes", ctypes.c_int32), ("n_tiles", ctypes.c_int32),
+                ("n_chunks", ctypes.c_int32), ("chunk_edges", ctypes.c_int32),
+                ("pad", ctypes.c_int32), ("reserved", ctypes.c_int32), ("n_slots", _c_i64),
+                ("tiles", _c_ptr), ("chunks", _c_ptr), ("row_offsets", _c_ptr),
+                ("lane_rows", _c_ptr), ("stripes", _c_ptr), ("col", _c_ptr), ("weight", _c_ptr),
+                ("slot_scales", _c_ptr), ("partials", _c_ptr)]
+
+
 class _StepArgs(ctypes.Structure):
     _fields_ = [("n_neurons", _c_i64), ("batch", _c_i64),
                 ("state", _Plane), ("dendrite", _Plane), ("adaptation", _Plane),
                 ("drive", _Plane), ("dendritic_drive", _Plane),
                 ("params", _Vector * 6), ("matrix", _Csr), ("plan", _RowPlan),
+                ("panels", _c_ptr),
                 ("out_state", _OutPlane), ("out_dendrite", _OutPlane),
                 ("out_adaptation", _OutPlane)]
 
@@ -120,6 +131,14 @@ def load_library() -> ctypes.CDLL:
     lib.ns_plan_row_blocks.restype = ctypes.c_int
     lib.ns_plan_row_blocks.argtypes = [_c_ptr, _c_i64, ctypes.c_int32, _c_ptr, _c_i64,
                                        ctypes.POINTER(_c_i64)]
+    lib.ns_panel_geometry.restype = ctypes.c_int
+    lib.ns_panel_geometry.argtypes = [_c_i64, ctypes.POINTER(ctypes.c_int32),
+                                      ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)]
+    lib.ns_plan_panels.restype = ctypes.c_int
+    lib.ns_plan_panels.argtypes = [_c_ptr, _c_ptr, _c_i64, ctypes.c_int32, ctypes.c_int32,
+                                   ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                   ctypes.POINTER(_PanelPlan),
+                                   ctypes.POINTER(_c_i64)] + [_c_ptr] * 7
     for name, kind in (("ns_dendritic_step", _StepArgs), ("ns_dendritic_event", _EventArgs),
                        ("ns_csr_spmm", _SpmmArgs)):
         fn = getattr(lib, name)
@@ -214,6 +233,129 @@ def new_planes(count: int, batch: int, n: int, like: torch.Tensor) -> list[torch
     return [storage[i].T for i in range(count)]
 
 
+def panel_geometry(batch: int) -> tuple[int, int, int]:
+    """(largest panel width, chunk edges, slots per lane) of the panel kernel."""
+    lib = load_library()
+    width, chunk, pad = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    _raise_on(lib.ns_panel_geometry(int(batch), ctypes.byref(width), ctypes.byref(chunk),
+                                    ctypes.byref(pad)), lib)
+    return width.value, chunk.value, pad.value
+
+
+def plan_panels_host(rowptr: torch.Tensor, col: torch.Tensor, batch: int, n_stripes: int,
+                     max_panel_width: int | None = None, n_groups: int | None = None):
+    """Host panel layout of a CSR (numpy arrays): see ns_plan_panels."""
+    lib = load_library()
+    width, chunk, pad = panel_geometry(batch)
+    if max_panel_width is not None:
+        width = min(width, int(max_panel_width))
+    rowptr = np.ascontiguousarray(rowptr.detach().to("cpu", torch.int32).numpy())
+    col = np.ascontiguousarray(col.detach().to("cpu", torch.int32).numpy())
+    n = rowptr.size - 1
+    plan = _PanelPlan()
+    rows = _c_i64()
+    groups = int(n_groups) if n_groups is not None else int(n_stripes)
+    args = (rowptr.ctypes.data, col.ctypes.data if col.size else None, n, width, int(n_stripes),
+            groups, chunk, pad, ctypes.byref(plan), ctypes.byref(rows))
+    _raise_on(lib.ns_plan_panels(*args, *([None] * 7)), lib)
+    tiles = np.empty(4 * plan.n_tiles, np.int32)
+    chunks = np.empty(8 * plan.n_chunks, np.int32)
+    offsets = np.empty(rows.value, np.uint16)
+    lanes = np.empty(512 * plan.n_chunks, np.uint16)
+    stripes = np.empty(plan.n_stripes + 1, np.int32)
+    perm = np.empty(plan.n_slots, np.int32)
+    cols = np.empty(plan.n_slots, np.uint16)
+    _raise_on(lib.ns_plan_panels(*args, tiles.ctypes.data, chunks.ctypes.data,
+                                 offsets.ctypes.data, lanes.ctypes.data, stripes.ctypes.data,
+                                 perm.ctypes.data, cols.ctypes.data), lib)
+    return plan, tiles, chunks, offsets, lanes, stripes, perm, cols
+
+
+def _device_tensor(array: np.ndarray, device) -> torch.Tensor:
+    if array.dtype == np.uint16:
+        array = array.view(np.int16)
+    return torch.from_numpy(np.ascontiguousarray(array)).to(device)
+
+
+class PanelLayout:
+    """Column-panel layout of one graph for batch width 1 or 2 (see ns_plan_panels).
+
+    Built once per graph structure on the host from copies of in_rowptr and
+    in_col (a synchronisation; set-up only).  Holds the device tables, the
+    slot permutation, the partials workspace and, per weight version
+    and encoding, the weights rearranged into slot order on the device.
+    Launches sharing a layout must be ordered on one stream.
+    """
+
+    def __init__(self, topology, batch: int, device, *, n_stripes: int | None = None,
+                 max_panel_width: int | None = None, n_groups: int | None = None) -> None:
+        n = topology.n_neurons
+        width, chunk, _ = panel_geometry(batch)
+        panels = -(-n // (min(width, max_panel_width or width) & ~3))
+        if n_groups is None:
+            # One workgroup per compute unit: groups of stripes per panel.
+            units = torch.cuda.get_device_properties(device).multi_processor_count
+            n_groups = max(1, units // panels)
+        if n_stripes is None:
+            # About four chunks of edges per (panel, stripe), at least one stripe per group.
+            per_pair = max(topology.n_edges, 1) / (panels * 4 * chunk)
+            n_stripes = max(int(n_groups), int(per_pair))
+        plan, tiles, chunks, offsets, lanes, stripes, perm, cols = plan_panels_host(
+            topology.in_rowptr, topology.in_col, batch, n_stripes, max_panel_width, n_groups)
+        self.batch, self.n = int(batch), n
+        self.n_panels, self.n_stripes, self.n_slots = plan.n_panels, plan.n_stripes, plan.n_slots
+        self.panel_width = plan.panel_width
+        self.tiles = _device_tensor(tiles, device)
+        self.chunks = _device_tensor(chunks, device)
+        self.row_offsets = _device_tensor(offsets, device)
+        self.lane_rows = _device_tensor(lanes, device)
+        self.stripes = _device_tensor(stripes, device)
+        self.col = _device_tensor(cols, device)
+        perm_t = torch.from_numpy(perm).to(device)
+        self.valid = perm_t >= 0
+        self.perm = perm_t.clamp_min(0).to(torch.int64)
+        self.partials = (torch.empty(plan.n_panels * n * batch, dtype=torch.float32, device=device)
+                         if plan.n_panels > 1 else None)
+        self._plan = plan
+        self._slot_weights: tuple | None = None
+        self._slot_key = None
+
+    def slot_weights(self, key, weight: torch.Tensor, block_scales: torch.Tensor | None):
+        """Weights of the CSR payload (original edge order) rearranged into slot order."""
+        if self._slot_key == key and self._slot_weights is not None:
+            return self._slot_weights
+        with torch.no_grad():
+            if weight.dtype in (torch.float32, torch.float16):
+                slots = torch.where(self.valid, weight[self.perm], torch.zeros((), dtype=weight.dtype,
+                                                                               device=weight.device))
+                scales = None
+            elif block_scales is None:        # fp8 e4m3 codes
+                slots = torch.where(self.valid, weight[self.perm], torch.zeros((), dtype=torch.uint8,
+                                                                               device=weight.device))
+                scales = None
+            else:                             # nvfp4: one nibble and one block-scale code per slot
+                edge = self.perm
+                nibble = (weight[edge >> 1] >> ((edge & 1) * 4).to(torch.uint8)) & 15
+                nibble = torch.where(self.valid, nibble, torch.zeros_like(nibble))
+                slots = (nibble[0::2] | (nibble[1::2] << 4)).contiguous()
+                scales = torch.where(self.valid, block_scales[edge >> 4],
+                                     torch.zeros((), dtype=torch.uint8, device=weight.device))
+            self._slot_weights = (slots.contiguous(), None if scales is None else scales.contiguous())
+            self._slot_key = key
+        return self._slot_weights
+
+    def plan_struct(self, slot_weight: torch.Tensor, slot_scales: torch.Tensor | None) -> _PanelPlan:
+        plan = _PanelPlan()
+        ctypes.memmove(ctypes.addressof(plan), ctypes.addressof(self._plan), ctypes.sizeof(plan))
+        plan.tiles, plan.chunks = self.tiles.data_ptr(), self.chunks.data_ptr()
+        plan.row_offsets, plan.lane_rows = self.row_offsets.data_ptr(), self.lane_rows.data_ptr()
+        plan.stripes, plan.col = self.stripes.data_ptr(), self.col.data_ptr()
+        plan.weight = slot_weight.data_ptr()
+        plan.slot_scales = slot_scales.data_ptr() if slot_scales is not None else None
+        plan.partials = self.partials.data_ptr() if self.partials is not None else None
+        return plan
+
+
 class NativeExtension:
     """Drop-in for the reference's compiled extension (hot-path ops only)."""
 
@@ -290,7 +432,7 @@ class NativeExtension:
     # -- ops ----------------------------------------------------------------
     def dendritic_step(self, state, dendrite, adaptation, params, rowptr, source, weight,
                        input, input_scalar, dendritic_input, dendritic_scalar, width,
-                       block_scales=None, global_scale=None):
+                       block_scales=None, global_scale=None, panels=None):
         _check_state(state)
         args = _StepArgs()
         args.state = _plane(state, state, "state")
@@ -304,7 +446,12 @@ class NativeExtension:
             raise RuntimeError("width must be 8, 16 or 32")
         batch, n = state.shape
         args.n_neurons, args.batch = n, batch
-        args.plan = self.plan_for(rowptr, batch)
+        panel_struct = None
+        if panels is not None:
+            panel_struct = panels          # a _PanelPlan built by PanelLayout.plan_struct
+            args.panels = ctypes.addressof(panel_struct)
+        else:
+            args.plan = self.plan_for(rowptr, batch)
         outs = new_planes(3, batch, n, state)
         args.out_state, args.out_dendrite, args.out_adaptation = (_out(o) for o in outs)
         stream = torch.cuda.current_stream(state.device).cuda_stream
@@ -380,7 +527,8 @@ class TickLauncher:
     """
 
     def __init__(self, extension: "NativeExtension", state_like: torch.Tensor, params, rowptr,
-                 col, weight, drive, dendritic_drive, block_scales=None, global_scale=None):
+                 col, weight, drive, dendritic_drive, block_scales=None, global_scale=None,
+                 panels=None):
         _check_state(state_like)
         self.lib = extension.lib
         args = _StepArgs()
@@ -397,12 +545,16 @@ class TickLauncher:
                                       else float(dendritic_drive), state_like)
         batch, n = state_like.shape
         args.n_neurons, args.batch = n, batch
-        bounds, blocks, capacity = extension.plan_tensors(rowptr, batch)
-        args.plan = _RowPlan(bounds.data_ptr(), blocks, capacity, 0)
+        bounds = None
+        if panels is not None:
+            args.panels = ctypes.addressof(panels)
+        else:
+            bounds, blocks, capacity = extension.plan_tensors(rowptr, batch)
+            args.plan = _RowPlan(bounds.data_ptr(), blocks, capacity, 0)
         self.args = args
         self.batch, self.n = batch, n
         self._keep = (list(params), rowptr, col, weight, drive_t, ddrive_t, block_scales,
-                      global_scale, bounds)
+                      global_scale, bounds, panels)
 
     def __call__(self, source: tuple, target: tuple, stream: int | None = None) -> None:
         """One tick from planes (s, d, a) into planes (s', d', a') (all [B,N] views)."""

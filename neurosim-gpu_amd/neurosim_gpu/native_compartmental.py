@@ -21,7 +21,7 @@ from __future__ import annotations
 import torch
 
 from .compartmental import DendriticDynamics, DendriticMatrixRuntime, DendriticPELSRuntime
-from .native import NativeExtension, load_native_extension
+from .native import NativeExtension, PanelLayout, load_native_extension
 from .topology import SparseTopology
 
 
@@ -78,12 +78,25 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
     changes) and decodes them in-kernel before each float32 multiply.
     Returned states stay valid after later ticks (every tick allocates fresh
     outputs).  ``threads_per_row`` is accepted for compatibility.
+
+    ``kernel`` picks the tick kernel: "panels" stages column panels of the
+    state in LDS and streams a panel-sorted copy of the graph (batch 1 or 2;
+    built once, at construction), "rows" streams the CSR as is and gathers
+    the state from cache, "auto" uses panels whenever the batch allows.
+    ``panel_width`` caps the neurons per panel (default: what LDS holds),
+    ``panel_stripes`` sets the row stripes (default: about four chunks of
+    edges per panel and stripe) and ``panel_groups`` the workgroups per panel
+    (default: compute units / panels).
     """
 
     def __init__(self, topology: SparseTopology, dynamics: DendriticDynamics,
                  initial_state: torch.Tensor, *, threads_per_row: int | None = None,
                  extension=None, weight_dtype: torch.dtype = torch.float32,
-                 weight_format: str | None = None) -> None:
+                 weight_format: str | None = None, kernel: str = "auto",
+                 panel_width: int | None = None, panel_stripes: int | None = None,
+                 panel_groups: int | None = None) -> None:
+        if kernel not in ("auto", "rows", "panels"):
+            raise ValueError("kernel must be 'auto', 'rows' or 'panels'")
         if threads_per_row not in (None, 8, 16, 32):
             raise ValueError("threads_per_row must be 8, 16, 32 or None")
         _require_gpu_float32(initial_state)
@@ -100,10 +113,31 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         self.weight_dtype = weight_dtype
         self.weight_format = weight_format
         self._invalidate_precision_cache()
+        batch = initial_state.shape[0]
+        native = isinstance(self.extension, NativeExtension)
+        if kernel == "panels" and (batch not in (1, 2) or not native):
+            raise ValueError("the panel kernel needs batch 1 or 2 and the native extension")
+        use_panels = kernel == "panels" or (kernel == "auto" and batch in (1, 2) and native)
+        self.kernel = "panels" if use_panels else "rows"
+        self._panels = (PanelLayout(topology, batch, initial_state.device, n_stripes=panel_stripes,
+                                    max_panel_width=panel_width, n_groups=panel_groups)
+                        if use_panels else None)
 
     def _invalidate_precision_cache(self) -> None:
         self._packed_weight = None
         self._packed_weight_version = -1
+        self._panel_struct = None
+        self._panel_struct_key = None
+
+    def _panel_plan(self, weight: torch.Tensor, scales: tuple):
+        """ctypes panel plan for this tick's weights (rebuilt when the weights change)."""
+        key = (self.topology.weight_version, self.checkpoint_precision, weight.data_ptr())
+        if self._panel_struct_key != key:
+            block = scales[0] if len(scales) == 2 else None
+            slots, slot_scales = self._panels.slot_weights(key, weight, block)
+            self._panel_struct = self._panels.plan_struct(slots, slot_scales)
+            self._panel_struct_key = key
+        return self._panel_struct
 
     @property
     def checkpoint_precision(self) -> str:
@@ -151,10 +185,13 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         u, us = self._drive(drive)
         v, vs = self._drive(dendritic_drive)
         weight, scales, backend = self._weights()
+        extra = {}
+        if self._panels is not None:
+            extra["panels"] = self._panel_plan(weight, scales)
         self.state, self.dendritic_state, self.adaptation_state = self.extension.dendritic_step(
             self.state, self.dendritic_state, self.adaptation_state, self._parameters(),
             self.topology.in_rowptr, self.topology.in_col, weight,
-            u, us, v, vs, self.threads_per_row, *scales)
+            u, us, v, vs, self.threads_per_row, *scales, **extra)
         self.last_backend = backend
         return self.state
 

@@ -31,7 +31,7 @@ def test_every_declared_symbol_is_exported(lib):
     names = declared_functions()
     assert set(names) == {"ns_abi_version", "ns_last_error", "ns_block_edges",
                           "ns_plan_row_blocks", "ns_dendritic_step", "ns_dendritic_event",
-                          "ns_csr_spmm"}
+                          "ns_csr_spmm", "ns_plan_panels", "ns_panel_geometry"}
     for name in names:
         assert hasattr(lib, name), name
     assert lib.ns_abi_version() == native.ABI_VERSION

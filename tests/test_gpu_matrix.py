@@ -154,8 +154,13 @@ def test_packed_formats_equal_decoded_fp32(gpu, fmt, edges):
             if tick == 3:
                 graph.apply_source_weights_(graph.weight * 0.7)
             if tick in (0, 3):
-                host = graph.in_weight.cpu().numpy()
-                csr = torch.from_numpy(op.quantize_dequantize(host, fmt)).to(gpu)
+                # decode exactly the payload the kernel reads (oracle decoder, edge by edge)
+                native._weights()
+                codes, *scales = native._packed_weight
+                block = scales[0].cpu().numpy() if fmt == "nvfp4" else None
+                host = op.decode_packed(codes.cpu().numpy(), block, np.float32(scales[-1].item()),
+                                        graph.n_edges, fmt)
+                csr = torch.from_numpy(host).to(gpu)
                 decoded.apply_source_weights_(csr[graph.out_weight_index.long()])
                 oracle_graph = otop.build(97, graph.src.cpu().numpy(), graph.dst.cpu().numpy(),
                                           decoded.weight.cpu().numpy())

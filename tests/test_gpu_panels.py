@@ -1,0 +1,124 @@
+"""The column-panel tick (batch 1 and 2) on the MI355X.
+
+Several panels are forced with small panel widths so the per-panel partial
+sums and the last-arrival combine run on small graphs; hub rows longer than
+one chunk exercise the continuation carry.  Bars: float32 within 1e-5 of the
+oracle; fp16/fp8/nvfp4 storage bitwise equal to the panel tick on the
+decoded float32 weights; bitwise repeatable.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from cases import column_drive, make_case, max_err, model_to, standard_model
+from oracle import precision as op
+from oracle import runtime as ort
+from oracle import topology as otop
+from neurosim_gpu import NativeDendriticMatrixRuntime, SparseTopology, topology_to
+
+pytestmark = pytest.mark.gpu
+FIELDS = ("state", "dendritic_state", "adaptation_state")
+
+
+def errors(native, oracle) -> float:
+    return max(max_err(getattr(native, f), getattr(oracle, f)) for f in FIELDS)
+
+
+def hub_case(gpu, n=12_000, seed=2):
+    """Random rows plus two hub rows (one longer than a chunk of 8192 edges when n allows)."""
+    rng = np.random.default_rng(seed)
+    hub = min(n, 9000)
+    dst = np.concatenate([np.zeros(hub, np.int64), np.full(n // 2, 3), rng.integers(0, n, 8 * n)])
+    src = np.concatenate([np.arange(hub), rng.permutation(n)[: n // 2], rng.integers(0, n, 8 * n)])
+    weight = (rng.standard_normal(dst.size) * 0.01).astype(np.float32)
+    graph = otop.build(n, src, dst, weight)
+    topology = SparseTopology.from_edges(n, torch.from_numpy(src), torch.from_numpy(dst),
+                                         torch.from_numpy(weight))
+    model, params = standard_model(n)
+    return graph, topology_to(topology, gpu), model_to(model, gpu), params
+
+
+@pytest.mark.parametrize("batch", [1, 2])
+@pytest.mark.parametrize("width,stripes,groups", [(None, None, None), (1000, 7, 3), (256, 9, 2)])
+def test_panels_match_oracle(gpu, batch, width, stripes, groups):
+    print(f"case panels batch={batch} width={width} stripes={stripes} groups={groups}", flush=True)
+    graph, topology, model, params = hub_case(gpu)
+    drive = column_drive(batch)
+    native = NativeDendriticMatrixRuntime(topology, model, torch.zeros(batch, graph.n, device=gpu),
+                                          kernel="panels", panel_width=width, panel_stripes=stripes,
+                                          panel_groups=groups)
+    oracle = ort.MatrixOracle(graph, params, torch.zeros(batch, graph.n))
+    assert native.kernel == "panels"
+    worst = 0.0
+    for _ in range(30):
+        native.step(drive.to(gpu), dendritic_drive=0.1)
+        oracle.step(drive, 0.1)
+        worst = max(worst, errors(native, oracle))
+    print(f"panels batch={batch} width={width}: {worst:.3e} over 30 ticks "
+          f"({native._panels.n_panels} panels x {native._panels.n_stripes} stripes)")
+    assert worst <= 1e-5
+
+
+@pytest.mark.parametrize("batch", [1, 2])
+def test_panels_and_rows_agree_and_repeat(gpu, batch):
+    case = make_case(20_000, 400_000, 5, gpu)
+    runs = {}
+    for kernel in ("panels", "rows", "panels"):
+        native = NativeDendriticMatrixRuntime(case.topology, case.model,
+                                              torch.zeros(batch, 20_000, device=gpu), kernel=kernel,
+                                              panel_width=4096)
+        for _ in range(25):
+            native.step(0.2, dendritic_drive=0.1)
+        if kernel in runs:
+            assert torch.equal(native.state, runs[kernel].state)      # bitwise repeatable
+        runs[kernel] = native
+    assert errors(runs["panels"], runs["rows"]) <= 2e-6
+
+
+@pytest.mark.parametrize("fmt", ["fp16", "fp8", "nvfp4"])
+@pytest.mark.parametrize("batch", [1, 2])
+def test_panel_formats_equal_decoded_fp32(gpu, fmt, batch):
+    graph, topology, model, params = hub_case(gpu, n=6000, seed=9)
+    kwargs = {"weight_dtype": torch.float16} if fmt == "fp16" else {"weight_format": fmt}
+    native = NativeDendriticMatrixRuntime(topology, model, torch.zeros(batch, 6000, device=gpu),
+                                          kernel="panels", panel_width=1024, panel_stripes=5,
+                                          **kwargs)
+    native._weights()
+    if fmt == "fp16":
+        decoded_host = topology.in_weight.half().float().cpu().numpy()
+    else:
+        codes, *scales = native._packed_weight
+        block = scales[0].cpu().numpy() if fmt == "nvfp4" else None
+        decoded_host = op.decode_packed(codes.cpu().numpy(), block, np.float32(scales[-1].item()),
+                                        topology.n_edges, fmt)
+    decoded = SparseTopology.from_edges(
+        6000, topology.src, topology.dst,
+        torch.from_numpy(decoded_host).to(gpu)[topology.out_weight_index.long()])
+    reference = NativeDendriticMatrixRuntime(decoded, model, torch.zeros(batch, 6000, device=gpu),
+                                             kernel="panels", panel_width=1024, panel_stripes=5)
+    oracle = ort.MatrixOracle(graph, params, torch.zeros(batch, 6000), in_weight=decoded_host)
+    for _ in range(10):
+        native.step(0.2, dendritic_drive=0.1)
+        reference.step(0.2, dendritic_drive=0.1)
+        oracle.step(0.2, 0.1)
+        for field in FIELDS:
+            assert torch.equal(getattr(native, field), getattr(reference, field))
+    assert errors(native, oracle) <= 1e-5
+
+
+def test_panel_weight_refresh_after_mutation(gpu):
+    case = make_case(3000, 60_000, 4, gpu)
+    native = NativeDendriticMatrixRuntime(case.topology, case.model, torch.zeros(1, 3000, device=gpu),
+                                          kernel="panels", panel_width=512, panel_stripes=4)
+    oracle = ort.MatrixOracle(case.graph, case.params, torch.zeros(1, 3000))
+    for tick in range(12):
+        if tick == 6:
+            case.topology.apply_source_weights_(case.topology.weight * 0.7)
+            oracle.matrix = ort.csr_matrix(otop.with_weights(case.graph,
+                                                             case.topology.weight.cpu().numpy()))
+        native.step(0.2, dendritic_drive=0.1)
+        oracle.step(0.2, 0.1)
+    assert errors(native, oracle) <= 1e-5
