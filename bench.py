@@ -54,11 +54,22 @@ def algorithmic_bytes(fmt: str, n: int, m: int, batch: int) -> int:
     return 4 * (n + 1) + 4 * m + weight_bytes(fmt, m) + 24 * batch * n + 24 * n
 
 
-def build_runtime(fmt: str, topology, model, device):
+def build_runtime(fmt: str, topology, model, device, kernel: str = "auto"):
     kwargs = {"fp32": {}, "fp16": {"weight_dtype": torch.float16},
               "fp8": {"weight_format": "fp8"}, "nvfp4": {"weight_format": "nvfp4"}}[fmt]
     return NativeDendriticMatrixRuntime(topology, model, torch.zeros(BATCH, N_NEURONS, device=device),
-                                        **kwargs)
+                                        kernel=kernel, **kwargs)
+
+
+def copy_calibration(mib: int = 256, repeats: int = 10) -> None:
+    """Plain device-to-device copies of a known size, for scaling PMC byte counters:
+    each launch reads and writes exactly ``mib`` MiB."""
+    source = torch.ones(mib * 1024 * 1024 // 4, dtype=torch.float32, device="cuda")
+    target = torch.empty_like(source)
+    for _ in range(repeats):
+        target.copy_(source)
+    torch.cuda.synchronize()
+    log(f"copy calibration: {repeats} copies of {mib} MiB")
 
 
 def time_ticks(runtime, steps: int, warmup: int) -> tuple[float, MatrixRollout]:
@@ -157,6 +168,10 @@ def main() -> None:
     cli.add_argument("--formats", default="fp32,fp16,fp8,nvfp4")
     cli.add_argument("--no-cpu-baseline", action="store_true")
     cli.add_argument("--no-mall-flush", action="store_true")
+    cli.add_argument("--kernel", default="auto", choices=("auto", "rows", "panels"),
+                     help="tick kernel: LDS column panels (batch 1-2) or CSR row blocks")
+    cli.add_argument("--copy-calibration", action="store_true",
+                     help="only run 256 MiB device copies (PMC byte-counter calibration)")
     args = cli.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -167,6 +182,9 @@ def main() -> None:
         cli.error("steps must be positive and warmup non-negative")
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    if args.copy_calibration:
+        copy_calibration()
+        return
     log("building graph on the host")
     topology_cpu = random_topology(N_NEURONS, CANDIDATES, device="cpu", seed=SEED)
     m = topology_cpu.n_edges
@@ -184,7 +202,7 @@ def main() -> None:
     flushed = None
     for fmt in args.formats.split(","):
         log(f"timing {fmt}: {args.warmup} warm-up + {args.steps} ticks")
-        runtime = build_runtime(fmt, topology, model, device)
+        runtime = build_runtime(fmt, topology, model, device, args.kernel)
         ms, rollout = time_ticks(runtime, args.steps, args.warmup)
         alg = algorithmic_bytes(fmt, N_NEURONS, m, BATCH)
         results[fmt] = {"ms_per_tick": round(ms, 5), "ticks_per_s": round(1000.0 / ms, 1),
@@ -207,7 +225,7 @@ def main() -> None:
         "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": WORKLOAD, "n_neurons": N_NEURONS, "n_edges": m, "batch": BATCH,
                    "candidate_edges": CANDIDATES, "seed": SEED, "weights": primary_fmt,
-                   "ticks_per_graph": CHUNK},
+                   "ticks_per_graph": CHUNK, "kernel": args.kernel},
         "ticks_per_s": primary["ticks_per_s"],
         "achieved_GBps": round(achieved, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,

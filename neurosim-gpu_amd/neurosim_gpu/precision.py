@@ -41,6 +41,20 @@ def _e2m1_constants(device: torch.device, dtype: torch.dtype) -> tuple[torch.Ten
                 torch.tensor(_E2M1_LEVELS, device=device, dtype=dtype))
 
 
+@lru_cache(maxsize=None)
+def _divisors(device: torch.device, dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
+    """0-d device tensors 448 and 6*448, created once per device/dtype.
+
+    Dividing a device tensor by a Python number lets PyTorch's GPU kernels
+    multiply by the rounded reciprocal instead, which can move the scale by
+    one ulp (and flip codes) against the CPU's correctly rounded division;
+    a device-tensor divisor keeps the true quotient on every device.
+    """
+    with torch.inference_mode(False), torch.no_grad():
+        return (torch.tensor(_FP8_MAX, device=device, dtype=dtype),
+                torch.tensor(6.0 * _FP8_MAX, device=device, dtype=dtype))
+
+
 def validate_precision(value: str) -> Precision:
     if value not in PRECISIONS:
         raise ValueError("precision must be 'fp32', 'fp16', 'fp8', or 'nvfp4'")
@@ -60,7 +74,8 @@ def _tiny() -> float:
 
 def _encode_e4m3(value: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     amax = value.abs().amax() if value.numel() else value.new_zeros(())
-    scale = (amax / _FP8_MAX).clamp_min(_tiny())
+    fp8_max, _ = _divisors(value.device, value.dtype)
+    scale = (amax / fp8_max).clamp_min(_tiny())
     codes = (value / scale).clamp(-_FP8_MAX, _FP8_MAX).to(torch.float8_e4m3fn)
     return codes, scale
 
@@ -75,7 +90,8 @@ def _encode_e2m1(value: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch
     magnitude = blocks.abs()
     block_amax = magnitude.amax(dim=-1, keepdim=True)
     amax = block_amax.amax() if value.numel() else value.new_zeros(())
-    global_scale = (amax / (6.0 * _FP8_MAX)).clamp_min(_tiny())
+    _, six_fp8_max = _divisors(value.device, value.dtype)
+    global_scale = (amax / six_fp8_max).clamp_min(_tiny())
     block_scale = (block_amax / (6.0 * global_scale)).clamp_max(_FP8_MAX).to(torch.float8_e4m3fn)
     unit = global_scale * block_scale.float()
     normalized = magnitude / torch.where(unit > 0, unit, 1.0)

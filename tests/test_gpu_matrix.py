@@ -247,6 +247,24 @@ def large_case(gpu):
     return make_case(166_000, 25_000_000, 0, gpu)
 
 
+@pytest.mark.parametrize("fmt", ["fp8", "nvfp4"])
+def test_device_encoder_is_bitwise_the_oracle_at_25m_edges(gpu, large_case, fmt):
+    """Codes, block scales and global scale encoded on the GPU == the CPU oracle's.
+
+    A Python-number divisor lets PyTorch's GPU division multiply by a rounded
+    reciprocal; at this size that moved the NVFP4 global scale by one ulp and
+    flipped codes.  The encoder must reproduce the CPU's true quotients.
+    """
+    print(f"case encode N=166000 M=25M fmt={fmt}", flush=True)
+    weight = large_case.graph.in_weight
+    codes, scales, scale = encode_sparse_weights(torch.from_numpy(weight).to(gpu), fmt)
+    want_codes, want_scales, want_scale = op.encode_sparse_weights(weight, fmt)
+    assert np.float32(scale.item()).tobytes() == np.float32(want_scale).tobytes()
+    assert np.array_equal(codes.cpu().numpy(), want_codes)
+    if fmt == "nvfp4":
+        assert np.array_equal(scales.cpu().numpy(), want_scales)
+
+
 @pytest.mark.parametrize("fmt", ["fp32", "fp16", "fp8", "nvfp4"])
 def test_cfg3_large_1000_ticks(gpu, large_case, fmt):
     """N=166000, M~25M, B=1: fp32 vs oracle; fp16/fp8/nvfp4 vs oracle on decoded weights."""
