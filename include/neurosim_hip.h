@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 2
+#define NS_ABI_VERSION 3
 
 /* Return codes. */
 #define NS_OK 0
@@ -91,33 +91,30 @@ typedef struct ns_row_plan {
 
 /* Column-panel layout of a CSR matrix for batch widths 1 and 2, built by
  * ns_plan_panels.  Columns are cut into `n_panels` panels of `panel_width`
- * neurons (the panel's slice of the state is staged in LDS); rows into
- * `n_stripes` stripes.  For every (panel p, stripe s) the stripe's rows, with
- * their edges whose source lies in panel p, are cut into chunks of at most
- * `chunk_edges` = 512*pad edges and 511 rows, each padded to whole lanes of
- * `pad` slots.  A tile is one workgroup's work: one panel and a run of
- * consecutive stripes (its chunks are contiguous).  Edge slot k is original
- * CSR edge perm[k] (or padding). */
+ * neurons (a panel's slice of the state fits in one workgroup's LDS).  A tile
+ * is one workgroup's work: one panel and a range of destination rows.  The
+ * tile's rows are sorted by the length of their segment in the panel and cut
+ * into groups; a group gives each of its rows 2^lg lanes of a 64-lane
+ * wavefront (64 >> lg rows), lane j of a row taking the row's edges j, j+2^lg,
+ * ...  A group's slots are step-major: slot (step k, lane l) is
+ * first_slot + 64*k + l.  Each of the tile's `waves` wavefronts owns a run of
+ * consecutive groups whose slots are contiguous.  Padding slots have source
+ * index `panel_width` (a zero kept in LDS) and weight code 0.  Edge slot k is
+ * original CSR edge perm[k] (or padding). */
 typedef struct ns_panel_plan {
   int32_t panel_width;
   int32_t n_panels;
-  int32_t n_stripes;
   int32_t n_tiles;
-  int32_t n_chunks;
-  int32_t chunk_edges;
-  int32_t pad;
-  int32_t reserved;
-  int64_t n_slots;             /* edge slots including padding */
-  const int32_t* tiles;        /* [n_tiles][4]: panel, first chunk, end chunk, group */
-  const int32_t* chunks;       /* [n_chunks][8]: first slot, edges, first row, rows,
-                                  first row offset, flags (1: first row continues the
-                                  previous chunk's last row, 2: last row continues,
-                                  4: last chunk of its (panel, stripe)),
-                                  lane table index, stripe */
-  const uint16_t* row_offsets; /* per chunk rows+1 offsets of each row's first edge */
-  const uint16_t* lane_rows;   /* [n_chunks][512]: chunk-local row of each lane's first
-                                  slot (lane l covers slots l*pad .. l*pad+pad-1) */
-  const int32_t* stripes;      /* [n_stripes+1] first row of each stripe */
+  int32_t n_groups;
+  int32_t waves;               /* wavefronts per workgroup the plan was built for */
+  int32_t reserved[3];
+  int64_t n_slots;             /* edge slots including padding and the tail padding */
+  const int32_t* tiles;        /* [n_tiles][4]: panel, first row, end row, tile index */
+  const int32_t* wave_groups;  /* [n_tiles*waves + 1]: wave w of tile t owns groups
+                                  wave_groups[t*waves+w] .. wave_groups[t*waves+w+1]-1 */
+  const int32_t* groups;       /* [n_groups][4]: first slot, steps, lg | rows << 8,
+                                  first entry in `rows` */
+  const uint16_t* rows;        /* tile-local row (row - tile's first row) of each group row */
   const uint16_t* col;         /* [n_slots] source index minus the panel's first neuron */
   const void* weight;          /* [n_slots] weights in slot order, encoding of the matrix:
                                   F32/F16 values, E4M3 codes, NVFP4 nibbles (two per byte) */
@@ -200,27 +197,28 @@ int ns_plan_row_blocks(const int32_t* rowptr_host, int64_t n_rows, int32_t block
 
 /* Host-side panel planner for a host copy of (rowptr, col).  Panel width is
  * the largest that fits `max_panel_width` neurons, equalised over panels and
- * rounded to a multiple of 4; stripes split rows by edge count; each panel's
- * stripes are dealt to `n_groups` tiles in consecutive runs.  Call once
- * with all output pointers NULL to get the sizes in *plan (n_panels,
- * n_stripes, n_tiles, n_chunks, n_slots, chunk_edges, pad, panel_width) and
- * *n_row_offsets, then again with arrays of those sizes:
- * tiles int32[4*n_tiles], chunks int32[8*n_chunks], row_offsets
- * uint16[n_row_offsets], lane_rows uint16[512*n_chunks], stripes int32[n_stripes+1],
- * perm int32[n_slots]
- * (-1 for padding), col uint16[n_slots].  Pointer fields of *plan are not
- * touched. */
+ * rounded to a multiple of 4.  Each panel's rows are cut into about
+ * `tiles_per_panel` tiles of equal cost (segment edges + 1 per row, at most
+ * 65536 rows each).  A row whose segment has L edges gets the smallest
+ * power-of-two lane count that leaves each lane at most `lane_target` edges
+ * (at most 64).  Groups go to the `waves` wavefronts of their tile longest
+ * first onto the least-loaded one.  Call once with all output pointers NULL to
+ * get the sizes in *plan (n_panels, panel_width, n_tiles, n_groups, n_slots,
+ * waves) and *n_row_entries, then again with arrays of those sizes: tiles
+ * int32[4*n_tiles], wave_groups int32[n_tiles*waves+1], groups
+ * int32[4*n_groups], rows uint16[n_row_entries], perm int32[n_slots] (-1 for
+ * padding), col uint16[n_slots].  Pointer fields of *plan are not touched. */
 int ns_plan_panels(const int32_t* rowptr_host, const int32_t* col_host, int64_t n_rows,
-                   int32_t max_panel_width, int32_t n_stripes, int32_t n_groups,
-                   int32_t chunk_edges, int32_t pad,
-                   ns_panel_plan* plan, int64_t* n_row_offsets, int32_t* tiles, int32_t* chunks,
-                   uint16_t* row_offsets, uint16_t* lane_rows, int32_t* stripes, int32_t* perm,
-                   uint16_t* col);
+                   int32_t max_panel_width, int32_t tiles_per_panel, int32_t waves,
+                   int32_t lane_target, ns_panel_plan* plan, int64_t* n_row_entries,
+                   int32_t* tiles, int32_t* wave_groups, int32_t* groups, uint16_t* rows,
+                   int32_t* perm, uint16_t* col);
 
 /* Panel geometry the tick kernels use for batch width `batch` (1 or 2):
- * largest panel width, chunk edges and padding (any NULL output is skipped). */
-int ns_panel_geometry(int64_t batch, int32_t* max_panel_width, int32_t* chunk_edges,
-                      int32_t* pad);
+ * largest panel width and the wavefronts per workgroup (NULL outputs are
+ * skipped). */
+int ns_panel_geometry(int64_t batch, int32_t* max_panel_width, int32_t* waves);
+
 
 /* Fused matrix tick.  Replaces dendritic_step
  * (reference: csrc/bindings.cpp:3-7,137-142; csrc/compartmental.cu:176-236),

@@ -17,10 +17,13 @@ namespace ns {
 constexpr int kThreads = 256;   // 4 wavefronts of 64 lanes
 constexpr int kMaxRows = 256;   // rows per row block (one lane per row at most density)
 
-// Column-panel kernels (batch widths 1 and 2): 512 lanes; a chunk holds at most
-// 511 rows so its rows+1 offsets fit one per lane.
-constexpr int kPanelThreads = 512;
-constexpr int kPanelMaxRows = kPanelThreads - 1;
+// Column-panel kernel (batch widths 1 and 2): 16 wavefronts per workgroup
+// stream their own runs of 64-lane steps; a slot stream ends with
+// kPanelTailSlots padding slots so prefetches may run past a stream's end.
+constexpr int kPanelWaves = 16;
+constexpr int kPanelThreads = kPanelWaves * 64;
+constexpr int kPanelMaxPrefetch = 16;                  // steps per register block, at most
+constexpr int kPanelTailSlots = 2 * kPanelMaxPrefetch * 64;
 
 struct Plane {
   const float* data;

@@ -3,22 +3,23 @@
 // The row-block tick gathers s[col] from L2 for every edge; each 4-byte
 // gather moves a whole cache line into the CU, so at 25M edges the gather
 // traffic, not HBM, bounds the tick.  Here the columns are cut into panels
-// whose slice of s fits in LDS and the CSR is re-laid out (once per graph) so
-// that tile (panel p, row stripe s) holds the stripe's edges whose source lies
-// in panel p, in row order, with 16-bit panel-local source indices:
+// whose slice of s fits in LDS, and the CSR is re-laid out once per graph
+// (ns_plan_panels) as sliced rows:
 //
-//  * one workgroup per tile (a panel and a run of stripes) stages its panel of
-//    s in LDS, then streams the tile's chunks (512 lanes x `pad` edge slots,
-//    16-byte loads; the next chunk's slots and the header after it are in
-//    flight while the current chunk is reduced; two barriers per chunk);
-//  * each lane decodes its slots, gathers s from LDS, and sums its products
-//    per row segment in registers; a row-parallel pass adds the pieces of
-//    rows that span lanes in lane order (deterministic, no atomics);
-//  * with one panel the lane that finishes a row applies the neuron update;
-//    with several, per-panel partial sums go to a workspace and a second,
-//    fully parallel kernel adds them in panel order and applies the update
-//    (stream order publishes the partials; an in-kernel hand-off would need
-//    agent-scope fences, which write back and invalidate L2 on this part).
+//  * a workgroup (16 wavefronts) owns one tile: one panel and a range of
+//    destination rows.  It stages the panel's slice of s in LDS, plus one zero
+//    that padding slots point at;
+//  * the tile's rows are grouped by segment length; a group gives each row
+//    2^lg lanes, and lane j of a row accumulates the row's edges j, j+2^lg, ...
+//    in one float32 FMA chain, so the inner loop has no row boundaries;
+//  * each wavefront owns a run of consecutive groups whose slots are one
+//    contiguous stream of 64-lane steps (16-bit panel-local source index plus
+//    the weight in its encoding).  The stream is read in register blocks of
+//    D steps, the next block in flight while the current one is consumed;
+//  * at a group's end the row's lanes are added by an xor butterfly and one
+//    lane per row applies the neuron update (one panel) or stores the panel's
+//    partial sum; a second kernel adds the partials in panel order and
+//    applies the update (several panels).
 //
 // Results are bitwise repeatable and identical across weight encodings that
 // decode to the same float32 values.
@@ -31,23 +32,20 @@
 
 namespace ns {
 
-template <int BT>
-struct PanelCfg;
-template <>
-struct PanelCfg<1> { static constexpr int pad = 16; };
-template <>
-struct PanelCfg<2> { static constexpr int pad = 8; };
-
-template <int BT>
-constexpr int panel_chunk() { return kPanelThreads * PanelCfg<BT>::pad; }
-
-// LDS left for the panel after the per-chunk scratch (row offsets, segment
-// sums, double-buffered), in floats, rounded to whole 4-neuron groups.
+// Neurons of one panel that fit in LDS next to the sentinel zero, in whole
+// 4-neuron groups.
 template <int BT>
 constexpr int panel_capacity_neurons() {
-  constexpr int scratch = 2 * (kPanelThreads * 4 + 3 * BT * kPanelThreads * 4) + 512;
-  return ((163840 - scratch) / 4 / BT) & ~3;
+  return ((163840 - 64) / (4 * BT) - 1) & ~3;
 }
+
+// Steps per register block: enough 64-lane loads in flight per wavefront
+// to cover HBM latency with 16 wavefronts per compute unit.
+template <int FMT>
+constexpr int block_steps() {
+  return FMT == NS_WEIGHT_F32 ? 8 : 12;
+}
+static_assert(block_steps<NS_WEIGHT_F16>() <= kPanelMaxPrefetch, "tail padding too short");
 
 struct PanelArgs {
   int64_t N, B;
@@ -55,10 +53,9 @@ struct PanelArgs {
   Params p;
   int32_t width, n_panels;
   const int32_t* tiles;
-  const int32_t* chunks;
-  const uint16_t* row_offsets;
-  const uint16_t* lane_rows;
-  const int32_t* stripes;
+  const int32_t* wave_groups;
+  const int32_t* groups;
+  const uint16_t* rows;
   const uint16_t* col;
   const void* weight;
   const uint8_t* slot_scales;
@@ -69,65 +66,44 @@ struct PanelArgs {
 };
 
 typedef float v4f __attribute__((ext_vector_type(4)));
-typedef uint32_t v4u __attribute__((ext_vector_type(4)));
-typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef const int32_t __attribute__((address_space(4)))* const_i32_ptr;
 
-// One lane's raw slots: PAD 16-bit columns and PAD weights in the matrix encoding.
-template <int PAD, int FMT>
-struct Raw {
-  static constexpr int kColWords = PAD / 2;                       // uint32 words of columns
-  static constexpr int kWeightWords = FMT == NS_WEIGHT_F32 ? PAD
-                                      : FMT == NS_WEIGHT_F16 ? PAD / 2
-                                      : FMT == NS_WEIGHT_E4M3 ? PAD / 4
-                                                              : PAD / 8;
-  static constexpr int kScaleWords = FMT == NS_WEIGHT_NVFP4 ? PAD / 4 : 0;
-  uint32_t col[kColWords];
-  uint32_t w[kWeightWords];
-  uint32_t sc[kScaleWords > 0 ? kScaleWords : 1];
+// One lane's raw slot: source index, weight bits (F32/F16/E4M3 code, or the
+// NVFP4 byte holding its nibble) and, for NVFP4, the block-scale code.
+struct Slot {
+  uint32_t c, w, sc;
 };
 
-template <int WORDS>
-__device__ __forceinline__ void load_words(const void* base, int64_t byte_offset, uint32_t* out) {
-  const char* p = static_cast<const char*>(base) + byte_offset;
-  if constexpr (WORDS % 4 == 0) {
-#pragma unroll
-    for (int i = 0; i < WORDS / 4; ++i) {
-      const v4u v = *reinterpret_cast<const v4u*>(p + 16 * i);
-      out[4 * i] = v.x; out[4 * i + 1] = v.y; out[4 * i + 2] = v.z; out[4 * i + 3] = v.w;
-    }
-  } else if constexpr (WORDS == 2) {
-    const v2u v = *reinterpret_cast<const v2u*>(p);
-    out[0] = v.x; out[1] = v.y;
-  } else {
-#pragma unroll
-    for (int i = 0; i < WORDS; ++i) out[i] = reinterpret_cast<const uint32_t*>(p)[i];
-  }
-}
-
-template <int PAD, int FMT>
-__device__ __forceinline__ void load_raw(const PanelArgs& A, int64_t slot, Raw<PAD, FMT>& r) {
-  using R = Raw<PAD, FMT>;
-  load_words<R::kColWords>(A.col, slot * 2, r.col);
-  constexpr int bytes_per_slot_x8 = FMT == NS_WEIGHT_F32 ? 32 : FMT == NS_WEIGHT_F16 ? 16
-                                    : FMT == NS_WEIGHT_E4M3 ? 8 : 4;
-  load_words<R::kWeightWords>(A.weight, slot * bytes_per_slot_x8 / 8, r.w);
-  if constexpr (FMT == NS_WEIGHT_NVFP4) load_words<R::kScaleWords>(A.slot_scales, slot, r.sc);
-}
-
 template <int FMT>
-__device__ __forceinline__ float decode_slot(const uint32_t* w, const uint32_t* sc, int k,
-                                             float gscale) {
+__device__ __forceinline__ Slot load_slot(const PanelArgs& A, int64_t q) {
+  Slot x;
+  x.c = A.col[q];
   if constexpr (FMT == NS_WEIGHT_F32) {
-    return __builtin_bit_cast(float, w[k]);
+    x.w = static_cast<const uint32_t*>(A.weight)[q];
   } else if constexpr (FMT == NS_WEIGHT_F16) {
-    const uint16_t h = static_cast<uint16_t>(w[k >> 1] >> (16 * (k & 1)));
-    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+    x.w = static_cast<const uint16_t*>(A.weight)[q];
   } else if constexpr (FMT == NS_WEIGHT_E4M3) {
-    return e4m3_to_float((w[k >> 2] >> (8 * (k & 3))) & 0xFFu) * gscale;
+    x.w = static_cast<const uint8_t*>(A.weight)[q];
   } else {
-    const uint32_t nibble = (w[k >> 3] >> (4 * (k & 7))) & 15u;
-    const float bs = e4m3_to_float((sc[k >> 2] >> (8 * (k & 3))) & 0xFFu) * gscale;
-    return nvfp4_weight(nibble, bs);
+    x.w = static_cast<const uint8_t*>(A.weight)[q >> 1];
+  }
+  x.sc = FMT == NS_WEIGHT_NVFP4 ? A.slot_scales[q] : 0u;
+  return x;
+}
+
+// Slots of a group start at multiples of 64, so a slot's nibble half is the lane's parity.
+template <int FMT>
+__device__ __forceinline__ float decode_slot(const Slot& x, int lane, float gscale) {
+  if constexpr (FMT == NS_WEIGHT_F32) {
+    return __builtin_bit_cast(float, x.w);
+  } else if constexpr (FMT == NS_WEIGHT_F16) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x.w)));
+  } else if constexpr (FMT == NS_WEIGHT_E4M3) {
+    return e4m3_to_float(x.w) * gscale;
+  } else {
+    const uint32_t nibble = (x.w >> ((lane & 1) * 4)) & 15u;
+    return nvfp4_weight(nibble, e4m3_to_float(x.sc) * gscale);
   }
 }
 
@@ -139,54 +115,41 @@ __device__ __forceinline__ void update(const PanelArgs& A, int64_t n, int64_t b,
   A.oa.put(b, n, x.adaptation);
 }
 
-typedef const int32_t __attribute__((address_space(4)))* const_i32_ptr;
-
-// Chunk header through the constant address space: scalar loads on their own
-// counter, so waiting for a header never waits for the streamed slots.
-struct Header {
-  int slot0, nedge, row0, nrows, off0, flags, lanes;
-};
-
-__device__ __forceinline__ Header load_header(const PanelArgs& A, int c) {
-  const_i32_ptr h = (const_i32_ptr)(A.chunks + 8 * static_cast<int64_t>(c));
-  return Header{h[0], h[1], h[2], h[3], h[4], h[5], h[6]};
-}
-
 template <int BT, int FMT>
 __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) {
-  constexpr int PAD = PanelCfg<BT>::pad;
+  constexpr int D = block_steps<FMT>();
   constexpr int CAP = panel_capacity_neurons<BT>();
-  __shared__ __attribute__((aligned(16))) float lds_s[CAP * BT];
-  __shared__ int32_t offs[2][kPanelThreads];
-  __shared__ float rowsum[2][BT][kPanelThreads];
-  __shared__ float head[2][BT][kPanelThreads];
-  __shared__ float tail[2][BT][kPanelThreads];
-  __shared__ float carry[BT];
+  __shared__ __attribute__((aligned(16))) float lds_s[(CAP + 1) * BT];
 
   const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const_i32_ptr tile = (const_i32_ptr)(A.tiles + 4 * static_cast<int64_t>(blockIdx.x));
-  const int panel = tile[0], c_begin = tile[1], c_end = tile[2];
+  const int panel = tile[0], row0 = tile[1];
   const int64_t base = static_cast<int64_t>(panel) * A.width;
   const int len = static_cast<int>(min<int64_t>(A.width, A.N - base));
   const float gscale = (FMT == NS_WEIGHT_E4M3 || FMT == NS_WEIGHT_NVFP4) ? *A.gscale : 1.0f;
 
-  // Pipeline: slots, row offset and lane row of chunk c+1 are in flight while
-  // chunk c is reduced; headers run one chunk further ahead.
-  Raw<PAD, FMT> next;
-  int next_off = 0, next_lane_row = 0;
-  Header h_next{}, h_after{};
-  auto fetch = [&](const Header& h) {
-    if (tid * PAD < h.nedge) load_raw<PAD, FMT>(A, h.slot0 + tid * PAD, next);
-    next_off = tid <= h.nrows ? A.row_offsets[h.off0 + tid] : 0;
-    next_lane_row = A.lane_rows[static_cast<int64_t>(h.lanes) * kPanelThreads + tid];
-  };
-  if (c_begin < c_end) {
-    h_next = load_header(A, c_begin);
-    fetch(h_next);
-    if (c_begin + 1 < c_end) h_after = load_header(A, c_begin + 1);
+  // This wavefront's stream: groups [g, g_end), slots [first, first + 64*total).
+  const_i32_ptr wg = (const_i32_ptr)(A.wave_groups + static_cast<int64_t>(blockIdx.x) * kPanelWaves + wave);
+  int g = wg[0];
+  const int g_end = wg[1];
+  int64_t first = 0;
+  int total = 0;
+  if (g < g_end) {
+    const_i32_ptr head = (const_i32_ptr)(A.groups + 4 * static_cast<int64_t>(g));
+    const_i32_ptr last = (const_i32_ptr)(A.groups + 4 * static_cast<int64_t>(g_end - 1));
+    first = head[0];
+    total = (last[0] - head[0]) / 64 + last[1];
   }
 
-  // Stage this panel's slice of s (neuron-major, BT columns per neuron), 8 loads deep.
+  // First register block in flight while the panel is staged.
+  Slot cur[D], nxt[D];
+#pragma unroll
+  for (int k = 0; k < D; ++k) cur[k] = load_slot<FMT>(A, first + 64 * k + lane);
+
+  // Stage this panel's slice of s (neuron-major, BT columns per neuron), 8 loads deep,
+  // and the zero that padding slots read.
   if (A.s_vec) {
     const v4f* src = reinterpret_cast<const v4f*>(A.s.data + base * BT);
     v4f* dst = reinterpret_cast<v4f*>(lds_s);
@@ -206,105 +169,75 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
       lds_s[i] = A.s.data[j * A.s.sb + (base + nn) * A.s.sn];
     }
   }
-  if (tid < BT) carry[tid] = 0.0f;
-  if (tid <= h_next.nrows) offs[0][tid] = next_off;
+  if (tid < BT) lds_s[A.width * BT + tid] = 0.0f;
   __syncthreads();
 
-  for (int c = c_begin; c < c_end; ++c) {
-    const int buf = (c - c_begin) & 1;
-    const Raw<PAD, FMT> raw = next;
-    const Header h = h_next;
-    const int lane_row = next_lane_row;
-    if (c + 1 < c_end) {
-      h_next = h_after;
-      fetch(h_next);
-      if (c + 2 < c_end) h_after = load_header(A, c + 2);
+  // Group state (wave-uniform).
+  int left = 0, lg = 0, nrows = 0, rowtab = 0;
+  float acc[BT];
+#pragma unroll
+  for (int j = 0; j < BT; ++j) acc[j] = 0.0f;
+  auto open = [&]() {
+    const_i32_ptr desc = (const_i32_ptr)(A.groups + 4 * static_cast<int64_t>(g));
+    left = desc[1];
+    lg = desc[2] & 255;
+    nrows = desc[2] >> 8;
+    rowtab = desc[3];
+  };
+  auto close = [&]() {
+    const int lanes = 1 << lg;
+    float t[BT];
+#pragma unroll
+    for (int j = 0; j < BT; ++j) {
+      t[j] = acc[j];
+      for (int off = 1; off < lanes; off <<= 1) t[j] += __shfl_xor(t[j], off, 64);
+      acc[j] = 0.0f;
     }
-
-    // Lane phase: products of this lane's slots (all LDS gathers in flight),
-    // then sums per row segment; pieces of lane-spanning rows go to LDS.
-    const int first = tid * PAD;
-    const int count = h.nedge - first < PAD ? h.nedge - first : PAD;
-    float prod[PAD][BT];
-#pragma unroll
-    for (int k = 0; k < PAD; ++k) {
-      const uint32_t word = raw.col[k >> 1];
-      const int local = static_cast<int>((word >> (16 * (k & 1))) & 0xFFFFu);
-      const float w = decode_slot<FMT>(raw.w, raw.sc, k, gscale);
-#pragma unroll
-      for (int j = 0; j < BT; ++j) prod[k][j] = k < count ? w * lds_s[local * BT + j] : 0.0f;
-    }
-    if (count > 0) {
-      int r = lane_row;
-      int row_end = offs[buf][r + 1];
-      bool started_here = offs[buf][r] == first;
-      float acc[BT];
-#pragma unroll
-      for (int j = 0; j < BT; ++j) acc[j] = 0.0f;
-      auto store = [&](bool continues) {
-#pragma unroll
-        for (int j = 0; j < BT; ++j) {
-          if (!started_here) head[buf][j][tid] = acc[j];
-          else if (continues) tail[buf][j][tid] = acc[j];
-          else rowsum[buf][j][r] = acc[j];
-        }
-      };
-#pragma unroll
-      for (int k = 0; k < PAD; ++k) {
-        if (k < count) {
-          while (first + k >= row_end) {   // close row r, skip rows with no edges here
-            store(false);
-            started_here = true;
-            ++r;
-            row_end = offs[buf][r + 1];
-#pragma unroll
-            for (int j = 0; j < BT; ++j) acc[j] = 0.0f;
-          }
-#pragma unroll
-          for (int j = 0; j < BT; ++j) acc[j] += prod[k][j];
-        }
-      }
-      store(first + count < row_end);
-    }
-    __syncthreads();
-
-    // Row phase: lane i < nrows finishes row i of the chunk; the next chunk's
-    // row offsets go to the other buffer.
-    if (tid < h.nrows) {
-      const int lo = offs[buf][tid], hi = offs[buf][tid + 1];
-      float total[BT];
-#pragma unroll
-      for (int j = 0; j < BT; ++j) total[j] = 0.0f;
-      if (lo < hi) {
-        const int t0 = lo / PAD, t1 = (hi - 1) / PAD;
-        if (t0 == t1) {
-#pragma unroll
-          for (int j = 0; j < BT; ++j) total[j] = rowsum[buf][j][tid];
-        } else {
-#pragma unroll
-          for (int j = 0; j < BT; ++j) {
-            float sum = tail[buf][j][t0];
-            for (int t = t0 + 1; t <= t1; ++t) sum += head[buf][j][t];
-            total[j] = sum;
-          }
-        }
-      }
-      const bool continued = tid == 0 && (h.flags & 1);
-      const bool continues = tid == h.nrows - 1 && (h.flags & 2);
+    const int k = lane >> lg;
+    if ((lane & (lanes - 1)) == 0 && k < nrows) {
+      const int64_t row = row0 + static_cast<int64_t>(A.rows[rowtab + k]);
 #pragma unroll
       for (int j = 0; j < BT; ++j) {
-        const float value = continued ? carry[j] + total[j] : total[j];
-        if (continues) {
-          carry[j] = value;
-        } else if (j < A.B) {
-          const int64_t row = h.row0 + tid;
-          if (A.n_panels == 1) update(A, row, j, value);
-          else A.partials[(static_cast<int64_t>(panel) * A.N + row) * A.B + j] = value;
+        if (j >= A.B) break;
+        if (A.n_panels == 1) update(A, row, j, t[j]);
+        else A.partials[(static_cast<int64_t>(panel) * A.N + row) * A.B + j] = t[j];
+      }
+    }
+    ++g;
+  };
+  // Groups with no steps (rows with no edges in this panel) close at once.
+  auto skip_empty = [&]() {
+    while (g < g_end) {
+      open();
+      if (left > 0) break;
+      close();
+    }
+  };
+  skip_empty();
+
+  for (int b = 0; b * D < total; ++b) {
+    const int64_t ahead = first + static_cast<int64_t>(b + 1) * D * 64 + lane;
+#pragma unroll
+    for (int k = 0; k < D; ++k) nxt[k] = load_slot<FMT>(A, ahead + 64 * k);
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+      if (b * D + i < total) {
+        const float w = decode_slot<FMT>(cur[i], lane, gscale);
+        if constexpr (BT == 1) {
+          acc[0] = __builtin_fmaf(w, lds_s[cur[i].c], acc[0]);
+        } else {
+          const v2f sv = *reinterpret_cast<const v2f*>(lds_s + 2 * cur[i].c);
+          acc[0] = __builtin_fmaf(w, sv.x, acc[0]);
+          acc[1] = __builtin_fmaf(w, sv.y, acc[1]);
+        }
+        if (--left == 0) {
+          close();
+          skip_empty();
         }
       }
     }
-    if (c + 1 < c_end && tid <= h_next.nrows) offs[buf ^ 1][tid] = next_off;
-    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < D; ++k) cur[k] = nxt[k];
   }
 }
 
@@ -337,44 +270,39 @@ hipError_t launch_panels(const PanelArgs& A, int fmt, int n_tiles, hipStream_t s
   return hipGetLastError();
 }
 
-int panel_geometry(int64_t batch, int32_t* width, int32_t* chunk, int32_t* pad) {
-  if (batch == 1) {
-    *width = panel_capacity_neurons<1>(); *chunk = panel_chunk<1>(); *pad = PanelCfg<1>::pad;
-  } else if (batch == 2) {
-    *width = panel_capacity_neurons<2>(); *chunk = panel_chunk<2>(); *pad = PanelCfg<2>::pad;
-  } else {
-    return fail("column panels support batch widths 1 and 2, not %lld", (long long)batch);
-  }
+int panel_geometry(int64_t batch, int32_t* width, int32_t* waves) {
+  if (batch == 1) *width = panel_capacity_neurons<1>();
+  else if (batch == 2) *width = panel_capacity_neurons<2>();
+  else return fail("column panels support batch widths 1 and 2, not %lld", (long long)batch);
+  *waves = kPanelWaves;
   return NS_OK;
 }
 
 // Validation and launch of the panel path for ns_dendritic_step.
 int panel_step(const ns_step_args& a, hipStream_t stream) {
   const ns_panel_plan& pl = *a.panels;
-  int32_t cap = 0, chunk = 0, pad = 0;
-  if (int rc = panel_geometry(a.batch, &cap, &chunk, &pad)) return rc;
-  if (pl.chunk_edges != chunk || pl.pad != pad)
-    return fail("panel plan was built for chunks of %d x %d, batch %lld needs %d x %d",
-                pl.chunk_edges / (pl.pad ? pl.pad : 1), pl.pad, (long long)a.batch,
-                chunk / pad, pad);
+  int32_t cap = 0, waves = 0;
+  if (int rc = panel_geometry(a.batch, &cap, &waves)) return rc;
+  if (pl.waves != waves)
+    return fail("panel plan was built for %d wavefronts per workgroup, the kernel runs %d",
+                pl.waves, waves);
   if (pl.panel_width < 4 || pl.panel_width > cap || pl.panel_width % 4)
     return fail("panel width %d is not a multiple of 4 in [4, %d]", pl.panel_width, cap);
   if (pl.n_panels < 1 || static_cast<int64_t>(pl.n_panels) * pl.panel_width < a.n_neurons ||
       static_cast<int64_t>(pl.n_panels - 1) * pl.panel_width >= a.n_neurons)
     return fail("%d panels of width %d do not cover N=%lld", pl.n_panels, pl.panel_width,
                 (long long)a.n_neurons);
-  if (pl.n_tiles < pl.n_panels || pl.n_stripes < 1)
-    return fail("panel plan needs at least one tile per panel and one stripe");
-  if (!pl.tiles || !pl.chunks || !pl.row_offsets || !pl.lane_rows || !pl.stripes)
+  if (pl.n_tiles < pl.n_panels || pl.n_groups < 0)
+    return fail("panel plan needs at least one tile per panel");
+  if (pl.n_slots < kPanelTailSlots) return fail("panel plan lacks its tail padding");
+  if (!pl.tiles || !pl.wave_groups || !pl.groups || !pl.rows || !pl.col || !pl.weight)
     return fail("panel plan tables are required");
-  if (pl.n_slots > 0 && (!pl.col || !pl.weight)) return fail("panel columns and weights are required");
-  if (a.matrix.format == NS_WEIGHT_NVFP4 && pl.n_slots > 0 && !pl.slot_scales)
+  if (a.matrix.format == NS_WEIGHT_NVFP4 && !pl.slot_scales)
     return fail("NVFP4 panels require per-slot block scales");
   if (pl.n_panels > 1 && !pl.partials) return fail("several panels need the partials workspace");
-  const uintptr_t need = a.matrix.format == NS_WEIGHT_NVFP4 ? 8 : 16;
-  if (reinterpret_cast<uintptr_t>(pl.col) % 16 || reinterpret_cast<uintptr_t>(pl.weight) % need ||
-      reinterpret_cast<uintptr_t>(pl.slot_scales) % 16)
-    return fail("panel arrays must be 16-byte aligned");
+  const uintptr_t need = a.matrix.format == NS_WEIGHT_F32 ? 4 : a.matrix.format == NS_WEIGHT_F16 ? 2 : 1;
+  if (reinterpret_cast<uintptr_t>(pl.col) % 2 || reinterpret_cast<uintptr_t>(pl.weight) % need)
+    return fail("panel arrays are misaligned");
   if (pl.partials) {
     const Extent part = extent_of(pl.partials, 1, 1, 1, int64_t{pl.n_panels} * a.n_neurons * a.batch);
     const Extent outs[3] = {extent(a.out_state, a.batch, a.n_neurons),
@@ -390,8 +318,7 @@ int panel_step(const ns_step_args& a, hipStream_t stream) {
   A.u = plane(a.drive); A.v = plane(a.dendritic_drive);
   for (int i = 0; i < 6; ++i) A.p.v[i] = Vec{a.params[i].data, a.params[i].stride};
   A.width = pl.panel_width; A.n_panels = pl.n_panels;
-  A.tiles = pl.tiles; A.chunks = pl.chunks; A.row_offsets = pl.row_offsets;
-  A.lane_rows = pl.lane_rows; A.stripes = pl.stripes;
+  A.tiles = pl.tiles; A.wave_groups = pl.wave_groups; A.groups = pl.groups; A.rows = pl.rows;
   A.col = pl.col; A.weight = pl.weight; A.slot_scales = pl.slot_scales;
   A.gscale = a.matrix.global_scale;
   A.partials = pl.partials;
@@ -410,13 +337,11 @@ int panel_step(const ns_step_args& a, hipStream_t stream) {
 
 using namespace ns;
 
-extern "C" int ns_panel_geometry(int64_t batch, int32_t* max_panel_width, int32_t* chunk_edges,
-                                 int32_t* pad) {
+extern "C" int ns_panel_geometry(int64_t batch, int32_t* max_panel_width, int32_t* waves) {
   clear_error();
-  int32_t w = 0, c = 0, p = 0;
-  if (int rc = panel_geometry(batch, &w, &c, &p)) return rc;
+  int32_t w = 0, v = 0;
+  if (int rc = panel_geometry(batch, &w, &v)) return rc;
   if (max_panel_width) *max_panel_width = w;
-  if (chunk_edges) *chunk_edges = c;
-  if (pad) *pad = p;
+  if (waves) *waves = v;
   return NS_OK;
 }

@@ -68,86 +68,101 @@ extern "C" int ns_plan_row_blocks(const int32_t* rowptr, int64_t n_rows, int32_t
 
 namespace {
 
-// The whole panel layout in host vectors (built twice: size query, then fill).
+// The sliced layout of one graph, in host vectors (built twice: size query, then fill).
 struct PanelLayout {
-  int32_t panel_width = 0, n_panels = 0, n_stripes = 0;
-  std::vector<int32_t> tiles, chunks, stripes, perm;
-  std::vector<uint16_t> row_offsets, col, lane_rows;
+  int32_t panel_width = 0, n_panels = 0;
+  std::vector<int32_t> tiles, wave_groups, groups, perm;
+  std::vector<uint16_t> rows, col;
 };
 
-// Appends the chunks of one (panel, stripe) pair: the stripe's rows in order,
-// each with its edges whose source lies in the panel.  A row longer than a
-// chunk continues in the next chunk (flags 1/2); the stripe's last chunk gets
-// flag 4.  Every chunk is padded with perm = -1 slots to whole lanes.
-void append_chunks(PanelLayout& out, const int32_t* rowptr, const int32_t* col,
-                   const std::vector<int32_t>& order, const std::vector<int32_t>& bucket,
-                   int32_t P, int64_t width, int32_t panel, int32_t stripe, int64_t r0, int64_t r1,
-                   int32_t chunk_edges, int32_t pad) {
-  int64_t c_edges = 0, c_rows = 0, c_flags = 0, c_first_row = r0, c_slot = 0, c_off = 0;
-  auto open_chunk = [&](int64_t first_row, int64_t flags) {
-    c_edges = 0; c_rows = 0; c_flags = flags; c_first_row = first_row;
-    c_slot = static_cast<int64_t>(out.perm.size());
-    c_off = static_cast<int64_t>(out.row_offsets.size());
-    out.row_offsets.push_back(0);
-  };
-  auto close_chunk = [&](bool last_row_continues, bool stripe_done) {
-    if (last_row_continues) c_flags |= 2;
-    if (stripe_done) c_flags |= 4;
-    const int64_t lanes_at = static_cast<int64_t>(out.lane_rows.size());
-    const int32_t rec[8] = {static_cast<int32_t>(c_slot), static_cast<int32_t>(c_edges),
-                            static_cast<int32_t>(c_first_row), static_cast<int32_t>(c_rows),
-                            static_cast<int32_t>(c_off), static_cast<int32_t>(c_flags),
-                            static_cast<int32_t>(lanes_at / kPanelThreads), stripe};
-    out.chunks.insert(out.chunks.end(), rec, rec + 8);
-    // Local row holding each lane's first slot (c_rows past the edges).
-    const uint16_t* offs = &out.row_offsets[c_off];
-    int64_t row = 0;
-    for (int64_t lane = 0; lane < kPanelThreads; ++lane) {
-      const int64_t first = lane * pad;
-      if (first >= c_edges) {
-        out.lane_rows.push_back(static_cast<uint16_t>(c_rows));
-        continue;
-      }
-      while (offs[row + 1] <= first) ++row;
-      out.lane_rows.push_back(static_cast<uint16_t>(row));
-    }
-    while ((static_cast<int64_t>(out.perm.size()) - c_slot) % pad) {   // whole lanes
-      out.perm.push_back(-1);
-      out.col.push_back(0);
-    }
-  };
-  open_chunk(r0, 0);
-  for (int64_t r = r0; r < r1; ++r) {
+int32_t log2_lanes(int64_t len, int32_t lane_target) {
+  // Lanes per row: the smallest power of two that leaves each lane at most
+  // lane_target edges, capped at a whole wavefront.
+  int32_t lg = 0;
+  while (lg < 6 && len > (int64_t{lane_target} << lg)) ++lg;
+  return lg;
+}
+
+struct Group {
+  int32_t lg, nrows, steps, first;   // first: index of its first row in the sorted order
+};
+
+// Lays out tile (panel p, rows [r0, r1)): rows sorted by segment length
+// (descending, ties by row), cut into groups of 64 >> lg rows sharing one
+// lanes-per-row width, groups dealt to the waves longest-first onto the
+// least-loaded wave, then every wave's groups emitted back to back.
+void append_tile(PanelLayout& out, const int32_t* rowptr, const int32_t* col,
+                 const std::vector<int32_t>& order, const std::vector<int32_t>& bucket,
+                 int32_t P, int64_t width, int32_t p, int64_t r0, int64_t r1, int32_t waves,
+                 int32_t lane_target) {
+  const int64_t nr = r1 - r0;
+  auto seg_len = [&](int64_t r) -> int64_t {
     const int32_t* b = &bucket[r * (P + 1)];
-    int64_t lo = rowptr[r] + b[panel], hi = rowptr[r] + b[panel + 1];
-    bool continued = false;
-    while (true) {
-      if (c_rows == kPanelMaxRows || (c_rows > 0 && c_edges + (hi - lo) > chunk_edges)) {
-        close_chunk(false, false);
-        open_chunk(r, 0);
+    return b[p + 1] - b[p];
+  };
+  std::vector<int32_t> sorted(nr);
+  for (int64_t i = 0; i < nr; ++i) sorted[i] = static_cast<int32_t>(r0 + i);
+  std::stable_sort(sorted.begin(), sorted.end(),
+                   [&](int32_t x, int32_t y) { return seg_len(x) > seg_len(y); });
+  std::vector<Group> groups;
+  for (int64_t i = 0; i < nr;) {
+    const int64_t len = seg_len(sorted[i]);
+    const int32_t lg = log2_lanes(len, lane_target);
+    const int64_t cap = 64 >> lg;
+    int64_t n = 1;
+    while (n < cap && i + n < nr && log2_lanes(seg_len(sorted[i + n]), lane_target) == lg) ++n;
+    const int64_t lanes = int64_t{1} << lg;
+    groups.push_back(Group{lg, static_cast<int32_t>(n),
+                           static_cast<int32_t>((len + lanes - 1) / lanes),
+                           static_cast<int32_t>(i)});
+    i += n;
+  }
+  // Longest-processing-time assignment (steps + 1 per group for its reduction).
+  std::vector<int32_t> by_cost(groups.size());
+  for (size_t g = 0; g < groups.size(); ++g) by_cost[g] = static_cast<int32_t>(g);
+  std::stable_sort(by_cost.begin(), by_cost.end(),
+                   [&](int32_t x, int32_t y) { return groups[x].steps > groups[y].steps; });
+  std::vector<int64_t> load(waves, 0);
+  std::vector<std::vector<int32_t>> mine(waves);
+  for (int32_t g : by_cost) {
+    const int32_t w = static_cast<int32_t>(std::min_element(load.begin(), load.end()) - load.begin());
+    load[w] += groups[g].steps + 1;
+    mine[w].push_back(g);
+  }
+  const int32_t tile_index = static_cast<int32_t>(out.tiles.size() / 4);
+  const int32_t rec[4] = {p, static_cast<int32_t>(r0), static_cast<int32_t>(r1), tile_index};
+  out.tiles.insert(out.tiles.end(), rec, rec + 4);
+  for (int32_t w = 0; w < waves; ++w) {
+    out.wave_groups.push_back(static_cast<int32_t>(out.groups.size() / 4));
+    for (int32_t g : mine[w]) {
+      const Group& grp = groups[g];
+      const int32_t lanes = 1 << grp.lg;
+      const int32_t rec_g[4] = {static_cast<int32_t>(out.perm.size()), grp.steps,
+                                grp.lg | (grp.nrows << 8), static_cast<int32_t>(out.rows.size())};
+      out.groups.insert(out.groups.end(), rec_g, rec_g + 4);
+      for (int32_t k = 0; k < grp.nrows; ++k)
+        out.rows.push_back(static_cast<uint16_t>(sorted[grp.first + k] - r0));
+      // Step-major slots: lane l = (row k, part j) takes the row's edges j, j+lanes, ...
+      for (int32_t step = 0; step < grp.steps; ++step) {
+        for (int32_t lane = 0; lane < 64; ++lane) {
+          const int32_t k = lane >> grp.lg, j = lane & (lanes - 1);
+          int32_t edge = -1;
+          if (k < grp.nrows) {
+            const int64_t r = sorted[grp.first + k];
+            const int64_t idx = int64_t{step} * lanes + j;
+            if (idx < seg_len(r)) edge = order[rowptr[r] + bucket[r * (P + 1) + p] + idx];
+          }
+          out.perm.push_back(edge);
+          out.col.push_back(edge < 0 ? static_cast<uint16_t>(width)
+                                     : static_cast<uint16_t>(col[edge] - p * width));
+        }
       }
-      const int64_t take = std::min<int64_t>(hi - lo, chunk_edges - c_edges);
-      if (continued && c_rows == 0) c_flags |= 1;
-      for (int64_t k = lo; k < lo + take; ++k) {
-        const int32_t e = order[k];
-        out.perm.push_back(e);
-        out.col.push_back(static_cast<uint16_t>(col[e] - panel * width));
-      }
-      c_edges += take;
-      ++c_rows;
-      out.row_offsets.push_back(static_cast<uint16_t>(c_edges));
-      lo += take;
-      if (lo == hi) break;
-      close_chunk(true, false);          // the row continues in a fresh chunk
-      open_chunk(r, 0);
-      continued = true;
     }
   }
-  close_chunk(false, true);
 }
 
 int build_panels(const int32_t* rowptr, const int32_t* col, int64_t n, int32_t max_width,
-                 int32_t want_stripes, int32_t groups_wanted, int32_t chunk_edges, int32_t pad,
+                 int32_t tiles_per_panel, int32_t waves, int32_t lane_target,
                  PanelLayout& out) {
   const int64_t m = rowptr[n];
   max_width &= ~3;                       // panel widths are whole 4-neuron groups
@@ -158,26 +173,8 @@ int build_panels(const int32_t* rowptr, const int32_t* col, int64_t n, int32_t m
   out.n_panels = static_cast<int32_t>((n + width - 1) / width);
   const int32_t P = out.n_panels;
 
-  // Stripes: rows split at equal edge counts (equal row counts when M == 0).
-  const int64_t stripes_wanted = std::max<int64_t>(1, std::min<int64_t>(want_stripes, n));
-  out.stripes.assign(1, 0);
-  for (int64_t k = 1; k < stripes_wanted; ++k) {
-    int64_t row;
-    if (m > 0) {
-      const int64_t target = (m * k) / stripes_wanted;
-      row = std::lower_bound(rowptr, rowptr + n + 1, static_cast<int32_t>(target)) - rowptr;
-    } else {
-      row = (n * k) / stripes_wanted;
-    }
-    if (row > out.stripes.back() && row < n) out.stripes.push_back(static_cast<int32_t>(row));
-  }
-  out.stripes.push_back(static_cast<int32_t>(n));
-  out.n_stripes = static_cast<int32_t>(out.stripes.size() - 1);
-  const int32_t S = out.n_stripes;
-  const int32_t groups = std::max<int32_t>(1, std::min<int32_t>(groups_wanted, S));
-
   // Each row's edges grouped by panel (stable counting sort).
-  std::vector<int32_t> order(m), bucket((n) * (P + 1), 0), fill(P);
+  std::vector<int32_t> order(m), bucket(n * (P + 1), 0), fill(P);
   for (int64_t r = 0; r < n; ++r) {
     int32_t* b = &bucket[r * (P + 1)];
     for (int64_t e = rowptr[r]; e < rowptr[r + 1]; ++e) {
@@ -191,18 +188,39 @@ int build_panels(const int32_t* rowptr, const int32_t* col, int64_t n, int32_t m
       order[rowptr[r] + fill[col[e] / width]++] = static_cast<int32_t>(e);
   }
 
-  // Work item (panel p, group g) walks stripes [g*S/groups, (g+1)*S/groups) of panel p.
+  // Tiles of panel p: consecutive row ranges of about equal cost (segment
+  // edges + 1 per row), at most 65536 rows each (16-bit tile-local rows).
+  const int64_t min_tiles = (n + 65535) / 65536;
+  const int64_t T = std::min<int64_t>(n, std::max<int64_t>(tiles_per_panel, min_tiles));
+  std::vector<int64_t> cost(n + 1);
   for (int32_t p = 0; p < P; ++p) {
-    for (int32_t g = 0; g < groups; ++g) {
-      const int32_t s0 = static_cast<int32_t>((int64_t{g} * S) / groups);
-      const int32_t s1 = static_cast<int32_t>((int64_t{g + 1} * S) / groups);
-      const int32_t first_chunk = static_cast<int32_t>(out.chunks.size() / 8);
-      for (int32_t st = s0; st < s1; ++st)
-        append_chunks(out, rowptr, col, order, bucket, P, width, p, st, out.stripes[st],
-                      out.stripes[st + 1], chunk_edges, pad);
-      const int32_t tile[4] = {p, first_chunk, static_cast<int32_t>(out.chunks.size() / 8), g};
-      out.tiles.insert(out.tiles.end(), tile, tile + 4);
+    cost[0] = 0;
+    for (int64_t r = 0; r < n; ++r)
+      cost[r + 1] = cost[r] + (bucket[r * (P + 1) + p + 1] - bucket[r * (P + 1) + p]) + 1;
+    int64_t r0 = 0;
+    for (int64_t t = 1; t <= T && r0 < n; ++t) {
+      int64_t r1 = n;
+      if (t < T) {
+        const int64_t target = (cost[n] * t) / T;
+        r1 = std::lower_bound(cost.begin(), cost.end(), target) - cost.begin();
+        r1 = std::max<int64_t>(r1, r0 + 1);
+      }
+      r1 = std::min<int64_t>(r1, std::min<int64_t>(n, r0 + 65536));
+      if (t == T) r1 = n;
+      while (r1 - r0 > 65536) {          // only possible on the last tile
+        append_tile(out, rowptr, col, order, bucket, P, width, p, r0, r0 + 65536, waves,
+                    lane_target);
+        r0 += 65536;
+      }
+      append_tile(out, rowptr, col, order, bucket, P, width, p, r0, r1, waves, lane_target);
+      r0 = r1;
     }
+  }
+  out.wave_groups.push_back(static_cast<int32_t>(out.groups.size() / 4));
+  // Trailing padding: prefetches run up to two blocks of steps past a stream's end.
+  for (int64_t k = 0; k < kPanelTailSlots; ++k) {
+    out.perm.push_back(-1);
+    out.col.push_back(static_cast<uint16_t>(width));
   }
   if (static_cast<int64_t>(out.perm.size()) >= (int64_t{1} << 31))
     return fail("panel layout needs 2^31 or more slots");
@@ -212,41 +230,37 @@ int build_panels(const int32_t* rowptr, const int32_t* col, int64_t n, int32_t m
 }  // namespace
 
 extern "C" int ns_plan_panels(const int32_t* rowptr, const int32_t* col, int64_t n_rows,
-                              int32_t max_panel_width, int32_t n_stripes, int32_t n_groups,
-                              int32_t chunk_edges, int32_t pad, ns_panel_plan* plan,
-                              int64_t* n_row_offsets, int32_t* tiles, int32_t* chunks,
-                              uint16_t* row_offsets, uint16_t* lane_rows, int32_t* stripes,
-                              int32_t* perm, uint16_t* col_out) {
+                              int32_t max_panel_width, int32_t tiles_per_panel, int32_t waves,
+                              int32_t lane_target, ns_panel_plan* plan, int64_t* n_row_entries,
+                              int32_t* tiles, int32_t* wave_groups, int32_t* groups,
+                              uint16_t* rows, int32_t* perm, uint16_t* col_out) {
   clear_error();
-  if (!rowptr || !plan || !n_row_offsets) return fail("rowptr, plan and n_row_offsets are required");
+  if (!rowptr || !plan || !n_row_entries) return fail("rowptr, plan and n_row_entries are required");
   if (n_rows <= 0 || n_rows >= (int64_t{1} << 31)) return fail("N must be in [1, 2^31)");
   if (rowptr[0] != 0) return fail("rowptr[0] must be 0");
   for (int64_t r = 0; r < n_rows; ++r)
     if (rowptr[r + 1] < rowptr[r]) return fail("rowptr must be non-decreasing");
   if (rowptr[n_rows] > 0 && !col) return fail("col is required");
-  if (max_panel_width < 4 || max_panel_width > 65536)
-    return fail("max_panel_width must be in [4, 65536]");
-  if (n_stripes < 1 || n_groups < 1) return fail("n_stripes and n_groups must be positive");
-  if (pad < 1 || chunk_edges != pad * kPanelThreads || chunk_edges > 65535)
-    return fail("chunk_edges must be pad * %d and below 65536", kPanelThreads);
+  if (max_panel_width < 4 || max_panel_width > 65532)
+    return fail("max_panel_width must be in [4, 65532]");
+  if (tiles_per_panel < 1) return fail("tiles_per_panel must be positive");
+  if (waves != kPanelWaves) return fail("the panel kernel runs %d wavefronts per workgroup", kPanelWaves);
+  if (lane_target < 1) return fail("lane_target must be positive");
   PanelLayout layout;
-  if (int rc = build_panels(rowptr, col, n_rows, max_panel_width, n_stripes, n_groups,
-                            chunk_edges, pad, layout))
+  if (int rc = build_panels(rowptr, col, n_rows, max_panel_width, tiles_per_panel, waves,
+                            lane_target, layout))
     return rc;
   plan->panel_width = layout.panel_width;
   plan->n_panels = layout.n_panels;
-  plan->n_stripes = layout.n_stripes;
   plan->n_tiles = static_cast<int32_t>(layout.tiles.size() / 4);
-  plan->n_chunks = static_cast<int32_t>(layout.chunks.size() / 8);
-  plan->chunk_edges = chunk_edges;
-  plan->pad = pad;
+  plan->n_groups = static_cast<int32_t>(layout.groups.size() / 4);
+  plan->waves = waves;
   plan->n_slots = static_cast<int64_t>(layout.perm.size());
-  *n_row_offsets = static_cast<int64_t>(layout.row_offsets.size());
+  *n_row_entries = static_cast<int64_t>(layout.rows.size());
   if (tiles) std::copy(layout.tiles.begin(), layout.tiles.end(), tiles);
-  if (chunks) std::copy(layout.chunks.begin(), layout.chunks.end(), chunks);
-  if (row_offsets) std::copy(layout.row_offsets.begin(), layout.row_offsets.end(), row_offsets);
-  if (lane_rows) std::copy(layout.lane_rows.begin(), layout.lane_rows.end(), lane_rows);
-  if (stripes) std::copy(layout.stripes.begin(), layout.stripes.end(), stripes);
+  if (wave_groups) std::copy(layout.wave_groups.begin(), layout.wave_groups.end(), wave_groups);
+  if (groups) std::copy(layout.groups.begin(), layout.groups.end(), groups);
+  if (rows) std::copy(layout.rows.begin(), layout.rows.end(), rows);
   if (perm) std::copy(layout.perm.begin(), layout.perm.end(), perm);
   if (col_out) std::copy(layout.col.begin(), layout.col.end(), col_out);
   return NS_OK;

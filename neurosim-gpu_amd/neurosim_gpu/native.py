@@ -35,7 +35,7 @@ import numpy as np
 import torch
 
 _LIB_NAME = "libneurosim_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 WEIGHT_F32, WEIGHT_F16, WEIGHT_E4M3, WEIGHT_NVFP4 = 0, 1, 2, 3
 _PLAN_CACHE = 64   # row plans kept per extension (one per live topology and batch width)
@@ -70,12 +70,10 @@ class _RowPlan(ctypes.Structure):
 
 class _PanelPlan(ctypes.Structure):
     _fields_ = [("panel_width", ctypes.c_int32), ("n_panels", ctypes.c_int32),
-                ("n_stripes", ctypes.c_int32), ("n_tiles", ctypes.c_int32),
-                ("n_chunks", ctypes.c_int32), ("chunk_edges", ctypes.c_int32),
-                ("pad", ctypes.c_int32), ("reserved", ctypes.c_int32), ("n_slots", _c_i64),
-                ("tiles", _c_ptr), ("chunks", _c_ptr), ("row_offsets", _c_ptr),
-                ("lane_rows", _c_ptr), ("stripes", _c_ptr), ("col", _c_ptr), ("weight", _c_ptr),
-                ("slot_scales", _c_ptr), ("partials", _c_ptr)]
+                ("n_tiles", ctypes.c_int32), ("n_groups", ctypes.c_int32),
+                ("waves", ctypes.c_int32), ("reserved", ctypes.c_int32 * 3), ("n_slots", _c_i64),
+                ("tiles", _c_ptr), ("wave_groups", _c_ptr), ("groups", _c_ptr), ("rows", _c_ptr),
+                ("col", _c_ptr), ("weight", _c_ptr), ("slot_scales", _c_ptr), ("partials", _c_ptr)]
 
 
 class _StepArgs(ctypes.Structure):
@@ -133,12 +131,11 @@ def load_library() -> ctypes.CDLL:
                                        ctypes.POINTER(_c_i64)]
     lib.ns_panel_geometry.restype = ctypes.c_int
     lib.ns_panel_geometry.argtypes = [_c_i64, ctypes.POINTER(ctypes.c_int32),
-                                      ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)]
+                                      ctypes.POINTER(ctypes.c_int32)]
     lib.ns_plan_panels.restype = ctypes.c_int
     lib.ns_plan_panels.argtypes = [_c_ptr, _c_ptr, _c_i64, ctypes.c_int32, ctypes.c_int32,
-                                   ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
-                                   ctypes.POINTER(_PanelPlan),
-                                   ctypes.POINTER(_c_i64)] + [_c_ptr] * 7
+                                   ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(_PanelPlan),
+                                   ctypes.POINTER(_c_i64)] + [_c_ptr] * 6
     for name, kind in (("ns_dendritic_step", _StepArgs), ("ns_dendritic_event", _EventArgs),
                        ("ns_csr_spmm", _SpmmArgs)):
         fn = getattr(lib, name)
@@ -233,42 +230,43 @@ def new_planes(count: int, batch: int, n: int, like: torch.Tensor) -> list[torch
     return [storage[i].T for i in range(count)]
 
 
-def panel_geometry(batch: int) -> tuple[int, int, int]:
-    """(largest panel width, chunk edges, slots per lane) of the panel kernel."""
+def panel_geometry(batch: int) -> tuple[int, int]:
+    """(largest panel width, wavefronts per workgroup) of the panel kernel."""
     lib = load_library()
-    width, chunk, pad = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
-    _raise_on(lib.ns_panel_geometry(int(batch), ctypes.byref(width), ctypes.byref(chunk),
-                                    ctypes.byref(pad)), lib)
-    return width.value, chunk.value, pad.value
+    width, waves = ctypes.c_int32(), ctypes.c_int32()
+    _raise_on(lib.ns_panel_geometry(int(batch), ctypes.byref(width), ctypes.byref(waves)), lib)
+    return width.value, waves.value
 
 
-def plan_panels_host(rowptr: torch.Tensor, col: torch.Tensor, batch: int, n_stripes: int,
-                     max_panel_width: int | None = None, n_groups: int | None = None):
+LANE_TARGET = 12   # at most this many edges per lane before a row gets more lanes
+
+
+def plan_panels_host(rowptr: torch.Tensor, col: torch.Tensor, batch: int, tiles_per_panel: int,
+                     max_panel_width: int | None = None, lane_target: int = LANE_TARGET):
     """Host panel layout of a CSR (numpy arrays): see ns_plan_panels."""
     lib = load_library()
-    width, chunk, pad = panel_geometry(batch)
+    width, waves = panel_geometry(batch)
     if max_panel_width is not None:
         width = min(width, int(max_panel_width))
     rowptr = np.ascontiguousarray(rowptr.detach().to("cpu", torch.int32).numpy())
     col = np.ascontiguousarray(col.detach().to("cpu", torch.int32).numpy())
     n = rowptr.size - 1
     plan = _PanelPlan()
-    rows = _c_i64()
-    groups = int(n_groups) if n_groups is not None else int(n_stripes)
-    args = (rowptr.ctypes.data, col.ctypes.data if col.size else None, n, width, int(n_stripes),
-            groups, chunk, pad, ctypes.byref(plan), ctypes.byref(rows))
-    _raise_on(lib.ns_plan_panels(*args, *([None] * 7)), lib)
+    entries = _c_i64()
+    args = (rowptr.ctypes.data, col.ctypes.data if col.size else None, n, width,
+            int(tiles_per_panel), waves, int(lane_target), ctypes.byref(plan),
+            ctypes.byref(entries))
+    _raise_on(lib.ns_plan_panels(*args, *([None] * 6)), lib)
     tiles = np.empty(4 * plan.n_tiles, np.int32)
-    chunks = np.empty(8 * plan.n_chunks, np.int32)
-    offsets = np.empty(rows.value, np.uint16)
-    lanes = np.empty(512 * plan.n_chunks, np.uint16)
-    stripes = np.empty(plan.n_stripes + 1, np.int32)
+    wave_groups = np.empty(plan.n_tiles * plan.waves + 1, np.int32)
+    groups = np.empty(4 * plan.n_groups, np.int32)
+    rows = np.empty(entries.value, np.uint16)
     perm = np.empty(plan.n_slots, np.int32)
     cols = np.empty(plan.n_slots, np.uint16)
-    _raise_on(lib.ns_plan_panels(*args, tiles.ctypes.data, chunks.ctypes.data,
-                                 offsets.ctypes.data, lanes.ctypes.data, stripes.ctypes.data,
-                                 perm.ctypes.data, cols.ctypes.data), lib)
-    return plan, tiles, chunks, offsets, lanes, stripes, perm, cols
+    _raise_on(lib.ns_plan_panels(*args, tiles.ctypes.data, wave_groups.ctypes.data,
+                                 groups.ctypes.data, rows.ctypes.data, perm.ctypes.data,
+                                 cols.ctypes.data), lib)
+    return plan, tiles, wave_groups, groups, rows, perm, cols
 
 
 def _device_tensor(array: np.ndarray, device) -> torch.Tensor:
@@ -287,29 +285,26 @@ class PanelLayout:
     Launches sharing a layout must be ordered on one stream.
     """
 
-    def __init__(self, topology, batch: int, device, *, n_stripes: int | None = None,
-                 max_panel_width: int | None = None, n_groups: int | None = None) -> None:
+    def __init__(self, topology, batch: int, device, *, tiles_per_panel: int | None = None,
+                 max_panel_width: int | None = None, lane_target: int = LANE_TARGET) -> None:
         n = topology.n_neurons
-        width, chunk, _ = panel_geometry(batch)
+        width, _ = panel_geometry(batch)
         panels = -(-n // (min(width, max_panel_width or width) & ~3))
-        if n_groups is None:
-            # One workgroup per compute unit: groups of stripes per panel.
+        if tiles_per_panel is None:
+            # One workgroup per compute unit in total.
             units = torch.cuda.get_device_properties(device).multi_processor_count
-            n_groups = max(1, units // panels)
-        if n_stripes is None:
-            # About four chunks of edges per (panel, stripe), at least one stripe per group.
-            per_pair = max(topology.n_edges, 1) / (panels * 4 * chunk)
-            n_stripes = max(int(n_groups), int(per_pair))
-        plan, tiles, chunks, offsets, lanes, stripes, perm, cols = plan_panels_host(
-            topology.in_rowptr, topology.in_col, batch, n_stripes, max_panel_width, n_groups)
+            tiles_per_panel = max(1, units // panels)
+        plan, tiles, wave_groups, groups, rows, perm, cols = plan_panels_host(
+            topology.in_rowptr, topology.in_col, batch, tiles_per_panel, max_panel_width,
+            lane_target)
         self.batch, self.n = int(batch), n
-        self.n_panels, self.n_stripes, self.n_slots = plan.n_panels, plan.n_stripes, plan.n_slots
+        self.n_panels, self.n_tiles, self.n_slots = plan.n_panels, plan.n_tiles, plan.n_slots
+        self.n_groups = plan.n_groups
         self.panel_width = plan.panel_width
         self.tiles = _device_tensor(tiles, device)
-        self.chunks = _device_tensor(chunks, device)
-        self.row_offsets = _device_tensor(offsets, device)
-        self.lane_rows = _device_tensor(lanes, device)
-        self.stripes = _device_tensor(stripes, device)
+        self.wave_groups = _device_tensor(wave_groups, device)
+        self.groups = _device_tensor(groups, device)
+        self.rows = _device_tensor(rows if rows.size else np.zeros(1, np.uint16), device)
         self.col = _device_tensor(cols, device)
         perm_t = torch.from_numpy(perm).to(device)
         self.valid = perm_t >= 0
@@ -325,7 +320,13 @@ class PanelLayout:
         if self._slot_key == key and self._slot_weights is not None:
             return self._slot_weights
         with torch.no_grad():
-            if weight.dtype in (torch.float32, torch.float16):
+            if weight.numel() == 0:           # no edges: every slot is padding (code 0)
+                nibbles = block_scales is not None
+                slots = torch.zeros(self.n_slots // 2 if nibbles else self.n_slots,
+                                    dtype=weight.dtype, device=weight.device)
+                scales = (torch.zeros(self.n_slots, dtype=torch.uint8, device=weight.device)
+                          if nibbles else None)
+            elif weight.dtype in (torch.float32, torch.float16):
                 slots = torch.where(self.valid, weight[self.perm], torch.zeros((), dtype=weight.dtype,
                                                                                device=weight.device))
                 scales = None
@@ -347,9 +348,9 @@ class PanelLayout:
     def plan_struct(self, slot_weight: torch.Tensor, slot_scales: torch.Tensor | None) -> _PanelPlan:
         plan = _PanelPlan()
         ctypes.memmove(ctypes.addressof(plan), ctypes.addressof(self._plan), ctypes.sizeof(plan))
-        plan.tiles, plan.chunks = self.tiles.data_ptr(), self.chunks.data_ptr()
-        plan.row_offsets, plan.lane_rows = self.row_offsets.data_ptr(), self.lane_rows.data_ptr()
-        plan.stripes, plan.col = self.stripes.data_ptr(), self.col.data_ptr()
+        plan.tiles, plan.wave_groups = self.tiles.data_ptr(), self.wave_groups.data_ptr()
+        plan.groups, plan.rows = self.groups.data_ptr(), self.rows.data_ptr()
+        plan.col = self.col.data_ptr()
         plan.weight = slot_weight.data_ptr()
         plan.slot_scales = slot_scales.data_ptr() if slot_scales is not None else None
         plan.partials = self.partials.data_ptr() if self.partials is not None else None

@@ -83,18 +83,16 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
     state in LDS and streams a panel-sorted copy of the graph (batch 1 or 2;
     built once, at construction), "rows" streams the CSR as is and gathers
     the state from cache, "auto" uses panels whenever the batch allows.
-    ``panel_width`` caps the neurons per panel (default: what LDS holds),
-    ``panel_stripes`` sets the row stripes (default: about four chunks of
-    edges per panel and stripe) and ``panel_groups`` the workgroups per panel
-    (default: compute units / panels).
+    ``panel_width`` caps the neurons per panel (default: what LDS holds) and
+    ``panel_tiles`` sets the workgroups per panel (default: compute units /
+    panels).
     """
 
     def __init__(self, topology: SparseTopology, dynamics: DendriticDynamics,
                  initial_state: torch.Tensor, *, threads_per_row: int | None = None,
                  extension=None, weight_dtype: torch.dtype = torch.float32,
                  weight_format: str | None = None, kernel: str = "auto",
-                 panel_width: int | None = None, panel_stripes: int | None = None,
-                 panel_groups: int | None = None) -> None:
+                 panel_width: int | None = None, panel_tiles: int | None = None) -> None:
         if kernel not in ("auto", "rows", "panels"):
             raise ValueError("kernel must be 'auto', 'rows' or 'panels'")
         if threads_per_row not in (None, 8, 16, 32):
@@ -119,8 +117,8 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
             raise ValueError("the panel kernel needs batch 1 or 2 and the native extension")
         use_panels = kernel == "panels" or (kernel == "auto" and batch in (1, 2) and native)
         self.kernel = "panels" if use_panels else "rows"
-        self._panels = (PanelLayout(topology, batch, initial_state.device, n_stripes=panel_stripes,
-                                    max_panel_width=panel_width, n_groups=panel_groups)
+        self._panels = (PanelLayout(topology, batch, initial_state.device,
+                                    tiles_per_panel=panel_tiles, max_panel_width=panel_width)
                         if use_panels else None)
 
     def _invalidate_precision_cache(self) -> None:

@@ -1,8 +1,8 @@
 """The column-panel tick (batch 1 and 2) on the MI355X.
 
 Several panels are forced with small panel widths so the per-panel partial
-sums and the last-arrival combine run on small graphs; hub rows longer than
-one chunk exercise the continuation carry.  Bars: float32 within 1e-5 of the
+sums and the combine kernel run on small graphs; hub rows take whole
+wavefronts (64 lanes per row) and rows of every length class mix in one tile.  Bars: float32 within 1e-5 of the
 oracle; fp16/fp8/nvfp4 storage bitwise equal to the panel tick on the
 decoded float32 weights; bitwise repeatable.
 """
@@ -28,7 +28,7 @@ def errors(native, oracle) -> float:
 
 
 def hub_case(gpu, n=12_000, seed=2):
-    """Random rows plus two hub rows (one longer than a chunk of 8192 edges when n allows)."""
+    """Random rows plus two hub rows (9000 and n/2 edges)."""
     rng = np.random.default_rng(seed)
     hub = min(n, 9000)
     dst = np.concatenate([np.zeros(hub, np.int64), np.full(n // 2, 3), rng.integers(0, n, 8 * n)])
@@ -42,14 +42,13 @@ def hub_case(gpu, n=12_000, seed=2):
 
 
 @pytest.mark.parametrize("batch", [1, 2])
-@pytest.mark.parametrize("width,stripes,groups", [(None, None, None), (1000, 7, 3), (256, 9, 2)])
-def test_panels_match_oracle(gpu, batch, width, stripes, groups):
-    print(f"case panels batch={batch} width={width} stripes={stripes} groups={groups}", flush=True)
+@pytest.mark.parametrize("width,tiles", [(None, None), (1000, 7), (256, 2)])
+def test_panels_match_oracle(gpu, batch, width, tiles):
+    print(f"case panels batch={batch} width={width} tiles={tiles}", flush=True)
     graph, topology, model, params = hub_case(gpu)
     drive = column_drive(batch)
     native = NativeDendriticMatrixRuntime(topology, model, torch.zeros(batch, graph.n, device=gpu),
-                                          kernel="panels", panel_width=width, panel_stripes=stripes,
-                                          panel_groups=groups)
+                                          kernel="panels", panel_width=width, panel_tiles=tiles)
     oracle = ort.MatrixOracle(graph, params, torch.zeros(batch, graph.n))
     assert native.kernel == "panels"
     worst = 0.0
@@ -58,7 +57,7 @@ def test_panels_match_oracle(gpu, batch, width, stripes, groups):
         oracle.step(drive, 0.1)
         worst = max(worst, errors(native, oracle))
     print(f"panels batch={batch} width={width}: {worst:.3e} over 30 ticks "
-          f"({native._panels.n_panels} panels x {native._panels.n_stripes} stripes)")
+          f"({native._panels.n_panels} panels, {native._panels.n_tiles} tiles)")
     assert worst <= 1e-5
 
 
@@ -84,7 +83,7 @@ def test_panel_formats_equal_decoded_fp32(gpu, fmt, batch):
     graph, topology, model, params = hub_case(gpu, n=6000, seed=9)
     kwargs = {"weight_dtype": torch.float16} if fmt == "fp16" else {"weight_format": fmt}
     native = NativeDendriticMatrixRuntime(topology, model, torch.zeros(batch, 6000, device=gpu),
-                                          kernel="panels", panel_width=1024, panel_stripes=5,
+                                          kernel="panels", panel_width=1024, panel_tiles=5,
                                           **kwargs)
     native._weights()
     if fmt == "fp16":
@@ -98,7 +97,7 @@ def test_panel_formats_equal_decoded_fp32(gpu, fmt, batch):
         6000, topology.src, topology.dst,
         torch.from_numpy(decoded_host).to(gpu)[topology.out_weight_index.long()])
     reference = NativeDendriticMatrixRuntime(decoded, model, torch.zeros(batch, 6000, device=gpu),
-                                             kernel="panels", panel_width=1024, panel_stripes=5)
+                                             kernel="panels", panel_width=1024, panel_tiles=5)
     oracle = ort.MatrixOracle(graph, params, torch.zeros(batch, 6000), in_weight=decoded_host)
     for _ in range(10):
         native.step(0.2, dendritic_drive=0.1)
@@ -112,7 +111,7 @@ def test_panel_formats_equal_decoded_fp32(gpu, fmt, batch):
 def test_panel_weight_refresh_after_mutation(gpu):
     case = make_case(3000, 60_000, 4, gpu)
     native = NativeDendriticMatrixRuntime(case.topology, case.model, torch.zeros(1, 3000, device=gpu),
-                                          kernel="panels", panel_width=512, panel_stripes=4)
+                                          kernel="panels", panel_width=512, panel_tiles=4)
     oracle = ort.MatrixOracle(case.graph, case.params, torch.zeros(1, 3000))
     for tick in range(12):
         if tick == 6:

@@ -1,9 +1,13 @@
 """The column-panel layout (ns_plan_panels) on the host: invariants, and a numpy
 emulation of the panel kernel's decomposition against the plain CSR product.
 
-Covers several panels (small panel widths), rows longer than one chunk (hub
-rows split with continuation flags), rows without edges, empty graphs and
-stripes of unequal size.
+The emulation walks every wavefront's stream exactly as the kernel does
+(register blocks of up to 16 steps, prefetch of the next block) and checks
+that every slot the kernel reads lies inside the slot arrays, that every edge
+lands in exactly one slot of its row and panel, that each (panel, row) is
+finished exactly once, and that the per-lane sums plus the lane butterfly
+reproduce the CSR product.  Covers several panels (small panel widths), hub
+rows that take all 64 lanes, rows without edges, empty graphs and tiny graphs.
 """
 
 from __future__ import annotations
@@ -14,6 +18,9 @@ import torch
 
 from oracle import topology as otop
 from neurosim_gpu.native import panel_geometry, plan_panels_host
+
+MAX_BLOCK_STEPS = 16
+TAIL_SLOTS = 2 * MAX_BLOCK_STEPS * 64
 
 
 def hub_graph(n: int, seed: int) -> otop.Graph:
@@ -33,88 +40,97 @@ GRAPHS = {
 }
 
 
-def emulate(graph: otop.Graph, batch: int, n_stripes: int, width: int | None, source: np.ndarray,
-            n_groups: int | None = None):
-    plan, tiles, chunks, offsets, lanes, stripes, perm, cols = plan_panels_host(
-        torch.from_numpy(graph.in_rowptr), torch.from_numpy(graph.in_col), batch, n_stripes, width,
-        n_groups)
+def emulate(graph: otop.Graph, batch: int, tiles_per_panel: int, width: int | None,
+            source: np.ndarray, lane_target: int = 12):
+    plan, tiles, wave_groups, groups, rows, perm, cols = plan_panels_host(
+        torch.from_numpy(graph.in_rowptr), torch.from_numpy(graph.in_col), batch, tiles_per_panel,
+        width, lane_target)
     n, m = graph.n, graph.n_edges
-    cap, chunk_edges, pad = panel_geometry(batch)
-    assert plan.chunk_edges == chunk_edges and plan.pad == pad
-    assert plan.panel_width % 4 == 0 and plan.panel_width <= min(cap, width or cap)
-    assert plan.n_panels * plan.panel_width >= n > (plan.n_panels - 1) * plan.panel_width
-    assert stripes[0] == 0 and stripes[-1] == n and np.all(np.diff(stripes) > 0)
-    rows_of_edge = np.repeat(np.arange(n), np.diff(graph.in_rowptr))
-    partial = np.zeros((plan.n_panels, n, batch))
-    written = np.zeros((plan.n_panels, n), dtype=np.int64)
-    stripe_done = np.zeros((plan.n_panels, plan.n_stripes), dtype=np.int64)
-    seen = np.zeros(m, dtype=np.int64)
+    cap, waves = panel_geometry(batch)
+    W, P = plan.panel_width, plan.n_panels
+    assert plan.waves == waves == 16
+    assert W % 4 == 0 and W <= min(cap, width or cap)
+    assert P * W >= n > (P - 1) * W
+    assert perm.size == cols.size == plan.n_slots
     tiles = tiles.reshape(-1, 4)
-    chunks = chunks.reshape(-1, 8)
-    lanes = lanes.reshape(-1, 512)
-    assert np.array_equal(np.sort(tiles[:, 1]), tiles[:, 1]) and tiles[0, 1] == 0
-    assert np.all(tiles[1:, 1] == tiles[:-1, 2]) and tiles[-1, 2] == plan.n_chunks
-    for panel, c0, c1, _group in tiles:
-        carry = np.zeros(batch)
-        current = None                 # stripe in progress and the next row expected
-        for c in range(c0, c1):
-            slot0, nedge, row0, nrows, off0, flags, lane_index, stripe = chunks[c]
-            assert slot0 % pad == 0 and 0 < nrows <= 511 and nedge <= chunk_edges
-            if current is None:
-                current, expected_row = stripe, stripes[stripe]
-            assert stripe == current and row0 == expected_row
-            offs = offsets[off0: off0 + nrows + 1].astype(np.int64)
-            assert offs[0] == 0 and offs[-1] == nedge and np.all(np.diff(offs) >= 0)
-            tail = perm[slot0 + nedge: slot0 + -(-nedge // pad) * pad]
-            assert np.all(tail == -1)
-            for lane in range(512):
-                first = lane * pad
-                if first < nedge:
-                    r = lanes[lane_index, lane]
-                    assert offs[r] <= first < offs[r + 1]
-                else:
-                    assert lanes[lane_index, lane] == nrows
-            for r in range(nrows):
-                slots = np.arange(slot0 + offs[r], slot0 + offs[r + 1])
-                edges = perm[slots]
-                assert np.all(edges >= 0)
-                seen[edges] += 1
-                row = row0 + r
-                assert np.all(rows_of_edge[edges] == row)
-                sources = graph.in_col[edges].astype(np.int64)
-                assert np.array_equal(sources - panel * plan.panel_width, cols[slots].astype(np.int64))
-                assert np.all(sources // plan.panel_width == panel)
-                value = (graph.in_weight[edges].astype(np.float64)[:, None] * source[sources]).sum(0)
-                if r == 0 and flags & 1:
-                    value = carry + value
-                if r == nrows - 1 and flags & 2:
-                    carry = value
-                    expected_row = row
-                    continue
-                partial[panel, row] = value
-                written[panel, row] += 1
-                expected_row = row + 1
-            if flags & 4:
-                assert expected_row == stripes[stripe + 1]
-                stripe_done[panel, stripe] += 1
-                current = None
-        assert current is None, "a tile ends at a stripe boundary"
+    groups = groups.reshape(-1, 4)
+    assert wave_groups.size == plan.n_tiles * waves + 1 and wave_groups[0] == 0
+    assert wave_groups[-1] == plan.n_groups and np.all(np.diff(wave_groups) >= 0)
+    covered = np.zeros((P, n), dtype=np.int64)
+    for panel, r0, r1, index in tiles:
+        assert 0 <= r0 < r1 <= n and r1 - r0 <= 65536
+        covered[panel, r0:r1] += 1
+    assert np.all(covered == 1), "each panel's tiles partition the rows"
+
+    rows_of_edge = np.repeat(np.arange(n), np.diff(graph.in_rowptr))
+    partial = np.zeros((P, n, batch))
+    written = np.zeros((P, n), dtype=np.int64)
+    seen = np.zeros(m, dtype=np.int64)
+    last_stream_end = 0
+    for t, (panel, r0, r1, _) in enumerate(tiles):
+        for w in range(waves):
+            g0, g1 = wave_groups[t * waves + w], wave_groups[t * waves + w + 1]
+            if g0 == g1:
+                continue
+            first = groups[g0, 0]
+            total = (groups[g1 - 1, 0] - first) // 64 + groups[g1 - 1, 1]
+            # furthest slot any lane reads: one block of prefetch past the last consumed block
+            blocks = -(-total // MAX_BLOCK_STEPS)
+            assert first + (blocks + 1) * MAX_BLOCK_STEPS * 64 <= plan.n_slots
+            last_stream_end = max(last_stream_end, first + 64 * total)
+            slot = first
+            for g in range(g0, g1):
+                slot0, steps, packed, rowtab = groups[g]
+                lg, nrows = packed & 255, packed >> 8
+                lanes = 1 << lg
+                assert slot0 == slot and slot0 % 64 == 0, "a wave's groups are contiguous"
+                assert 0 <= lg <= 6 and 1 <= nrows <= 64 >> lg and steps >= 0
+                block = np.arange(slot0, slot0 + 64 * steps).reshape(steps, 64)
+                edges = perm[block]
+                srcs = cols[block].astype(np.int64)
+                pad = edges < 0
+                assert np.all(srcs[pad] == W), "padding reads the sentinel zero"
+                for k in range(64 >> lg):
+                    lane_edges = edges[:, k * lanes:(k + 1) * lanes]
+                    if k >= nrows:
+                        assert np.all(lane_edges < 0)
+                        continue
+                    row = r0 + int(rows[rowtab + k])
+                    assert r0 <= row < r1
+                    mine = lane_edges.T          # [lane j, step]: edges j, j+lanes, ...
+                    order = lane_edges.reshape(-1)
+                    real = order[order >= 0]
+                    assert np.all(rows_of_edge[real] == row)
+                    assert np.all(graph.in_col[real] // W == panel)
+                    seen[real] += 1
+                    lane_sums = []
+                    for j in range(lanes):
+                        e = mine[j][mine[j] >= 0]
+                        assert np.array_equal(cols[block[:, k * lanes + j]][mine[j] >= 0].astype(np.int64),
+                                              graph.in_col[e] - panel * W)
+                        lane_sums.append((graph.in_weight[e].astype(np.float64)[:, None]
+                                          * source[graph.in_col[e]]).sum(0))
+                    while len(lane_sums) > 1:        # the xor butterfly pairs neighbours first
+                        lane_sums = [lane_sums[i] + lane_sums[i + 1] for i in range(0, len(lane_sums), 2)]
+                    partial[panel, row] = lane_sums[0]
+                    written[panel, row] += 1
+                slot += 64 * steps
     assert np.all(seen == 1), "every edge lands in exactly one slot"
     assert np.all(written == 1), "every (panel, row) is finished exactly once"
-    assert np.all(stripe_done == 1), "every (panel, stripe) completes exactly once"
+    tail = perm[last_stream_end:]
+    assert tail.size >= TAIL_SLOTS and np.all(tail == -1) and np.all(cols[last_stream_end:] == W)
     return plan, partial.sum(0)
 
 
 @pytest.mark.parametrize("name", list(GRAPHS))
-@pytest.mark.parametrize("batch,stripes,width,groups", [(1, 7, None, 3), (1, 3, 256, 3),
-                                                         (2, 5, 1000, 2), (2, 1, 64, 1)])
-def test_panel_layout_reproduces_the_csr_product(name, batch, stripes, width, groups):
+@pytest.mark.parametrize("batch,tiles,width", [(1, 3, None), (1, 5, 256), (2, 2, 1000), (2, 1, 64)])
+def test_panel_layout_reproduces_the_csr_product(name, batch, tiles, width):
     graph = GRAPHS[name]()
     if width is not None and graph.n // width > 24:
         width = -(-graph.n // 24)          # keep the python emulation to <= 24 panels
     rng = np.random.default_rng(11)
     source = rng.random((graph.n, batch))
-    plan, result = emulate(graph, batch, stripes, width, source, groups)
+    plan, result = emulate(graph, batch, tiles, width, source)
     from scipy.sparse import csr_matrix
 
     matrix = csr_matrix((graph.in_weight.astype(np.float64), graph.in_col, graph.in_rowptr),
@@ -123,12 +139,24 @@ def test_panel_layout_reproduces_the_csr_product(name, batch, stripes, width, gr
     np.testing.assert_allclose(result, expected, rtol=1e-12, atol=1e-12)
 
 
-def test_hub_rows_are_split_across_chunks():
+def test_lane_widths_follow_segment_length():
     graph = hub_graph(12_000, 2)
-    plan, tiles, chunks, *_ = plan_panels_host(torch.from_numpy(graph.in_rowptr),
-                                               torch.from_numpy(graph.in_col), 1, 4, None, 2)
-    flags = chunks.reshape(-1, 8)[:, 5]
-    assert (flags & 1).any() and (flags & 2).any()
+    plan, tiles, wave_groups, groups, rows, perm, cols = plan_panels_host(
+        torch.from_numpy(graph.in_rowptr), torch.from_numpy(graph.in_col), 1, 4)
+    lg = groups.reshape(-1, 4)[:, 2] & 255
+    assert lg.max() == 6, "the 9000-edge hub row takes a whole wavefront"
+    assert (lg == 0).any()
+
+
+def test_waves_are_balanced_within_a_tile():
+    graph = otop.random_graph(20_000, 1_000_000, seed=4)
+    plan, tiles, wave_groups, groups, rows, perm, cols = plan_panels_host(
+        torch.from_numpy(graph.in_rowptr), torch.from_numpy(graph.in_col), 1, 8)
+    groups = groups.reshape(-1, 4)
+    cost = groups[:, 1] + 1
+    for t in range(plan.n_tiles):
+        loads = [cost[wave_groups[t * 16 + w]: wave_groups[t * 16 + w + 1]].sum() for w in range(16)]
+        assert max(loads) <= 1.1 * np.mean(loads) + max(cost)
 
 
 def test_planner_rejects_bad_geometry():
@@ -138,13 +166,13 @@ def test_planner_rejects_bad_geometry():
     rowptr = np.array([0, 1, 2], np.int32)
     col = np.array([0, 5], np.int32)      # column out of range
     plan = native._PanelPlan()
-    rows = native._c_i64()
+    entries = native._c_i64()
     import ctypes
 
-    rc = lib.ns_plan_panels(rowptr.ctypes.data, col.ctypes.data, 2, 64, 1, 1, 8192, 16,
-                            ctypes.byref(plan), ctypes.byref(rows), *([None] * 7))
+    rc = lib.ns_plan_panels(rowptr.ctypes.data, col.ctypes.data, 2, 64, 1, 16, 12,
+                            ctypes.byref(plan), ctypes.byref(entries), *([None] * 6))
     assert rc != 0 and b"out of range" in lib.ns_last_error()
     col = np.array([0, 1], np.int32)
-    rc = lib.ns_plan_panels(rowptr.ctypes.data, col.ctypes.data, 2, 64, 1, 1, 4096, 16,
-                            ctypes.byref(plan), ctypes.byref(rows), *([None] * 7))
-    assert rc != 0 and b"chunk_edges" in lib.ns_last_error()
+    rc = lib.ns_plan_panels(rowptr.ctypes.data, col.ctypes.data, 2, 64, 1, 8, 12,
+                            ctypes.byref(plan), ctypes.byref(entries), *([None] * 6))
+    assert rc != 0 and b"wavefronts" in lib.ns_last_error()
