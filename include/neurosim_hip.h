@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 3
+#define NS_ABI_VERSION 4
 
 /* Return codes. */
 #define NS_OK 0
@@ -96,11 +96,11 @@ typedef struct ns_row_plan {
  * tile's rows are sorted by the length of their segment in the panel and cut
  * into groups; a group gives each of its rows 2^lg lanes of a 64-lane
  * wavefront (64 >> lg rows), lane j of a row taking the row's edges j, j+2^lg,
- * ...  A group's slots are step-major: slot (step k, lane l) is
- * first_slot + 64*k + l.  Each of the tile's `waves` wavefronts owns a run of
- * consecutive groups whose slots are contiguous.  Padding slots have source
- * index `panel_width` (a zero kept in LDS) and weight code 0.  Edge slot k is
- * original CSR edge perm[k] (or padding). */
+ * ...  Every group has at least one step.  A group's slots are step-major:
+ * slot (step k, lane l) is first_slot + 64*k + l.  Each of the tile's `waves`
+ * wavefronts owns a run of consecutive groups whose slots are contiguous (its
+ * stream).  Padding slots have source index `panel_width` (a zero kept in LDS)
+ * and weight code 0.  Edge slot k is original CSR edge perm[k] (or padding). */
 typedef struct ns_panel_plan {
   int32_t panel_width;
   int32_t n_panels;
@@ -109,18 +109,23 @@ typedef struct ns_panel_plan {
   int32_t waves;               /* wavefronts per workgroup the plan was built for */
   int32_t reserved[3];
   int64_t n_slots;             /* edge slots including padding and the tail padding */
-  const int32_t* tiles;        /* [n_tiles][4]: panel, first row, end row, tile index */
+  int64_t n_step_words;        /* uint32 words of `last_steps` */
+  const int32_t* tiles;        /* [n_tiles][4]: panel, first row, end row, first entry of
+                                  the tile's rows in `rows` */
   const int32_t* wave_groups;  /* [n_tiles*waves + 1]: wave w of tile t owns groups
                                   wave_groups[t*waves+w] .. wave_groups[t*waves+w+1]-1 */
   const int32_t* groups;       /* [n_groups][4]: first slot, steps, lg | rows << 8,
                                   first entry in `rows` */
   const uint16_t* rows;        /* tile-local row (row - tile's first row) of each group row */
+  const uint32_t* last_steps;  /* bit k set: step k (slots 64k .. 64k+63) is a group's last */
   const uint16_t* col;         /* [n_slots] source index minus the panel's first neuron */
   const void* weight;          /* [n_slots] weights in slot order, encoding of the matrix:
                                   F32/F16 values, E4M3 codes, NVFP4 nibbles (two per byte) */
   const uint8_t* slot_scales;  /* NVFP4: e4m3 block-scale code of each slot's edge */
-  float* partials;             /* workspace [n_panels][N][batch] (n_panels > 1): per-panel
-                                  row sums, added in panel order by a second kernel */
+  float* partials;             /* workspace float[2][n_panels*N*batch]: the second half
+                                  holds row sums in row-table order, the first half the
+                                  per-panel row sums by row (several panels), added in
+                                  panel order by a second kernel */
 } ns_panel_plan;
 
 /* Arguments of one fused matrix tick. */
@@ -201,18 +206,20 @@ int ns_plan_row_blocks(const int32_t* rowptr_host, int64_t n_rows, int32_t block
  * `tiles_per_panel` tiles of equal cost (segment edges + 1 per row, at most
  * 65536 rows each).  A row whose segment has L edges gets the smallest
  * power-of-two lane count that leaves each lane at most `lane_target` edges
- * (at most 64).  Groups go to the `waves` wavefronts of their tile longest
- * first onto the least-loaded one.  Call once with all output pointers NULL to
- * get the sizes in *plan (n_panels, panel_width, n_tiles, n_groups, n_slots,
- * waves) and *n_row_entries, then again with arrays of those sizes: tiles
- * int32[4*n_tiles], wave_groups int32[n_tiles*waves+1], groups
- * int32[4*n_groups], rows uint16[n_row_entries], perm int32[n_slots] (-1 for
- * padding), col uint16[n_slots].  Pointer fields of *plan are not touched. */
+ * (at most 64).  Groups go to the `waves` wavefronts of their tile (which
+ * must be the kernel's wavefronts per workgroup) longest first onto the
+ * least-loaded one.  Call once with all output pointers NULL to get the sizes
+ * in *plan (n_panels, panel_width, n_tiles, n_groups, n_slots, waves,
+ * n_step_words) and *n_row_entries, then again with arrays of those sizes:
+ * tiles int32[4*n_tiles], wave_groups int32[n_tiles*waves+1], groups
+ * int32[4*n_groups], rows uint16[n_row_entries], last_steps
+ * uint32[n_step_words], perm int32[n_slots] (-1 for padding), col
+ * uint16[n_slots].  Pointer fields of *plan are not touched. */
 int ns_plan_panels(const int32_t* rowptr_host, const int32_t* col_host, int64_t n_rows,
                    int32_t max_panel_width, int32_t tiles_per_panel, int32_t waves,
                    int32_t lane_target, ns_panel_plan* plan, int64_t* n_row_entries,
                    int32_t* tiles, int32_t* wave_groups, int32_t* groups, uint16_t* rows,
-                   int32_t* perm, uint16_t* col);
+                   uint32_t* last_steps, int32_t* perm, uint16_t* col);
 
 /* Panel geometry the tick kernels use for batch width `batch` (1 or 2):
  * largest panel width and the wavefronts per workgroup (NULL outputs are

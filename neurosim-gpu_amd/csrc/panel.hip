@@ -12,14 +12,19 @@
 //  * the tile's rows are grouped by segment length; a group gives each row
 //    2^lg lanes, and lane j of a row accumulates the row's edges j, j+2^lg, ...
 //    in one float32 FMA chain, so the inner loop has no row boundaries;
-//  * each wavefront owns a run of consecutive groups whose slots are one
-//    contiguous stream of 64-lane steps (16-bit panel-local source index plus
-//    the weight in its encoding).  The stream is read in register blocks of
-//    D steps, the next block in flight while the current one is consumed;
-//  * at a group's end the row's lanes are added by an xor butterfly and one
-//    lane per row applies the neuron update (one panel) or stores the panel's
-//    partial sum; a second kernel adds the partials in panel order and
-//    applies the update (several panels).
+//  * each wavefront owns a run of consecutive groups (balanced by the planner)
+//    whose slots are one contiguous stream of 64-lane steps (16-bit
+//    panel-local source index plus the weight in its encoding).  The stream
+//    is read in register blocks of D steps, the next block in flight while
+//    the current one is consumed;
+//  * a bitmap over steps marks each group's last step: inside a block the
+//    sums are only snapshotted there, and after the block the groups that
+//    ended are closed in order (xor butterfly over the row's lanes, one lane
+//    per row stores the sum at the group's row-table entries);
+//  * after its streams the workgroup maps row-table entries back to rows:
+//    with one panel it updates its own rows, with several it stores the
+//    panel's partial sums by row and a second kernel adds them in panel
+//    order and applies the update.
 //
 // Results are bitwise repeatable and identical across weight encodings that
 // decode to the same float32 values.
@@ -39,13 +44,15 @@ constexpr int panel_capacity_neurons() {
   return ((163840 - 64) / (4 * BT) - 1) & ~3;
 }
 
-// Steps per register block: enough 64-lane loads in flight per wavefront
-// to cover HBM latency with 16 wavefronts per compute unit.
-template <int FMT>
+// Steps per register block: enough 64-lane loads in flight per wavefront to
+// cover HBM latency with 16 wavefronts per compute unit, within 128 VGPRs.
+template <int BT, int FMT>
 constexpr int block_steps() {
-  return FMT == NS_WEIGHT_F32 ? 8 : 12;
+  if constexpr (FMT == NS_WEIGHT_F32) return 8;
+  else if constexpr (FMT == NS_WEIGHT_F16) return BT == 1 ? 12 : 8;
+  else if constexpr (FMT == NS_WEIGHT_E4M3) return BT == 1 ? 16 : 12;
+  else return BT == 1 ? 12 : 8;
 }
-static_assert(block_steps<NS_WEIGHT_F16>() <= kPanelMaxPrefetch, "tail padding too short");
 
 struct PanelArgs {
   int64_t N, B;
@@ -56,11 +63,13 @@ struct PanelArgs {
   const int32_t* wave_groups;
   const int32_t* groups;
   const uint16_t* rows;
+  const uint32_t* last_steps;
   const uint16_t* col;
   const void* weight;
   const uint8_t* slot_scales;
   const float* gscale;
-  float* partials;
+  float* sorted;     // [rows-table entries][BT]: row sums in row-table order
+  float* partials;   // [n_panels][N][BT]: row sums by row (several panels)
   OutPlane os, od, oa;
   int32_t s_vec;   // s.sn == 1 (B == 1) or neuron-major B == 2, 16-byte aligned
 };
@@ -68,6 +77,7 @@ struct PanelArgs {
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v2f __attribute__((ext_vector_type(2)));
 typedef const int32_t __attribute__((address_space(4)))* const_i32_ptr;
+typedef const uint32_t __attribute__((address_space(4)))* const_u32_ptr;
 
 // One lane's raw slot: source index, weight bits (F32/F16/E4M3 code, or the
 // NVFP4 byte holding its nibble) and, for NVFP4, the block-scale code.
@@ -75,20 +85,21 @@ struct Slot {
   uint32_t c, w, sc;
 };
 
+// Slots of one register block: this lane's slot of step k is q0 + 64k.
 template <int FMT>
-__device__ __forceinline__ Slot load_slot(const PanelArgs& A, int64_t q) {
+__device__ __forceinline__ Slot load_slot(const PanelArgs& A, int64_t q0, int k) {
   Slot x;
-  x.c = A.col[q];
+  x.c = A.col[q0 + 64 * k];
   if constexpr (FMT == NS_WEIGHT_F32) {
-    x.w = static_cast<const uint32_t*>(A.weight)[q];
+    x.w = static_cast<const uint32_t*>(A.weight)[q0 + 64 * k];
   } else if constexpr (FMT == NS_WEIGHT_F16) {
-    x.w = static_cast<const uint16_t*>(A.weight)[q];
+    x.w = static_cast<const uint16_t*>(A.weight)[q0 + 64 * k];
   } else if constexpr (FMT == NS_WEIGHT_E4M3) {
-    x.w = static_cast<const uint8_t*>(A.weight)[q];
+    x.w = static_cast<const uint8_t*>(A.weight)[q0 + 64 * k];
   } else {
-    x.w = static_cast<const uint8_t*>(A.weight)[q >> 1];
+    x.w = static_cast<const uint8_t*>(A.weight)[(q0 >> 1) + 32 * k];
   }
-  x.sc = FMT == NS_WEIGHT_NVFP4 ? A.slot_scales[q] : 0u;
+  x.sc = FMT == NS_WEIGHT_NVFP4 ? A.slot_scales[q0 + 64 * k] : 0u;
   return x;
 }
 
@@ -115,22 +126,42 @@ __device__ __forceinline__ void update(const PanelArgs& A, int64_t n, int64_t b,
   A.oa.put(b, n, x.adaptation);
 }
 
+// A group descriptor held in scalar registers.
+struct Group {
+  int lg, nrows, rowtab;
+};
+
+__device__ __forceinline__ Group load_group(const PanelArgs& A, int g) {
+  const_i32_ptr desc = (const_i32_ptr)(A.groups + 4 * static_cast<int64_t>(g));
+  return Group{desc[2] & 255, desc[2] >> 8, desc[3]};
+}
+
+// Boundary bits of steps [k0, k0 + D) of the whole slot array.
+template <int D>
+__device__ __forceinline__ uint32_t boundary_bits(const PanelArgs& A, int64_t k0) {
+  const_u32_ptr w = (const_u32_ptr)(A.last_steps + (k0 >> 5));
+  const uint64_t both = w[0] | (static_cast<uint64_t>(w[1]) << 32);
+  return static_cast<uint32_t>(both >> (k0 & 31)) & ((1u << D) - 1u);
+}
+
 template <int BT, int FMT>
 __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) {
-  constexpr int D = block_steps<FMT>();
+  constexpr int D = block_steps<BT, FMT>();
+  static_assert(D <= kPanelMaxPrefetch, "tail padding too short");
   constexpr int CAP = panel_capacity_neurons<BT>();
+  constexpr int kRowsAhead = 4;
   __shared__ __attribute__((aligned(16))) float lds_s[(CAP + 1) * BT];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const_i32_ptr tile = (const_i32_ptr)(A.tiles + 4 * static_cast<int64_t>(blockIdx.x));
-  const int panel = tile[0], row0 = tile[1];
+  const int panel = tile[0], row0 = tile[1], row1 = tile[2], entry0 = tile[3];
   const int64_t base = static_cast<int64_t>(panel) * A.width;
   const int len = static_cast<int>(min<int64_t>(A.width, A.N - base));
   const float gscale = (FMT == NS_WEIGHT_E4M3 || FMT == NS_WEIGHT_NVFP4) ? *A.gscale : 1.0f;
 
-  // This wavefront's stream: groups [g, g_end), slots [first, first + 64*total).
+  // This wavefront's stream: groups [g, g_end), steps [first/64, first/64 + total).
   const_i32_ptr wg = (const_i32_ptr)(A.wave_groups + static_cast<int64_t>(blockIdx.x) * kPanelWaves + wave);
   int g = wg[0];
   const int g_end = wg[1];
@@ -143,10 +174,22 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
     total = (last[0] - head[0]) / 64 + last[1];
   }
 
-  // First register block in flight while the panel is staged.
-  Slot cur[D], nxt[D];
+  // First register block in flight while the panel is staged, and this
+  // thread's first row-table entries for the epilogue.
+  Slot buf_a[D], buf_b[D];
 #pragma unroll
-  for (int k = 0; k < D; ++k) cur[k] = load_slot<FMT>(A, first + 64 * k + lane);
+  for (int k = 0; k < D; ++k) buf_a[k] = load_slot<FMT>(A, first + lane, k);
+  uint32_t bits = boundary_bits<D>(A, first / 64);
+  Group now{0, 0, 0}, next{0, 0, 0};
+  if (g < g_end) now = load_group(A, g);
+  if (g + 1 < g_end) next = load_group(A, g + 1);
+  const int nrows = row1 - row0;
+  int rows_ahead[kRowsAhead];
+#pragma unroll
+  for (int k = 0; k < kRowsAhead; ++k) {
+    const int e = tid + k * kPanelThreads;
+    rows_ahead[k] = e < nrows ? A.rows[entry0 + e] : 0;
+  }
 
   // Stage this panel's slice of s (neuron-major, BT columns per neuron), 8 loads deep,
   // and the zero that padding slots read.
@@ -172,73 +215,93 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
   if (tid < BT) lds_s[A.width * BT + tid] = 0.0f;
   __syncthreads();
 
-  // Group state (wave-uniform).
-  int left = 0, lg = 0, nrows = 0, rowtab = 0;
   float acc[BT];
 #pragma unroll
   for (int j = 0; j < BT; ++j) acc[j] = 0.0f;
-  auto open = [&]() {
-    const_i32_ptr desc = (const_i32_ptr)(A.groups + 4 * static_cast<int64_t>(g));
-    left = desc[1];
-    lg = desc[2] & 255;
-    nrows = desc[2] >> 8;
-    rowtab = desc[3];
-  };
-  auto close = [&]() {
-    const int lanes = 1 << lg;
-    float t[BT];
-#pragma unroll
-    for (int j = 0; j < BT; ++j) {
-      t[j] = acc[j];
-      for (int off = 1; off < lanes; off <<= 1) t[j] += __shfl_xor(t[j], off, 64);
-      acc[j] = 0.0f;
-    }
-    const int k = lane >> lg;
-    if ((lane & (lanes - 1)) == 0 && k < nrows) {
-      const int64_t row = row0 + static_cast<int64_t>(A.rows[rowtab + k]);
-#pragma unroll
-      for (int j = 0; j < BT; ++j) {
-        if (j >= A.B) break;
-        if (A.n_panels == 1) update(A, row, j, t[j]);
-        else A.partials[(static_cast<int64_t>(panel) * A.N + row) * A.B + j] = t[j];
-      }
-    }
-    ++g;
-  };
-  // Groups with no steps (rows with no edges in this panel) close at once.
-  auto skip_empty = [&]() {
-    while (g < g_end) {
-      open();
-      if (left > 0) break;
-      close();
-    }
-  };
-  skip_empty();
 
-  for (int b = 0; b * D < total; ++b) {
-    const int64_t ahead = first + static_cast<int64_t>(b + 1) * D * 64 + lane;
+  // One register block: prefetch the block after it into `ahead`, accumulate,
+  // then close the groups that ended.  A closed group's row sums go to the
+  // row-table-ordered buffer at the group's row-table entries (an address
+  // made of scalars and the lane id, so closing waits on no vector load).
+  auto block = [&](Slot (&here)[D], Slot (&ahead)[D], int b) {
+    const int64_t ahead0 = first + static_cast<int64_t>(b + 1) * D * 64;
 #pragma unroll
-    for (int k = 0; k < D; ++k) nxt[k] = load_slot<FMT>(A, ahead + 64 * k);
+    for (int k = 0; k < D; ++k) ahead[k] = load_slot<FMT>(A, ahead0 + lane, k);
+    const int rem = total - b * D;
+    uint32_t ends = rem < D ? bits & ((1u << rem) - 1u) : bits;
+    bits = boundary_bits<D>(A, ahead0 / 64);
+
+    float fin[D][BT];
 #pragma unroll
     for (int i = 0; i < D; ++i) {
-      if (b * D + i < total) {
-        const float w = decode_slot<FMT>(cur[i], lane, gscale);
-        if constexpr (BT == 1) {
-          acc[0] = __builtin_fmaf(w, lds_s[cur[i].c], acc[0]);
-        } else {
-          const v2f sv = *reinterpret_cast<const v2f*>(lds_s + 2 * cur[i].c);
-          acc[0] = __builtin_fmaf(w, sv.x, acc[0]);
-          acc[1] = __builtin_fmaf(w, sv.y, acc[1]);
-        }
-        if (--left == 0) {
-          close();
-          skip_empty();
-        }
+      const float w = decode_slot<FMT>(here[i], lane, gscale);
+      if constexpr (BT == 1) {
+        acc[0] = __builtin_fmaf(w, lds_s[here[i].c], acc[0]);
+      } else {
+        const v2f sv = *reinterpret_cast<const v2f*>(lds_s + 2 * here[i].c);
+        acc[0] = __builtin_fmaf(w, sv.x, acc[0]);
+        acc[1] = __builtin_fmaf(w, sv.y, acc[1]);
+      }
+      const bool end = (ends >> i) & 1u;
+#pragma unroll
+      for (int j = 0; j < BT; ++j) {
+        fin[i][j] = acc[j];
+        acc[j] = end ? 0.0f : acc[j];
       }
     }
+
+    while (ends) {
+      const int i = __builtin_ctz(ends);
+      ends &= ends - 1u;
+      float t[BT];
 #pragma unroll
-    for (int k = 0; k < D; ++k) cur[k] = nxt[k];
+      for (int j = 0; j < BT; ++j) t[j] = fin[0][j];
+#pragma unroll
+      for (int k = 1; k < D; ++k)
+        if (k == i) {
+#pragma unroll
+          for (int j = 0; j < BT; ++j) t[j] = fin[k][j];
+        }
+      const int lanes = 1 << now.lg;
+#pragma unroll
+      for (int j = 0; j < BT; ++j)
+        for (int off = 1; off < lanes; off <<= 1) t[j] += __shfl_xor(t[j], off, 64);
+      const int k = lane >> now.lg;
+      if ((lane & (lanes - 1)) == 0 && k < now.nrows) {
+#pragma unroll
+        for (int j = 0; j < BT; ++j)
+          A.sorted[(static_cast<int64_t>(now.rowtab) + k) * BT + j] = t[j];
+      }
+      ++g;
+      now = next;
+      if (g + 1 < g_end) next = load_group(A, g + 1);
+    }
+  };
+  for (int b = 0; b * D < total; b += 2) {
+    block(buf_a, buf_b, b);
+    if ((b + 1) * D >= total) break;
+    block(buf_b, buf_a, b + 1);
   }
+
+  // Map the tile's row-table-ordered sums back to rows: with one panel update
+  // the rows here, with several store this panel's partial sums by row.
+  __syncthreads();
+  auto finish_row = [&](int e, int r) {
+    const int64_t row = row0 + static_cast<int64_t>(r);
+#pragma unroll
+    for (int j = 0; j < BT; ++j) {
+      const float value = A.sorted[(static_cast<int64_t>(entry0) + e) * BT + j];
+      if (A.n_panels == 1) update(A, row, j, value);
+      else A.partials[(static_cast<int64_t>(panel) * A.N + row) * BT + j] = value;
+    }
+  };
+#pragma unroll
+  for (int k = 0; k < kRowsAhead; ++k) {
+    const int e = tid + k * kPanelThreads;
+    if (e < nrows) finish_row(e, rows_ahead[k]);
+  }
+  for (int e = tid + kRowsAhead * kPanelThreads; e < nrows; e += kPanelThreads)
+    finish_row(e, A.rows[entry0 + e]);
 }
 
 // Several panels: add each row's panel partial sums in panel order, then update.
@@ -295,16 +358,18 @@ int panel_step(const ns_step_args& a, hipStream_t stream) {
   if (pl.n_tiles < pl.n_panels || pl.n_groups < 0)
     return fail("panel plan needs at least one tile per panel");
   if (pl.n_slots < kPanelTailSlots) return fail("panel plan lacks its tail padding");
-  if (!pl.tiles || !pl.wave_groups || !pl.groups || !pl.rows || !pl.col || !pl.weight)
+  if (!pl.tiles || !pl.wave_groups || !pl.groups || !pl.rows || !pl.last_steps || !pl.col ||
+      !pl.weight)
     return fail("panel plan tables are required");
+  if (pl.n_step_words < pl.n_slots / 64 / 32 + 2) return fail("panel plan's step bitmap is short");
   if (a.matrix.format == NS_WEIGHT_NVFP4 && !pl.slot_scales)
     return fail("NVFP4 panels require per-slot block scales");
-  if (pl.n_panels > 1 && !pl.partials) return fail("several panels need the partials workspace");
+  if (!pl.partials) return fail("the panel path needs its partials workspace");
   const uintptr_t need = a.matrix.format == NS_WEIGHT_F32 ? 4 : a.matrix.format == NS_WEIGHT_F16 ? 2 : 1;
   if (reinterpret_cast<uintptr_t>(pl.col) % 2 || reinterpret_cast<uintptr_t>(pl.weight) % need)
     return fail("panel arrays are misaligned");
-  if (pl.partials) {
-    const Extent part = extent_of(pl.partials, 1, 1, 1, int64_t{pl.n_panels} * a.n_neurons * a.batch);
+  {
+    const Extent part = extent_of(pl.partials, 1, 1, 1, 2 * int64_t{pl.n_panels} * a.n_neurons * a.batch);
     const Extent outs[3] = {extent(a.out_state, a.batch, a.n_neurons),
                             extent(a.out_dendrite, a.batch, a.n_neurons),
                             extent(a.out_adaptation, a.batch, a.n_neurons)};
@@ -319,9 +384,11 @@ int panel_step(const ns_step_args& a, hipStream_t stream) {
   for (int i = 0; i < 6; ++i) A.p.v[i] = Vec{a.params[i].data, a.params[i].stride};
   A.width = pl.panel_width; A.n_panels = pl.n_panels;
   A.tiles = pl.tiles; A.wave_groups = pl.wave_groups; A.groups = pl.groups; A.rows = pl.rows;
+  A.last_steps = pl.last_steps;
   A.col = pl.col; A.weight = pl.weight; A.slot_scales = pl.slot_scales;
   A.gscale = a.matrix.global_scale;
   A.partials = pl.partials;
+  A.sorted = pl.partials + int64_t{pl.n_panels} * a.n_neurons * a.batch;
   A.os = out_plane(a.out_state); A.od = out_plane(a.out_dendrite);
   A.oa = out_plane(a.out_adaptation);
   const bool aligned = reinterpret_cast<uintptr_t>(a.state.data) % 16 == 0;

@@ -73,6 +73,7 @@ struct PanelLayout {
   int32_t panel_width = 0, n_panels = 0;
   std::vector<int32_t> tiles, wave_groups, groups, perm;
   std::vector<uint16_t> rows, col;
+  std::vector<uint32_t> last_steps;   // bit k: step k (slots 64k..64k+63) ends a group
 };
 
 int32_t log2_lanes(int64_t len, int32_t lane_target) {
@@ -89,8 +90,8 @@ struct Group {
 
 // Lays out tile (panel p, rows [r0, r1)): rows sorted by segment length
 // (descending, ties by row), cut into groups of 64 >> lg rows sharing one
-// lanes-per-row width, groups dealt to the waves longest-first onto the
-// least-loaded wave, then every wave's groups emitted back to back.
+// lanes-per-row width, groups dealt longest first onto the least-loaded of the
+// tile's wavefronts, then every wavefront's groups emitted back to back.
 void append_tile(PanelLayout& out, const int32_t* rowptr, const int32_t* col,
                  const std::vector<int32_t>& order, const std::vector<int32_t>& bucket,
                  int32_t P, int64_t width, int32_t p, int64_t r0, int64_t r1, int32_t waves,
@@ -112,8 +113,10 @@ void append_tile(PanelLayout& out, const int32_t* rowptr, const int32_t* col,
     int64_t n = 1;
     while (n < cap && i + n < nr && log2_lanes(seg_len(sorted[i + n]), lane_target) == lg) ++n;
     const int64_t lanes = int64_t{1} << lg;
-    groups.push_back(Group{lg, static_cast<int32_t>(n),
-                           static_cast<int32_t>((len + lanes - 1) / lanes),
+    // Every group takes at least one step (rows with no edges read one padding
+    // step), so each group ends on a step the boundary bitmap can mark.
+    const int64_t steps = std::max<int64_t>(1, (len + lanes - 1) / lanes);
+    groups.push_back(Group{lg, static_cast<int32_t>(n), static_cast<int32_t>(steps),
                            static_cast<int32_t>(i)});
     i += n;
   }
@@ -129,8 +132,8 @@ void append_tile(PanelLayout& out, const int32_t* rowptr, const int32_t* col,
     load[w] += groups[g].steps + 1;
     mine[w].push_back(g);
   }
-  const int32_t tile_index = static_cast<int32_t>(out.tiles.size() / 4);
-  const int32_t rec[4] = {p, static_cast<int32_t>(r0), static_cast<int32_t>(r1), tile_index};
+  const int32_t rec[4] = {p, static_cast<int32_t>(r0), static_cast<int32_t>(r1),
+                          static_cast<int32_t>(out.rows.size())};
   out.tiles.insert(out.tiles.end(), rec, rec + 4);
   for (int32_t w = 0; w < waves; ++w) {
     out.wave_groups.push_back(static_cast<int32_t>(out.groups.size() / 4));
@@ -140,6 +143,10 @@ void append_tile(PanelLayout& out, const int32_t* rowptr, const int32_t* col,
       const int32_t rec_g[4] = {static_cast<int32_t>(out.perm.size()), grp.steps,
                                 grp.lg | (grp.nrows << 8), static_cast<int32_t>(out.rows.size())};
       out.groups.insert(out.groups.end(), rec_g, rec_g + 4);
+      const int64_t last = static_cast<int64_t>(out.perm.size()) / 64 + grp.steps - 1;
+      if (static_cast<int64_t>(out.last_steps.size()) <= last / 32)
+        out.last_steps.resize(last / 32 + 1, 0u);
+      out.last_steps[last / 32] |= 1u << (last % 32);
       for (int32_t k = 0; k < grp.nrows; ++k)
         out.rows.push_back(static_cast<uint16_t>(sorted[grp.first + k] - r0));
       // Step-major slots: lane l = (row k, part j) takes the row's edges j, j+lanes, ...
@@ -224,6 +231,9 @@ int build_panels(const int32_t* rowptr, const int32_t* col, int64_t n, int32_t m
   }
   if (static_cast<int64_t>(out.perm.size()) >= (int64_t{1} << 31))
     return fail("panel layout needs 2^31 or more slots");
+  // One word per 32 steps of the whole slot array, plus one spare word so a
+  // 64-bit read at any step stays inside.
+  out.last_steps.resize(static_cast<int64_t>(out.perm.size()) / 64 / 32 + 2, 0u);
   return NS_OK;
 }
 
@@ -233,7 +243,8 @@ extern "C" int ns_plan_panels(const int32_t* rowptr, const int32_t* col, int64_t
                               int32_t max_panel_width, int32_t tiles_per_panel, int32_t waves,
                               int32_t lane_target, ns_panel_plan* plan, int64_t* n_row_entries,
                               int32_t* tiles, int32_t* wave_groups, int32_t* groups,
-                              uint16_t* rows, int32_t* perm, uint16_t* col_out) {
+                              uint16_t* rows, uint32_t* last_steps, int32_t* perm,
+                              uint16_t* col_out) {
   clear_error();
   if (!rowptr || !plan || !n_row_entries) return fail("rowptr, plan and n_row_entries are required");
   if (n_rows <= 0 || n_rows >= (int64_t{1} << 31)) return fail("N must be in [1, 2^31)");
@@ -256,11 +267,13 @@ extern "C" int ns_plan_panels(const int32_t* rowptr, const int32_t* col, int64_t
   plan->n_groups = static_cast<int32_t>(layout.groups.size() / 4);
   plan->waves = waves;
   plan->n_slots = static_cast<int64_t>(layout.perm.size());
+  plan->n_step_words = static_cast<int64_t>(layout.last_steps.size());
   *n_row_entries = static_cast<int64_t>(layout.rows.size());
   if (tiles) std::copy(layout.tiles.begin(), layout.tiles.end(), tiles);
   if (wave_groups) std::copy(layout.wave_groups.begin(), layout.wave_groups.end(), wave_groups);
   if (groups) std::copy(layout.groups.begin(), layout.groups.end(), groups);
   if (rows) std::copy(layout.rows.begin(), layout.rows.end(), rows);
+  if (last_steps) std::copy(layout.last_steps.begin(), layout.last_steps.end(), last_steps);
   if (perm) std::copy(layout.perm.begin(), layout.perm.end(), perm);
   if (col_out) std::copy(layout.col.begin(), layout.col.end(), col_out);
   return NS_OK;

@@ -35,7 +35,7 @@ import numpy as np
 import torch
 
 _LIB_NAME = "libneurosim_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 WEIGHT_F32, WEIGHT_F16, WEIGHT_E4M3, WEIGHT_NVFP4 = 0, 1, 2, 3
 _PLAN_CACHE = 64   # row plans kept per extension (one per live topology and batch width)
@@ -72,8 +72,9 @@ class _PanelPlan(ctypes.Structure):
     _fields_ = [("panel_width", ctypes.c_int32), ("n_panels", ctypes.c_int32),
                 ("n_tiles", ctypes.c_int32), ("n_groups", ctypes.c_int32),
                 ("waves", ctypes.c_int32), ("reserved", ctypes.c_int32 * 3), ("n_slots", _c_i64),
-                ("tiles", _c_ptr), ("wave_groups", _c_ptr), ("groups", _c_ptr), ("rows", _c_ptr),
-                ("col", _c_ptr), ("weight", _c_ptr), ("slot_scales", _c_ptr), ("partials", _c_ptr)]
+                ("n_step_words", _c_i64), ("tiles", _c_ptr), ("wave_groups", _c_ptr),
+                ("groups", _c_ptr), ("rows", _c_ptr), ("last_steps", _c_ptr), ("col", _c_ptr),
+                ("weight", _c_ptr), ("slot_scales", _c_ptr), ("partials", _c_ptr)]
 
 
 class _StepArgs(ctypes.Structure):
@@ -135,7 +136,7 @@ def load_library() -> ctypes.CDLL:
     lib.ns_plan_panels.restype = ctypes.c_int
     lib.ns_plan_panels.argtypes = [_c_ptr, _c_ptr, _c_i64, ctypes.c_int32, ctypes.c_int32,
                                    ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(_PanelPlan),
-                                   ctypes.POINTER(_c_i64)] + [_c_ptr] * 6
+                                   ctypes.POINTER(_c_i64)] + [_c_ptr] * 7
     for name, kind in (("ns_dendritic_step", _StepArgs), ("ns_dendritic_event", _EventArgs),
                        ("ns_csr_spmm", _SpmmArgs)):
         fn = getattr(lib, name)
@@ -238,7 +239,7 @@ def panel_geometry(batch: int) -> tuple[int, int]:
     return width.value, waves.value
 
 
-LANE_TARGET = 12   # at most this many edges per lane before a row gets more lanes
+LANE_TARGET = 24   # at most this many edges per lane before a row gets more lanes
 
 
 def plan_panels_host(rowptr: torch.Tensor, col: torch.Tensor, batch: int, tiles_per_panel: int,
@@ -256,17 +257,18 @@ def plan_panels_host(rowptr: torch.Tensor, col: torch.Tensor, batch: int, tiles_
     args = (rowptr.ctypes.data, col.ctypes.data if col.size else None, n, width,
             int(tiles_per_panel), waves, int(lane_target), ctypes.byref(plan),
             ctypes.byref(entries))
-    _raise_on(lib.ns_plan_panels(*args, *([None] * 6)), lib)
+    _raise_on(lib.ns_plan_panels(*args, *([None] * 7)), lib)
     tiles = np.empty(4 * plan.n_tiles, np.int32)
     wave_groups = np.empty(plan.n_tiles * plan.waves + 1, np.int32)
     groups = np.empty(4 * plan.n_groups, np.int32)
     rows = np.empty(entries.value, np.uint16)
+    last_steps = np.empty(plan.n_step_words, np.uint32)
     perm = np.empty(plan.n_slots, np.int32)
     cols = np.empty(plan.n_slots, np.uint16)
     _raise_on(lib.ns_plan_panels(*args, tiles.ctypes.data, wave_groups.ctypes.data,
-                                 groups.ctypes.data, rows.ctypes.data, perm.ctypes.data,
-                                 cols.ctypes.data), lib)
-    return plan, tiles, wave_groups, groups, rows, perm, cols
+                                 groups.ctypes.data, rows.ctypes.data, last_steps.ctypes.data,
+                                 perm.ctypes.data, cols.ctypes.data), lib)
+    return plan, tiles, wave_groups, groups, rows, last_steps, perm, cols
 
 
 def _device_tensor(array: np.ndarray, device) -> torch.Tensor:
@@ -294,7 +296,7 @@ class PanelLayout:
             # One workgroup per compute unit in total.
             units = torch.cuda.get_device_properties(device).multi_processor_count
             tiles_per_panel = max(1, units // panels)
-        plan, tiles, wave_groups, groups, rows, perm, cols = plan_panels_host(
+        plan, tiles, wave_groups, groups, rows, last_steps, perm, cols = plan_panels_host(
             topology.in_rowptr, topology.in_col, batch, tiles_per_panel, max_panel_width,
             lane_target)
         self.batch, self.n = int(batch), n
@@ -305,12 +307,14 @@ class PanelLayout:
         self.wave_groups = _device_tensor(wave_groups, device)
         self.groups = _device_tensor(groups, device)
         self.rows = _device_tensor(rows if rows.size else np.zeros(1, np.uint16), device)
+        self.last_steps = _device_tensor(last_steps.view(np.int32), device)
         self.col = _device_tensor(cols, device)
         perm_t = torch.from_numpy(perm).to(device)
         self.valid = perm_t >= 0
         self.perm = perm_t.clamp_min(0).to(torch.int64)
-        self.partials = (torch.empty(plan.n_panels * n * batch, dtype=torch.float32, device=device)
-                         if plan.n_panels > 1 else None)
+        # per-panel sums by row, then the same sums in row-table order
+        self.partials = torch.empty(2 * plan.n_panels * n * batch, dtype=torch.float32,
+                                    device=device)
         self._plan = plan
         self._slot_weights: tuple | None = None
         self._slot_key = None
@@ -350,10 +354,11 @@ class PanelLayout:
         ctypes.memmove(ctypes.addressof(plan), ctypes.addressof(self._plan), ctypes.sizeof(plan))
         plan.tiles, plan.wave_groups = self.tiles.data_ptr(), self.wave_groups.data_ptr()
         plan.groups, plan.rows = self.groups.data_ptr(), self.rows.data_ptr()
+        plan.last_steps = self.last_steps.data_ptr()
         plan.col = self.col.data_ptr()
         plan.weight = slot_weight.data_ptr()
         plan.slot_scales = slot_scales.data_ptr() if slot_scales is not None else None
-        plan.partials = self.partials.data_ptr() if self.partials is not None else None
+        plan.partials = self.partials.data_ptr()
         return plan
 
 

@@ -1,8 +1,8 @@
 """The column-panel layout (ns_plan_panels) on the host: invariants, and a numpy
 emulation of the panel kernel's decomposition against the plain CSR product.
 
-The emulation walks every wavefront's stream exactly as the kernel does
-(register blocks of up to 16 steps, prefetch of the next block) and checks
+The emulation walks every wavefront's stream as the kernel does (register
+blocks of up to 16 steps, prefetch of the next block) and checks
 that every slot the kernel reads lies inside the slot arrays, that every edge
 lands in exactly one slot of its row and panel, that each (panel, row) is
 finished exactly once, and that the per-lane sums plus the lane butterfly
@@ -41,8 +41,8 @@ GRAPHS = {
 
 
 def emulate(graph: otop.Graph, batch: int, tiles_per_panel: int, width: int | None,
-            source: np.ndarray, lane_target: int = 12):
-    plan, tiles, wave_groups, groups, rows, perm, cols = plan_panels_host(
+            source: np.ndarray, lane_target: int = 24):
+    plan, tiles, wave_groups, groups, rows, last_steps, perm, cols = plan_panels_host(
         torch.from_numpy(graph.in_rowptr), torch.from_numpy(graph.in_col), batch, tiles_per_panel,
         width, lane_target)
     n, m = graph.n, graph.n_edges
@@ -52,14 +52,20 @@ def emulate(graph: otop.Graph, batch: int, tiles_per_panel: int, width: int | No
     assert W % 4 == 0 and W <= min(cap, width or cap)
     assert P * W >= n > (P - 1) * W
     assert perm.size == cols.size == plan.n_slots
+    assert last_steps.size == plan.n_slots // 64 // 32 + 2
+    step_ends = np.unpackbits(last_steps.view(np.uint8), bitorder="little").astype(bool)
+    marked = np.zeros_like(step_ends)
     tiles = tiles.reshape(-1, 4)
     groups = groups.reshape(-1, 4)
     assert wave_groups.size == plan.n_tiles * waves + 1 and wave_groups[0] == 0
     assert wave_groups[-1] == plan.n_groups and np.all(np.diff(wave_groups) >= 0)
     covered = np.zeros((P, n), dtype=np.int64)
-    for panel, r0, r1, index in tiles:
+    for panel, r0, r1, entry0 in tiles:
         assert 0 <= r0 < r1 <= n and r1 - r0 <= 65536
         covered[panel, r0:r1] += 1
+        # the tile's row-table entries are contiguous and list each of its rows once
+        assert np.array_equal(np.sort(rows[entry0:entry0 + r1 - r0].astype(np.int64)),
+                              np.arange(r1 - r0))
     assert np.all(covered == 1), "each panel's tiles partition the rows"
 
     rows_of_edge = np.repeat(np.arange(n), np.diff(graph.in_rowptr))
@@ -67,7 +73,7 @@ def emulate(graph: otop.Graph, batch: int, tiles_per_panel: int, width: int | No
     written = np.zeros((P, n), dtype=np.int64)
     seen = np.zeros(m, dtype=np.int64)
     last_stream_end = 0
-    for t, (panel, r0, r1, _) in enumerate(tiles):
+    for t, (panel, r0, r1, _) in enumerate(tiles):   # _: the tile's first row-table entry
         for w in range(waves):
             g0, g1 = wave_groups[t * waves + w], wave_groups[t * waves + w + 1]
             if g0 == g1:
@@ -84,7 +90,8 @@ def emulate(graph: otop.Graph, batch: int, tiles_per_panel: int, width: int | No
                 lg, nrows = packed & 255, packed >> 8
                 lanes = 1 << lg
                 assert slot0 == slot and slot0 % 64 == 0, "a wave's groups are contiguous"
-                assert 0 <= lg <= 6 and 1 <= nrows <= 64 >> lg and steps >= 0
+                assert 0 <= lg <= 6 and 1 <= nrows <= 64 >> lg and steps >= 1
+                marked[slot0 // 64 + steps - 1] = True
                 block = np.arange(slot0, slot0 + 64 * steps).reshape(steps, 64)
                 edges = perm[block]
                 srcs = cols[block].astype(np.int64)
@@ -96,7 +103,7 @@ def emulate(graph: otop.Graph, batch: int, tiles_per_panel: int, width: int | No
                         assert np.all(lane_edges < 0)
                         continue
                     row = r0 + int(rows[rowtab + k])
-                    assert r0 <= row < r1
+                    assert r0 <= row < r1 and _ <= rowtab + k < _ + r1 - r0
                     mine = lane_edges.T          # [lane j, step]: edges j, j+lanes, ...
                     order = lane_edges.reshape(-1)
                     real = order[order >= 0]
@@ -115,6 +122,7 @@ def emulate(graph: otop.Graph, batch: int, tiles_per_panel: int, width: int | No
                     partial[panel, row] = lane_sums[0]
                     written[panel, row] += 1
                 slot += 64 * steps
+    assert np.array_equal(marked, step_ends), "the bitmap marks exactly each group's last step"
     assert np.all(seen == 1), "every edge lands in exactly one slot"
     assert np.all(written == 1), "every (panel, row) is finished exactly once"
     tail = perm[last_stream_end:]
@@ -141,7 +149,7 @@ def test_panel_layout_reproduces_the_csr_product(name, batch, tiles, width):
 
 def test_lane_widths_follow_segment_length():
     graph = hub_graph(12_000, 2)
-    plan, tiles, wave_groups, groups, rows, perm, cols = plan_panels_host(
+    plan, tiles, wave_groups, groups, rows, last_steps, perm, cols = plan_panels_host(
         torch.from_numpy(graph.in_rowptr), torch.from_numpy(graph.in_col), 1, 4)
     lg = groups.reshape(-1, 4)[:, 2] & 255
     assert lg.max() == 6, "the 9000-edge hub row takes a whole wavefront"
@@ -150,10 +158,9 @@ def test_lane_widths_follow_segment_length():
 
 def test_waves_are_balanced_within_a_tile():
     graph = otop.random_graph(20_000, 1_000_000, seed=4)
-    plan, tiles, wave_groups, groups, rows, perm, cols = plan_panels_host(
+    plan, tiles, wave_groups, groups, rows, last_steps, perm, cols = plan_panels_host(
         torch.from_numpy(graph.in_rowptr), torch.from_numpy(graph.in_col), 1, 8)
-    groups = groups.reshape(-1, 4)
-    cost = groups[:, 1] + 1
+    cost = groups.reshape(-1, 4)[:, 1] + 1
     for t in range(plan.n_tiles):
         loads = [cost[wave_groups[t * 16 + w]: wave_groups[t * 16 + w + 1]].sum() for w in range(16)]
         assert max(loads) <= 1.1 * np.mean(loads) + max(cost)
@@ -170,9 +177,9 @@ def test_planner_rejects_bad_geometry():
     import ctypes
 
     rc = lib.ns_plan_panels(rowptr.ctypes.data, col.ctypes.data, 2, 64, 1, 16, 12,
-                            ctypes.byref(plan), ctypes.byref(entries), *([None] * 6))
+                            ctypes.byref(plan), ctypes.byref(entries), *([None] * 7))
     assert rc != 0 and b"out of range" in lib.ns_last_error()
     col = np.array([0, 1], np.int32)
     rc = lib.ns_plan_panels(rowptr.ctypes.data, col.ctypes.data, 2, 64, 1, 8, 12,
-                            ctypes.byref(plan), ctypes.byref(entries), *([None] * 6))
+                            ctypes.byref(plan), ctypes.byref(entries), *([None] * 7))
     assert rc != 0 and b"wavefronts" in lib.ns_last_error()
