@@ -11,7 +11,12 @@ fp16, fp8 e4m3 and nvfp4 weight storage.
 Prints one JSON line.  ``value`` is ms per fp32 tick (lower is better);
 ``roofline`` prices the fp32 tick's algorithmic bytes against MI355X's 8 TB/s;
 ``cpu_baseline`` times the CPU oracle (the reference's float32 torch CPU path,
-restated) on a bounded sample of the same tick on this host.
+restated) on a bounded sample of the same tick on this host.  ``configs``
+adds the other workloads, each timed the same way: the batched tick
+(N=50000, M~1M, B=8, per-column drive), the PELS event tick (N=50000, M~1M,
+B=1, theta 0.02, driven and with inputs withdrawn) and the scale-out tick
+(N=1000000, M~100M, B=16, fp8 weights, 200 graph-captured ticks, with the
+CPU oracle on a 10-tick sample).
 
     python bench.py [--gpus 1] [--steps 1000] [--warmup 50]
 """
@@ -31,7 +36,8 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "neurosim-gpu_amd"))
 
 from neurosim_gpu import (DendriticDynamics, Dynamics, MatrixRollout,  # noqa: E402
-                          NativeDendriticMatrixRuntime, random_topology, topology_to)
+                          NativeDendriticMatrixRuntime, NativeDendriticPELSRuntime,
+                          random_topology, topology_to)
 
 N_NEURONS, CANDIDATES, SEED, BATCH = 166_000, 25_000_000, 0, 1
 HBM_PEAK_GBPS = 8000.0
@@ -83,7 +89,10 @@ def time_ticks(runtime, steps: int, warmup: int) -> tuple[float, MatrixRollout]:
     tail_rollout = (MatrixRollout(runtime, tail - tail % 2, drive=0.2, dendritic_drive=0.1)
                     if tail >= 2 else None)
     odd = tail % 2
-    rollout.run(warmup // chunk)
+    # Every graph is replayed once before the timed region (the first replay uploads it).
+    rollout.run(max(1, warmup // chunk))
+    if tail_rollout is not None:
+        tail_rollout.run()
     for _ in range(warmup % chunk):
         runtime.step(0.2, dendritic_drive=0.1)
     torch.cuda.synchronize()
@@ -118,8 +127,29 @@ def mall_flushed_ms(rollout: MatrixRollout, ticks: int = 20) -> float:
     return total / ticks
 
 
-def cpu_baseline(topology_cpu, model_cpu, ticks: int = 20) -> dict:
-    """The CPU oracle's float32 tick on this host (bounded sample, all cores)."""
+def standard_model(n: int, device):
+    """alpha .72, gain .8, dt 1, tau_d 4, tau_a 25, coupling .5, strength .2
+    (rho = exp(-dt/tau) computed on the host), as (host model, device model)."""
+    soma = Dynamics(torch.full((n,), .72), torch.full((n,), .8))
+    model_cpu = DendriticDynamics.from_time_constants(soma, dt=1., tau_dendrite=4.,
+                                                      tau_adaptation=25., coupling=.5,
+                                                      adaptation_strength=.2)
+    model = DendriticDynamics(Dynamics(soma.alpha.to(device), soma.gain.to(device)),
+                              model_cpu.dendrite_decay.to(device),
+                              model_cpu.adaptation_decay.to(device),
+                              model_cpu.coupling.to(device),
+                              model_cpu.adaptation_strength.to(device))
+    return model_cpu, model
+
+
+def column_drive(batch: int, seed: int = 1) -> torch.Tensor:
+    """Per-column somatic drive U(0, 0.4) of shape [B, 1] from a host generator."""
+    return torch.rand((batch, 1), generator=torch.Generator().manual_seed(seed)) * 0.4
+
+
+def oracle_tick_ms(topology_cpu, model_cpu, batch: int, drive, ticks: int, warmup: int = 3,
+                   weight=None) -> tuple[float, int]:
+    """ms per float32 tick of the CPU oracle (all host threads)."""
     sys.path.insert(0, str(ROOT))
     from oracle import dynamics as od
     from oracle import runtime as ort
@@ -136,13 +166,19 @@ def cpu_baseline(topology_cpu, model_cpu, ticks: int = 20) -> dict:
     cores = os.cpu_count() or 1
     threads = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
     torch.set_num_threads(threads)
-    oracle = ort.MatrixOracle(graph, params, torch.zeros(BATCH, N_NEURONS))
-    for _ in range(3):
-        oracle.step(0.2, 0.1)
+    oracle = ort.MatrixOracle(graph, params, torch.zeros(batch, topology_cpu.n_neurons),
+                              in_weight=weight)
+    for _ in range(warmup):
+        oracle.step(drive, 0.1)
     begin = time.perf_counter()
     for _ in range(ticks):
-        oracle.step(0.2, 0.1)
-    ms = (time.perf_counter() - begin) * 1000 / ticks
+        oracle.step(drive, 0.1)
+    return (time.perf_counter() - begin) * 1000 / ticks, threads
+
+
+def cpu_baseline(topology_cpu, model_cpu, ticks: int = 20) -> dict:
+    """The CPU oracle's float32 tick on this host (bounded sample, all cores)."""
+    ms, threads = oracle_tick_ms(topology_cpu, model_cpu, BATCH, 0.2, ticks)
     return {"value": round(ms, 3), "unit": "ms/tick", "cores": threads, "kind": "port",
             "sample": f"{ticks} fp32 ticks (after 3 warm-up) of the same N=166000 M=24988875 B=1 "
                       f"graph, torch CPU CSR product + elementwise update, {threads} threads"}
@@ -160,6 +196,145 @@ def measured_traffic(fmt: str) -> float | None:
     return None
 
 
+def rollout_ms(runtime, ticks: int, repeats: int, drive, dendritic_drive) -> float:
+    """ms per tick of `repeats` replays of one graph of `ticks` matrix ticks."""
+    rollout = MatrixRollout(runtime, ticks, drive=drive, dendritic_drive=dendritic_drive)
+    rollout.run(1)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    rollout.run(repeats)
+    end.record()
+    torch.cuda.synchronize()
+    if not bool(torch.isfinite(rollout.state).all()):
+        raise RuntimeError("non-finite state after the timed ticks")
+    return start.elapsed_time(end) / (ticks * repeats)
+
+
+def measure_batched(device) -> dict:
+    """N=50000, M~1M, B=8, drive [8,1] U(0,.4) (seed 1), dendritic .1, fp32, 1000 ticks."""
+    n, candidates, batch = 50_000, 1_000_000, 8
+    topology_cpu = random_topology(n, candidates, device="cpu", seed=0)
+    m = topology_cpu.n_edges
+    _, model = standard_model(n, device)
+    runtime = NativeDendriticMatrixRuntime(topology_to(topology_cpu, device), model,
+                                           torch.zeros(batch, n, device=device))
+    ms = rollout_ms(runtime, 100, 10, column_drive(batch).to(device), 0.1)
+    alg = algorithmic_bytes("fp32", n, m, batch) + 4 * batch
+    return {"workload": f"dendritic matrix tick, N={n} M={m} B={batch}, fp32 weights, "
+                        "per-column drive", "kernel": runtime.kernel,
+            "ms_per_tick": round(ms, 5), "algorithmic_bytes": alg,
+            "achieved_GBps": round(alg / ms / 1e6, 1),
+            "pct_hbm_peak": round(100 * alg / ms / 1e6 / HBM_PEAK_GBPS, 1)}
+
+
+def measure_pels(device, theta: float = 0.02) -> dict:
+    """N=50000, M~1M, B=1: ms/tick of the two-kernel event tick in graphs of 64
+    ticks, for three activity regimes: drive .2/.1 switched on at a zero state,
+    both inputs withdrawn after 512 driven ticks, and quiescence after 4096
+    withdrawn ticks.  Each regime's activity (emitting sources and pushed
+    edges per tick) is counted on an eager run of the same 64 ticks."""
+    n, candidates, chunk = 50_000, 1_000_000, 64
+    topology_cpu = random_topology(n, candidates, device="cpu", seed=0)
+    topology = topology_to(topology_cpu, device)
+    _, model = standard_model(n, device)
+    runtime = NativeDendriticPELSRuntime(topology, model, torch.zeros(1, n, device=device),
+                                         theta=theta)
+    out_degree = (topology.out_rowptr[1:] - topology.out_rowptr[:-1]).to(torch.int64)
+    fields = ("state", "dendritic_state", "adaptation_state", "emitted_state",
+              "persistent_current")
+    result = {"workload": f"PELS event tick, N={n} M={topology_cpu.n_edges} B=1, theta {theta}",
+              "ticks_per_graph": chunk}
+
+    def phase(drive: float, dendritic: float) -> dict:
+        with torch.inference_mode():
+            saved = [getattr(runtime, f).clone() for f in fields]
+            sources = edges = 0
+            for _ in range(chunk):
+                before = runtime.emitted_state
+                runtime.step(drive, dendritic_drive=dendritic)
+                changed = runtime.emitted_state[0] != before[0]
+                sources += int(changed.sum())
+                edges += int(out_degree[changed].sum())
+            for f, value in zip(fields, saved):
+                setattr(runtime, f, value.clone())
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                runtime.step(drive, dendritic_drive=dendritic)
+            torch.cuda.current_stream().wait_stream(side)
+            for f, value in zip(fields, saved):
+                setattr(runtime, f, value.clone())
+            # The graph's first tick reads these input tensors again on every replay;
+            # only the persistent current is updated in place, so it is reset each time.
+            current = runtime.persistent_current
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for _ in range(chunk):
+                    runtime.step(drive, dendritic_drive=dendritic)
+            timings = []
+            for _ in range(8):
+                current.copy_(saved[-1])
+                start = torch.cuda.Event(enable_timing=True)
+                end = torch.cuda.Event(enable_timing=True)
+                start.record()
+                graph.replay()
+                end.record()
+                end.synchronize()
+                timings.append(start.elapsed_time(end) / chunk)
+            for f, value in zip(fields, saved):
+                setattr(runtime, f, value)
+        ms = sorted(timings)[len(timings) // 2]
+        per_tick_sources, per_tick_edges = sources / chunk, edges / chunk
+        alg = int(44 * n + 28 * n + 8 * per_tick_sources + 20 * per_tick_edges)
+        return {"ms_per_tick": round(ms, 5), "emitting_sources_per_tick": round(per_tick_sources, 1),
+                "pushed_edges_per_tick": round(per_tick_edges, 1), "algorithmic_bytes": alg,
+                "achieved_GBps": round(alg / ms / 1e6, 1)}
+
+    result["driven_onset"] = phase(0.2, 0.1)
+    with torch.inference_mode():
+        for _ in range(512):
+            runtime.step(0.2, dendritic_drive=0.1)
+    result["withdrawn_onset"] = phase(0.0, 0.0)
+    with torch.inference_mode():
+        for _ in range(4096):
+            runtime.step(0.0, dendritic_drive=0.0)
+    result["quiescent"] = phase(0.0, 0.0)
+    return result
+
+
+def measure_scaleout(device, cpu_sample: bool) -> dict:
+    """N=1000000, M~100M, B=16, drive [16,1] U(0,.4) (seed 1), fp8 e4m3 weights,
+    200 graph-captured ticks; CPU oracle (fp32, decoded weights) on 10 ticks."""
+    n, candidates, batch = 1_000_000, 100_000_000, 16
+    log("scale-out: building N=1000000 M=100M graph on the host")
+    topology_cpu = random_topology(n, candidates, device="cpu", seed=0)
+    m = topology_cpu.n_edges
+    model_cpu, model = standard_model(n, device)
+    runtime = NativeDendriticMatrixRuntime(topology_to(topology_cpu, device), model,
+                                           torch.zeros(batch, n, device=device), weight_format="fp8")
+    drive = column_drive(batch)
+    ms = rollout_ms(runtime, 100, 2, drive.to(device), 0.1)
+    alg = algorithmic_bytes("fp8", n, m, batch) + 4 * batch
+    result = {"workload": f"dendritic matrix tick, N={n} M={m} B={batch}, fp8 e4m3 weights, "
+                          "per-column drive", "kernel": runtime.kernel, "ticks": 200,
+              "ms_per_tick": round(ms, 5), "algorithmic_bytes": alg,
+              "achieved_GBps": round(alg / ms / 1e6, 1),
+              "pct_hbm_peak": round(100 * alg / ms / 1e6 / HBM_PEAK_GBPS, 1)}
+    if cpu_sample:
+        log("scale-out: timing the CPU oracle on 10 ticks")
+        from neurosim_gpu.precision import quantize_dequantize
+        decoded = quantize_dequantize(topology_cpu.in_weight, "fp8").numpy()
+        cpu_ms, threads = oracle_tick_ms(topology_cpu, model_cpu, batch, drive, 10, warmup=1,
+                                         weight=decoded)
+        result["cpu_baseline"] = {"value": round(cpu_ms, 1), "unit": "ms/tick", "cores": threads,
+                                  "kind": "port", "sample": "10 fp32 ticks on the decoded fp8 "
+                                  "weights, torch CPU CSR product + elementwise update"}
+    del runtime
+    torch.cuda.empty_cache()
+    return result
+
+
 def main() -> None:
     cli = argparse.ArgumentParser(description=__doc__)
     cli.add_argument("--gpus", type=int, default=1)
@@ -172,6 +347,8 @@ def main() -> None:
                      help="tick kernel: LDS column panels (batch 1-2) or CSR row blocks")
     cli.add_argument("--copy-calibration", action="store_true",
                      help="only run 256 MiB device copies (PMC byte-counter calibration)")
+    cli.add_argument("--configs", default="batched,pels,scaleout",
+                     help="other workloads to time after the headline one ('none' for none)")
     args = cli.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -188,16 +365,8 @@ def main() -> None:
     log("building graph on the host")
     topology_cpu = random_topology(N_NEURONS, CANDIDATES, device="cpu", seed=SEED)
     m = topology_cpu.n_edges
-    soma = Dynamics(torch.full((N_NEURONS,), .72), torch.full((N_NEURONS,), .8))
-    model_cpu = DendriticDynamics.from_time_constants(soma, dt=1., tau_dendrite=4.,
-                                                      tau_adaptation=25., coupling=.5,
-                                                      adaptation_strength=.2)
+    model_cpu, model = standard_model(N_NEURONS, device)
     topology = topology_to(topology_cpu, device)
-    model = DendriticDynamics(Dynamics(soma.alpha.to(device), soma.gain.to(device)),
-                              model_cpu.dendrite_decay.to(device),
-                              model_cpu.adaptation_decay.to(device),
-                              model_cpu.coupling.to(device),
-                              model_cpu.adaptation_strength.to(device))
     results = {}
     flushed = None
     for fmt in args.formats.split(","):
@@ -239,6 +408,22 @@ def main() -> None:
     if not args.no_cpu_baseline:
         log("timing the CPU oracle")
         line["cpu_baseline"] = cpu_baseline(topology_cpu, model_cpu)
+    del topology
+    torch.cuda.empty_cache()
+    extra = {}
+    for name in [c for c in args.configs.split(",") if c and c != "none"]:
+        log(f"timing {name}")
+        if name == "batched":
+            extra[name] = measure_batched(device)
+        elif name == "pels":
+            extra[name] = measure_pels(device)
+        elif name == "scaleout":
+            extra[name] = measure_scaleout(device, not args.no_cpu_baseline)
+        else:
+            cli.error(f"unknown config {name}")
+        log(f"{name}: {extra[name]}")
+    if extra:
+        line["configs"] = extra
     print(json.dumps(line), flush=True)
 
 

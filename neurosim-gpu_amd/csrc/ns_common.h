@@ -86,30 +86,28 @@ __device__ __forceinline__ NextState advance_one(const Params& p, int64_t n, flo
   return out;
 }
 
-// OCP fp8 e4m3fn -> float32, exact.  The e4m3 bit fields shifted into an IEEE
-// binary16 (1-5-10) give the same significand with an exponent bias of 15
-// instead of 7, so the binary16 value times 2^8 is the e4m3 value; binary16
-// subnormals cover the e4m3 subnormals exactly.  Codes 0x7F/0xFF are NaN.
+// OCP fp8 e4m3fn -> float32, exact (bias 7, subnormals, 0x7F/0xFF NaN): the
+// gfx950 conversion instruction, which decodes the OCP format; every one of
+// the 256 codes is checked against the oracle's decoder by the GPU tests.
 __device__ __forceinline__ float e4m3_to_float(uint32_t code) {
-  const uint16_t bits = static_cast<uint16_t>(((code & 0x80u) << 8) | ((code & 0x7Fu) << 7));
-  const _Float16 h = __builtin_bit_cast(_Float16, bits);
-  const float value = static_cast<float>(h) * 256.0f;
-  return (code & 0x7Fu) == 0x7Fu ? __builtin_nanf("") : value;
+  return __builtin_amdgcn_cvt_f32_fp8(static_cast<int>(code), 0);
 }
 
-// e2m1 magnitude of a 3-bit code: 0, 0.5, 1, 1.5, 2, 3, 4, 6.  Twice the
-// magnitude is a small integer; the nibble table below packs those integers.
-__device__ __forceinline__ float e2m1_magnitude(uint32_t code3) {
-  constexpr uint32_t kTwice = 0xC8643210u;
-  return 0.5f * static_cast<float>((kTwice >> (code3 * 4u)) & 15u);
+// The signed e2m1 values (0, 0.5, 1, 1.5, 2, 3, 4, 6; bit 3 the sign) of the
+// two nibbles of `byte` (low nibble first), via the gfx950 conversion with a
+// unit scale, which is exact.
+typedef float ns_v2f __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ ns_v2f e2m1_pair(uint32_t byte) {
+  return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(byte, 1.0f, 0);
 }
 
 // Decoded weight of an NVFP4 nibble given its block scale already decoded and
-// multiplied by the global scale (one float32 rounding, as in the reference's
-// levels[code & 7] * (block.float() * global); precision.py:109).
+// multiplied by the global scale: the signed level times that product, one
+// float32 rounding, as in the reference's levels[code & 7] * (block.float() *
+// global) with the sign applied after (precision.py:109-110; negation commutes
+// with the rounding).
 __device__ __forceinline__ float nvfp4_weight(uint32_t nibble, float block_times_global) {
-  const float magnitude = e2m1_magnitude(nibble & 7u) * block_times_global;
-  return (nibble & 8u) ? -magnitude : magnitude;
+  return e2m1_pair(nibble & 15u).x * block_times_global;
 }
 
 }  // namespace ns

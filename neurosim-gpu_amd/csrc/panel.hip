@@ -21,8 +21,8 @@
 //    sums are only snapshotted there, and after the block the groups that
 //    ended are closed in order (xor butterfly over the row's lanes, one lane
 //    per row stores the sum at the group's row-table entries);
-//  * after its streams the workgroup maps row-table entries back to rows:
-//    with one panel it updates its own rows, with several it stores the
+//  * after its stream each wavefront maps its row-table entries back to rows:
+//    with one panel it updates those rows, with several it stores the
 //    panel's partial sums by row and a second kernel adds them in panel
 //    order and applies the update.
 //
@@ -113,8 +113,8 @@ __device__ __forceinline__ float decode_slot(const Slot& x, int lane, float gsca
   } else if constexpr (FMT == NS_WEIGHT_E4M3) {
     return e4m3_to_float(x.w) * gscale;
   } else {
-    const uint32_t nibble = (x.w >> ((lane & 1) * 4)) & 15u;
-    return nvfp4_weight(nibble, e4m3_to_float(x.sc) * gscale);
+    const ns_v2f pair = e2m1_pair(x.w & 0xFFu);
+    return ((lane & 1) ? pair.y : pair.x) * (e4m3_to_float(x.sc) * gscale);
   }
 }
 
@@ -149,14 +149,13 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
   constexpr int D = block_steps<BT, FMT>();
   static_assert(D <= kPanelMaxPrefetch, "tail padding too short");
   constexpr int CAP = panel_capacity_neurons<BT>();
-  constexpr int kRowsAhead = 4;
   __shared__ __attribute__((aligned(16))) float lds_s[(CAP + 1) * BT];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const_i32_ptr tile = (const_i32_ptr)(A.tiles + 4 * static_cast<int64_t>(blockIdx.x));
-  const int panel = tile[0], row0 = tile[1], row1 = tile[2], entry0 = tile[3];
+  const int panel = tile[0], row0 = tile[1];
   const int64_t base = static_cast<int64_t>(panel) * A.width;
   const int len = static_cast<int>(min<int64_t>(A.width, A.N - base));
   const float gscale = (FMT == NS_WEIGHT_E4M3 || FMT == NS_WEIGHT_NVFP4) ? *A.gscale : 1.0f;
@@ -174,8 +173,7 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
     total = (last[0] - head[0]) / 64 + last[1];
   }
 
-  // First register block in flight while the panel is staged, and this
-  // thread's first row-table entries for the epilogue.
+  // First register block in flight while the panel is staged.
   Slot buf_a[D], buf_b[D];
 #pragma unroll
   for (int k = 0; k < D; ++k) buf_a[k] = load_slot<FMT>(A, first + lane, k);
@@ -183,13 +181,6 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
   Group now{0, 0, 0}, next{0, 0, 0};
   if (g < g_end) now = load_group(A, g);
   if (g + 1 < g_end) next = load_group(A, g + 1);
-  const int nrows = row1 - row0;
-  int rows_ahead[kRowsAhead];
-#pragma unroll
-  for (int k = 0; k < kRowsAhead; ++k) {
-    const int e = tid + k * kPanelThreads;
-    rows_ahead[k] = e < nrows ? A.rows[entry0 + e] : 0;
-  }
 
   // Stage this panel's slice of s (neuron-major, BT columns per neuron), 8 loads deep,
   // and the zero that padding slots read.
@@ -283,25 +274,26 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
     block(buf_b, buf_a, b + 1);
   }
 
-  // Map the tile's row-table-ordered sums back to rows: with one panel update
-  // the rows here, with several store this panel's partial sums by row.
-  __syncthreads();
-  auto finish_row = [&](int e, int r) {
-    const int64_t row = row0 + static_cast<int64_t>(r);
+  // Map this wavefront's row-table entries (one contiguous range: its groups'
+  // rows in order) back to rows as soon as its own stream is done: with one
+  // panel update the rows here, with several store this panel's partial sums
+  // by row.  The entries were stored by this wavefront's lanes; the fence
+  // orders those stores before the loads below.
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+  if (wg[0] < g_end) {
+    const_i32_ptr head = (const_i32_ptr)(A.groups + 4 * static_cast<int64_t>(wg[0]));
+    const_i32_ptr last = (const_i32_ptr)(A.groups + 4 * static_cast<int64_t>(g_end - 1));
+    const int e_begin = head[3], e_end = last[3] + (last[2] >> 8);
+    for (int e = e_begin + lane; e < e_end; e += 64) {
+      const int64_t row = row0 + static_cast<int64_t>(A.rows[e]);
 #pragma unroll
-    for (int j = 0; j < BT; ++j) {
-      const float value = A.sorted[(static_cast<int64_t>(entry0) + e) * BT + j];
-      if (A.n_panels == 1) update(A, row, j, value);
-      else A.partials[(static_cast<int64_t>(panel) * A.N + row) * BT + j] = value;
+      for (int j = 0; j < BT; ++j) {
+        const float value = A.sorted[static_cast<int64_t>(e) * BT + j];
+        if (A.n_panels == 1) update(A, row, j, value);
+        else A.partials[(static_cast<int64_t>(panel) * A.N + row) * BT + j] = value;
+      }
     }
-  };
-#pragma unroll
-  for (int k = 0; k < kRowsAhead; ++k) {
-    const int e = tid + k * kPanelThreads;
-    if (e < nrows) finish_row(e, rows_ahead[k]);
   }
-  for (int e = tid + kRowsAhead * kPanelThreads; e < nrows; e += kPanelThreads)
-    finish_row(e, A.rows[entry0 + e]);
 }
 
 // Several panels: add each row's panel partial sums in panel order, then update.

@@ -13,12 +13,13 @@ import numpy as np
 import pytest
 import torch
 
-from cases import column_drive, make_case, max_err
+from cases import column_drive, make_case, max_err, model_to, standard_model
 from oracle import precision as op
 from oracle import runtime as ort
 from oracle import topology as otop
 from neurosim_gpu import (NativeDendriticMatrixRuntime, NativeDendriticPELSRuntime,
-                          SparseTopology, encode_sparse_weights, load_native_extension)
+                          SparseTopology, encode_sparse_weights, load_native_extension,
+                          random_topology, topology_to)
 
 pytestmark = pytest.mark.gpu
 FIELDS = ("state", "dendritic_state", "adaptation_state")
@@ -284,4 +285,34 @@ def test_cfg3_large_1000_ticks(gpu, large_case, fmt):
             if tick % 50 == 49:
                 worst = max(worst, errors(native, oracle))
     print(f"cfg3 {fmt} max abs error over 1000 ticks: {worst:.3e}")
+    assert worst <= 1e-5
+
+
+def test_cfg5_scaleout_fp8_10_ticks(gpu):
+    """N=1000000, M~100M, B=16, drive [16,1] U(0,.4) seed 1, fp8 weights: 10 ticks vs
+    the oracle's float32 run on the decoded weights (the graph's two constructions
+    are compared bitwise at the smaller sizes; here the oracle reads the product's
+    host CSR arrays)."""
+    print("case cfg5 N=1000000 M=100M B=16 fp8 ticks=10", flush=True)
+    n, batch = 1_000_000, 16
+    topology_cpu = random_topology(n, 100_000_000, device="cpu", seed=0)
+    graph = otop.Graph(n=n, src=topology_cpu.src.numpy(), dst=topology_cpu.dst.numpy(),
+                       weight=topology_cpu.weight.numpy(),
+                       out_rowptr=topology_cpu.out_rowptr.numpy(),
+                       in_rowptr=topology_cpu.in_rowptr.numpy(), in_col=topology_cpu.in_col.numpy(),
+                       in_weight=topology_cpu.in_weight.numpy(),
+                       out_weight_index=topology_cpu.out_weight_index.numpy())
+    model, params = standard_model(n)
+    native = NativeDendriticMatrixRuntime(topology_to(topology_cpu, gpu), model_to(model, gpu),
+                                          torch.zeros(batch, n, device=gpu), weight_format="fp8")
+    oracle = ort.MatrixOracle(graph, params, torch.zeros(batch, n),
+                              in_weight=op.quantize_dequantize(graph.in_weight, "fp8"))
+    drive = column_drive(batch)
+    worst = 0.0
+    with torch.inference_mode():
+        for _ in range(10):
+            native.step(drive.to(gpu), dendritic_drive=0.1)
+            oracle.step(drive, 0.1)
+            worst = max(worst, errors(native, oracle))
+    print(f"cfg5 fp8 max abs error over 10 ticks: {worst:.3e}")
     assert worst <= 1e-5
