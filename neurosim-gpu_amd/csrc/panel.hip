@@ -78,6 +78,8 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v2f __attribute__((ext_vector_type(2)));
 typedef const int32_t __attribute__((address_space(4)))* const_i32_ptr;
 typedef const uint32_t __attribute__((address_space(4)))* const_u32_ptr;
+typedef const __attribute__((address_space(1))) void* global_void_ptr;
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
 // One lane's raw slot: source index, weight bits (F32/F16/E4M3 code, or the
 // NVFP4 byte holding its nibble) and, for NVFP4, the block-scale code.
@@ -185,17 +187,17 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
   // Stage this panel's slice of s (neuron-major, BT columns per neuron), 8 loads deep,
   // and the zero that padding slots read.
   if (A.s_vec) {
+    // Contiguous slice: direct global -> LDS loads, wavefront chunk ch covering
+    // float4s [64ch, 64ch + 64) (each lane's 16 bytes land at its own offset).
     const v4f* src = reinterpret_cast<const v4f*>(A.s.data + base * BT);
-    v4f* dst = reinterpret_cast<v4f*>(lds_s);
     const int n4 = len * BT / 4;
-    for (int i0 = tid; i0 < n4; i0 += 8 * kPanelThreads) {
-      v4f v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = src[min(i0 + u * kPanelThreads, n4 - 1)];
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (i0 + u * kPanelThreads < n4) dst[i0 + u * kPanelThreads] = v[u];
+    for (int ch = wave; ch * 64 < n4; ch += kPanelWaves) {
+      const int i = ch * 64 + lane;
+      if (i < n4)
+        __builtin_amdgcn_global_load_lds((const global_void_ptr)(src + i),
+                                         (lds_void_ptr)(lds_s + ch * 256), 16, 0, 0);
     }
+    __builtin_amdgcn_s_waitcnt(0);
     for (int i = n4 * 4 + tid; i < len * BT; i += kPanelThreads) lds_s[i] = A.s.data[base * BT + i];
   } else {
     for (int i = tid; i < len * BT; i += kPanelThreads) {
@@ -296,17 +298,22 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
   }
 }
 
-// Several panels: add each row's panel partial sums in panel order, then update.
+// Several panels: add each row's panel partial sums in panel order, then
+// update; one neuron (all BT columns) per thread.
+template <int BT>
 __global__ __launch_bounds__(kThreads) void panel_combine_kernel(PanelArgs A) {
-  const int64_t count = A.N * A.B;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < count; i += stride) {
-    const int64_t n = i / A.B, b = i - n * A.B;
-    float sum = 0.0f;
-    for (int p = 0; p < A.n_panels; ++p)
-      sum += __builtin_nontemporal_load(A.partials + p * count + i);
-    update(A, n, b, sum);
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (n >= A.N) return;
+  const int64_t plane = A.N * BT;
+  float sum[BT];
+#pragma unroll
+  for (int j = 0; j < BT; ++j) sum[j] = 0.0f;
+  for (int p = 0; p < A.n_panels; ++p) {
+#pragma unroll
+    for (int j = 0; j < BT; ++j) sum[j] += A.partials[p * plane + n * BT + j];
   }
+#pragma unroll
+  for (int j = 0; j < BT; ++j) update(A, n, j, sum[j]);
 }
 
 template <int BT>
@@ -320,8 +327,8 @@ hipError_t launch_panels(const PanelArgs& A, int fmt, int n_tiles, hipStream_t s
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || A.n_panels == 1) return err;
-  const int64_t blocks = std::min<int64_t>((A.N * A.B + kThreads - 1) / kThreads, 16384);
-  panel_combine_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, stream>>>(A);
+  const int64_t blocks = (A.N + kThreads - 1) / kThreads;
+  panel_combine_kernel<BT><<<dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, stream>>>(A);
   return hipGetLastError();
 }
 
