@@ -142,8 +142,10 @@ extern "C" int ns_dendritic_event(const ns_event_args* args, void* stream) {
 
   EventArgs A{};
   A.N = N; A.B = B; A.count = B * N;
-  A.s = plane(a.state); A.d = plane(a.dendrite); A.a = plane(a.adaptation);
-  A.u = plane(a.drive); A.v = plane(a.dendritic_drive); A.emitted = plane(a.emitted);
+  A.s = plane(a.state, a.state.data); A.d = plane(a.dendrite, a.state.data);
+  A.a = plane(a.adaptation, a.state.data);
+  A.u = plane(a.drive, a.state.data); A.v = plane(a.dendritic_drive, a.state.data);
+  A.emitted = plane(a.emitted, a.state.data);
   for (int i = 0; i < 6; ++i) A.p.v[i] = Vec{a.params[i].data, a.params[i].stride};
   A.current = a.current; A.csb = a.current_stride_b; A.csn = a.current_stride_n;
   A.theta = Vec{a.theta.data, a.theta.stride};

@@ -25,12 +25,20 @@ constexpr int kPanelThreads = kPanelWaves * 64;
 constexpr int kPanelMaxPrefetch = 16;                  // steps per register block, at most
 constexpr int kPanelTailSlots = 2 * kPanelMaxPrefetch * 64;
 
+// A [B, N] operand that is either a strided tensor or one scalar.  `data` is
+// never null: a scalar plane points at some valid float with zero strides, so
+// a read is one unconditional load and a bitwise blend with `scalar` under
+// `mask` (all ones for a tensor, zero for a scalar).  A branch on the pointer,
+// or on a flag the compiler can see is boolean, would make a kernel wait for
+// each plane's kernel arguments before it requests the next plane's.
 struct Plane {
   const float* data;
   int64_t sb, sn;
   float scalar;
+  uint32_t mask;
   __device__ __forceinline__ float get(int64_t b, int64_t n) const {
-    return data ? data[b * sb + n * sn] : scalar;
+    const uint32_t x = __builtin_bit_cast(uint32_t, data[b * sb + n * sn]);
+    return __builtin_bit_cast(float, (x & mask) | (__builtin_bit_cast(uint32_t, scalar) & ~mask));
   }
 };
 
@@ -61,29 +69,39 @@ __device__ __forceinline__ float clamp01(float x) {
   return x < 0.0f ? 0.0f : (x > 1.0f ? 1.0f : x);
 }
 
+// A neuron's six parameters, loaded together so their loads can be issued
+// before anything that waits on memory.
+struct NeuronParams {
+  float alpha, gain, rho_d, rho_a, coupling, strength;
+};
+
+__device__ __forceinline__ NeuronParams load_params(const Params& p, int64_t n) {
+  return NeuronParams{p.v[0].get(n), p.v[1].get(n), p.v[2].get(n),
+                      p.v[3].get(n), p.v[4].get(n), p.v[5].get(n)};
+}
+
 // One three-state update.  Each statement is one tensor op of the reference:
 //   d' = rho_d*d + (1-rho_d)*tanh(j + v)
 //   u  = ((1-c)*j + c*d') - k*a
 //   s' = clamp(alpha*s + (1-alpha)*(gain*tanh(u + drive)), 0, 1)
 //   a' = rho_a*a + (1-rho_a)*s'
-__device__ __forceinline__ NextState advance_one(const Params& p, int64_t n, float j, float s,
-                                                 float d, float a, float drive, float ddrive) {
+__device__ __forceinline__ NextState advance_loaded(const NeuronParams& p, float j, float s,
+                                                    float d, float a, float drive, float ddrive) {
 #pragma clang fp contract(off)
-  const float alpha = p.v[0].get(n);
-  const float gain = p.v[1].get(n);
-  const float rho_d = p.v[2].get(n);
-  const float rho_a = p.v[3].get(n);
-  const float coupling = p.v[4].get(n);
-  const float strength = p.v[5].get(n);
   NextState out;
   const float dend_in = tanhf(j + ddrive);
-  out.dendrite = rho_d * d + (1.0f - rho_d) * dend_in;
-  const float mixed = (1.0f - coupling) * j + coupling * out.dendrite;
-  const float current = mixed - strength * a;
-  const float equilibrium = gain * tanhf(current + drive);
-  out.soma = clamp01(alpha * s + (1.0f - alpha) * equilibrium);
-  out.adaptation = rho_a * a + (1.0f - rho_a) * out.soma;
+  out.dendrite = p.rho_d * d + (1.0f - p.rho_d) * dend_in;
+  const float mixed = (1.0f - p.coupling) * j + p.coupling * out.dendrite;
+  const float current = mixed - p.strength * a;
+  const float equilibrium = p.gain * tanhf(current + drive);
+  out.soma = clamp01(p.alpha * s + (1.0f - p.alpha) * equilibrium);
+  out.adaptation = p.rho_a * a + (1.0f - p.rho_a) * out.soma;
   return out;
+}
+
+__device__ __forceinline__ NextState advance_one(const Params& p, int64_t n, float j, float s,
+                                                 float d, float a, float drive, float ddrive) {
+  return advance_loaded(load_params(p, n), j, s, d, a, drive, ddrive);
 }
 
 // OCP fp8 e4m3fn -> float32, exact (bias 7, subnormals, 0x7F/0xFF NaN): the

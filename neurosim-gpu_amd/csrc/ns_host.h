@@ -54,7 +54,11 @@ inline bool overlaps(const Extent& x, const Extent& y) {
   return x.lo < y.hi && y.lo < x.hi;
 }
 
-inline Plane plane(const ns_plane& p) { return Plane{p.data, p.stride_b, p.stride_n, p.scalar}; }
+// `valid` is any readable device float, used as the address of a scalar plane.
+inline Plane plane(const ns_plane& p, const float* valid) {
+  if (p.data) return Plane{p.data, p.stride_b, p.stride_n, p.scalar, ~0u};
+  return Plane{valid, 0, 0, p.scalar, 0u};
+}
 inline OutPlane out_plane(const ns_out_plane& p) {
   return OutPlane{p.data, p.stride_b, p.stride_n};
 }

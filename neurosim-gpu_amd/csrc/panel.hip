@@ -105,6 +105,41 @@ __device__ __forceinline__ Slot load_slot(const PanelArgs& A, int64_t q0, int k)
   return x;
 }
 
+// `p` kept a scalar operand of the loads made through it (scalar base plus
+// 32-bit lane offset) instead of being folded into per-lane 64-bit addresses.
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* scalar_base(const T* p) {
+  typedef const __attribute__((address_space(1))) T* global_ptr;
+  global_ptr q = (global_ptr)p;
+  asm volatile("" : "+s"(q));
+  return q;
+}
+
+// One register block of D steps starting at slot block0 (a multiple of 64).
+// For float32 weights the loads take a scalar base per block and the lane
+// offset: with per-lane 64-bit addresses the compiler reuses a register of
+// the block in flight for the next block's address and so waits for that
+// block before issuing the next one.  The narrower encodings keep per-lane
+// addresses, which compile without that wait.
+template <int FMT, int D>
+__device__ __forceinline__ void load_block(const PanelArgs& A, int64_t block0, int lane,
+                                           Slot (&dst)[D]) {
+  if constexpr (FMT == NS_WEIGHT_F32) {
+    const auto col = scalar_base(A.col + block0);
+    const auto weight = scalar_base(static_cast<const uint32_t*>(A.weight) + block0);
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+      const uint32_t at = static_cast<uint32_t>(lane) + 64u * k;
+      dst[k].c = col[at];
+      dst[k].w = weight[at];
+      dst[k].sc = 0u;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < D; ++k) dst[k] = load_slot<FMT>(A, block0 + lane, k);
+  }
+}
+
 // Slots of a group start at multiples of 64, so a slot's nibble half is the lane's parity.
 template <int FMT>
 __device__ __forceinline__ float decode_slot(const Slot& x, int lane, float gscale) {
@@ -177,8 +212,7 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
 
   // First register block in flight while the panel is staged.
   Slot buf_a[D], buf_b[D];
-#pragma unroll
-  for (int k = 0; k < D; ++k) buf_a[k] = load_slot<FMT>(A, first + lane, k);
+  load_block<FMT, D>(A, first, lane, buf_a);
   uint32_t bits = boundary_bits<D>(A, first / 64);
   Group now{0, 0, 0}, next{0, 0, 0};
   if (g < g_end) now = load_group(A, g);
@@ -218,8 +252,7 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
   // made of scalars and the lane id, so closing waits on no vector load).
   auto block = [&](Slot (&here)[D], Slot (&ahead)[D], int b) {
     const int64_t ahead0 = first + static_cast<int64_t>(b + 1) * D * 64;
-#pragma unroll
-    for (int k = 0; k < D; ++k) ahead[k] = load_slot<FMT>(A, ahead0 + lane, k);
+    load_block<FMT, D>(A, ahead0, lane, ahead);
     const int rem = total - b * D;
     uint32_t ends = rem < D ? bits & ((1u << rem) - 1u) : bits;
     bits = boundary_bits<D>(A, ahead0 / 64);
@@ -299,21 +332,49 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
 }
 
 // Several panels: add each row's panel partial sums in panel order, then
-// update; one neuron (all BT columns) per thread.
+// update; one neuron (all BT columns) per thread.  Every load (state,
+// parameters, the first kCombineBatch panels' sums) is issued before the first
+// add, so the kernel waits on memory about once rather than once per panel.
+constexpr int kCombineBatch = 8;
+
 template <int BT>
 __global__ __launch_bounds__(kThreads) void panel_combine_kernel(PanelArgs A) {
   const int64_t n = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (n >= A.N) return;
   const int64_t plane = A.N * BT;
+  const NeuronParams prm = load_params(A.p, n);
+  float s[BT], d[BT], a[BT], u[BT], v[BT];
+#pragma unroll
+  for (int j = 0; j < BT; ++j) {
+    s[j] = A.s.get(j, n); d[j] = A.d.get(j, n); a[j] = A.a.get(j, n);
+    u[j] = A.u.get(j, n); v[j] = A.v.get(j, n);
+  }
   float sum[BT];
 #pragma unroll
   for (int j = 0; j < BT; ++j) sum[j] = 0.0f;
-  for (int p = 0; p < A.n_panels; ++p) {
+  for (int p0 = 0; p0 < A.n_panels; p0 += kCombineBatch) {
+    float part[kCombineBatch][BT];
 #pragma unroll
-    for (int j = 0; j < BT; ++j) sum[j] += A.partials[p * plane + n * BT + j];
+    for (int q = 0; q < kCombineBatch; ++q) {
+      // Past the last panel, reread the last panel's sum (not added) so that
+      // no load waits behind a branch.
+      const int p = min(p0 + q, A.n_panels - 1);
+#pragma unroll
+      for (int j = 0; j < BT; ++j) part[q][j] = A.partials[p * plane + n * BT + j];
+    }
+#pragma unroll
+    for (int q = 0; q < kCombineBatch; ++q)
+#pragma unroll
+      for (int j = 0; j < BT; ++j)
+        if (p0 + q < A.n_panels) sum[j] += part[q][j];
   }
 #pragma unroll
-  for (int j = 0; j < BT; ++j) update(A, n, j, sum[j]);
+  for (int j = 0; j < BT; ++j) {
+    const NextState x = advance_loaded(prm, sum[j], s[j], d[j], a[j], u[j], v[j]);
+    A.os.put(j, n, x.soma);
+    A.od.put(j, n, x.dendrite);
+    A.oa.put(j, n, x.adaptation);
+  }
 }
 
 template <int BT>
@@ -378,8 +439,9 @@ int panel_step(const ns_step_args& a, hipStream_t stream) {
 
   PanelArgs A{};
   A.N = a.n_neurons; A.B = a.batch;
-  A.s = plane(a.state); A.d = plane(a.dendrite); A.a = plane(a.adaptation);
-  A.u = plane(a.drive); A.v = plane(a.dendritic_drive);
+  A.s = plane(a.state, a.state.data); A.d = plane(a.dendrite, a.state.data);
+  A.a = plane(a.adaptation, a.state.data);
+  A.u = plane(a.drive, a.state.data); A.v = plane(a.dendritic_drive, a.state.data);
   for (int i = 0; i < 6; ++i) A.p.v[i] = Vec{a.params[i].data, a.params[i].stride};
   A.width = pl.panel_width; A.n_panels = pl.n_panels;
   A.tiles = pl.tiles; A.wave_groups = pl.wave_groups; A.groups = pl.groups; A.rows = pl.rows;

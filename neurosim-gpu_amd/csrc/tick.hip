@@ -438,8 +438,9 @@ extern "C" int ns_dendritic_step(const ns_step_args* args, void* stream) {
 
   TickArgs A{};
   A.N = a.n_neurons; A.B = a.batch; A.M = a.matrix.n_edges;
-  A.s = plane(a.state); A.d = plane(a.dendrite); A.a = plane(a.adaptation);
-  A.u = plane(a.drive); A.v = plane(a.dendritic_drive);
+  A.s = plane(a.state, a.state.data); A.d = plane(a.dendrite, a.state.data);
+  A.a = plane(a.adaptation, a.state.data);
+  A.u = plane(a.drive, a.state.data); A.v = plane(a.dendritic_drive, a.state.data);
   for (int i = 0; i < 6; ++i) A.p.v[i] = Vec{a.params[i].data, a.params[i].stride};
   A.rowptr = a.matrix.rowptr; A.col = a.matrix.col; A.weight = a.matrix.weight;
   A.scales = a.matrix.block_scales; A.gscale = a.matrix.global_scale;
@@ -471,7 +472,7 @@ extern "C" int ns_csr_spmm(const ns_spmm_args* args, void* stream) {
 
   TickArgs A{};
   A.N = a.n_neurons; A.B = a.batch; A.M = a.matrix.n_edges;
-  A.s = plane(a.source);
+  A.s = plane(a.source, a.source.data);
   A.rowptr = a.matrix.rowptr; A.col = a.matrix.col; A.weight = a.matrix.weight;
   A.scales = a.matrix.block_scales; A.gscale = a.matrix.global_scale;
   A.bounds = a.plan.bounds; A.n_blocks = a.plan.n_blocks;
