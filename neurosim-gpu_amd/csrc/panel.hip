@@ -197,6 +197,20 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
   const int len = static_cast<int>(min<int64_t>(A.width, A.N - base));
   const float gscale = (FMT == NS_WEIGHT_E4M3 || FMT == NS_WEIGHT_NVFP4) ? *A.gscale : 1.0f;
 
+  // A contiguous slice of s is staged with direct global -> LDS loads, issued
+  // first since they need only the panel: wavefront chunk ch covers float4s
+  // [64ch, 64ch + 64) (each lane's 16 bytes land at its own offset).
+  const v4f* src = reinterpret_cast<const v4f*>(A.s.data + base * BT);
+  const int n4 = len * BT / 4;
+  if (A.s_vec) {
+    for (int ch = wave; ch * 64 < n4; ch += kPanelWaves) {
+      const int i = ch * 64 + lane;
+      if (i < n4)
+        __builtin_amdgcn_global_load_lds((const global_void_ptr)(src + i),
+                                         (lds_void_ptr)(lds_s + ch * 256), 16, 0, 0);
+    }
+  }
+
   // This wavefront's stream: groups [g, g_end), steps [first/64, first/64 + total).
   const_i32_ptr wg = (const_i32_ptr)(A.wave_groups + static_cast<int64_t>(blockIdx.x) * kPanelWaves + wave);
   int g = wg[0];
@@ -218,19 +232,9 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
   if (g < g_end) now = load_group(A, g);
   if (g + 1 < g_end) next = load_group(A, g + 1);
 
-  // Stage this panel's slice of s (neuron-major, BT columns per neuron), 8 loads deep,
-  // and the zero that padding slots read.
+  // Finish staging: the slice's last floats (not a whole float4) or, for a
+  // strided state, the whole slice; then the zero that padding slots read.
   if (A.s_vec) {
-    // Contiguous slice: direct global -> LDS loads, wavefront chunk ch covering
-    // float4s [64ch, 64ch + 64) (each lane's 16 bytes land at its own offset).
-    const v4f* src = reinterpret_cast<const v4f*>(A.s.data + base * BT);
-    const int n4 = len * BT / 4;
-    for (int ch = wave; ch * 64 < n4; ch += kPanelWaves) {
-      const int i = ch * 64 + lane;
-      if (i < n4)
-        __builtin_amdgcn_global_load_lds((const global_void_ptr)(src + i),
-                                         (lds_void_ptr)(lds_s + ch * 256), 16, 0, 0);
-    }
     __builtin_amdgcn_s_waitcnt(0);
     for (int i = n4 * 4 + tid; i < len * BT; i += kPanelThreads) lds_s[i] = A.s.data[base * BT + i];
   } else {
