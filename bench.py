@@ -14,9 +14,10 @@ Prints one JSON line.  ``value`` is ms per fp32 tick (lower is better);
 restated) on a bounded sample of the same tick on this host.  ``configs``
 adds the other workloads, each timed the same way: the batched tick
 (N=50000, M~1M, B=8, per-column drive), the PELS event tick (N=50000, M~1M,
-B=1, theta 0.02, driven and with inputs withdrawn) and the scale-out tick
+B=1, theta 0.02, driven and with inputs withdrawn), the scale-out tick
 (N=1000000, M~100M, B=16, fp8 weights, 200 graph-captured ticks, with the
-CPU oracle on a 10-tick sample).
+CPU oracle on a 10-tick sample), and the fp8/NVFP4 device encoding of the
+headline graph's weights.
 
     python bench.py [--gpus 1] [--steps 1000] [--warmup 50]
 """
@@ -211,6 +212,43 @@ def rollout_ms(runtime, ticks: int, repeats: int, drive, dendritic_drive) -> flo
     return start.elapsed_time(end) / (ticks * repeats)
 
 
+def measure_encode(weight: torch.Tensor, repeats: int = 20) -> dict:
+    """fp8 and NVFP4 encoding of the headline graph's float32 CSR weights on
+    the device: ns_encode_weights (two launches) against the torch-op
+    encoder it replaces, each timed over ``repeats`` calls with HIP events,
+    plus a bitwise comparison of the two payloads."""
+    from neurosim_gpu.native import encode_weights
+    from neurosim_gpu.precision import encode_sparse_weights
+
+    m = weight.numel()
+    out = {"workload": f"weight encoding, M={m} float32 CSR weights", "repeats": repeats}
+    for fmt in ("fp8", "nvfp4"):
+        # weight read twice (amax, then encode), payload written once
+        alg = 8 * m + (m if fmt == "fp8" else (m + 1) // 2 + (m + 15) // 16) + 4
+        timed = {}
+        for name, fn in (("hip", encode_weights), ("torch_ops", encode_sparse_weights)):
+            for _ in range(3):
+                result = fn(weight, fmt)
+            torch.cuda.synchronize()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            for _ in range(repeats):
+                result = fn(weight, fmt)
+            end.record()
+            torch.cuda.synchronize()
+            timed[name] = (start.elapsed_time(end) / repeats, result)
+        hip_ms, (codes, scales, scale) = timed["hip"]
+        ops_ms, (codes_ref, scales_ref, scale_ref) = timed["torch_ops"]
+        same = bool(torch.equal(codes, codes_ref)) and bool(torch.equal(scale.reshape(()), scale_ref.reshape(())))
+        if fmt == "nvfp4":
+            same = same and bool(torch.equal(scales, scales_ref))
+        out[fmt] = {"hip_ms": round(hip_ms, 4), "torch_ops_ms": round(ops_ms, 4),
+                    "algorithmic_bytes": alg, "hip_GBps": round(alg / hip_ms / 1e6, 1),
+                    "pct_hbm_peak": round(100 * alg / hip_ms / 1e6 / HBM_PEAK_GBPS, 1),
+                    "payload_equal_to_torch_ops": same}
+    return out
+
+
 def measure_batched(device) -> dict:
     """N=50000, M~1M, B=8, drive [8,1] U(0,.4) (seed 1), dendritic .1, fp32, 1000 ticks."""
     n, candidates, batch = 50_000, 1_000_000, 8
@@ -347,7 +385,7 @@ def main() -> None:
                      help="tick kernel: LDS column panels (batch 1-2) or CSR row blocks")
     cli.add_argument("--copy-calibration", action="store_true",
                      help="only run 256 MiB device copies (PMC byte-counter calibration)")
-    cli.add_argument("--configs", default="batched,pels,scaleout",
+    cli.add_argument("--configs", default="encode,batched,pels,scaleout",
                      help="other workloads to time after the headline one ('none' for none)")
     args = cli.parse_args()
     if args.gpus != 1:
@@ -408,10 +446,15 @@ def main() -> None:
     if not args.no_cpu_baseline:
         log("timing the CPU oracle")
         line["cpu_baseline"] = cpu_baseline(topology_cpu, model_cpu)
+    extra = {}
+    configs = [c for c in args.configs.split(",") if c and c != "none"]
+    if "encode" in configs:
+        log("timing encode")
+        extra["encode"] = measure_encode(topology.in_weight)
+        log(f"encode: {extra['encode']}")
     del topology
     torch.cuda.empty_cache()
-    extra = {}
-    for name in [c for c in args.configs.split(",") if c and c != "none"]:
+    for name in [c for c in configs if c != "encode"]:
         log(f"timing {name}")
         if name == "batched":
             extra[name] = measure_batched(device)

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 4
+#define NS_ABI_VERSION 5
 
 /* Return codes. */
 #define NS_OK 0
@@ -180,6 +180,19 @@ typedef struct ns_spmm_args {
   ns_out_plane out;            /* J, [B,N]; must not overlap `source` */
 } ns_spmm_args;
 
+/* Arguments of one weight encoding (fp8 e4m3 or NVFP4 CSR payload). */
+typedef struct ns_encode_args {
+  const float* weight;         /* [n_edges] float32 in CSR order, 16-byte aligned */
+  int64_t n_edges;             /* M >= 0 */
+  int32_t format;              /* NS_WEIGHT_E4M3 or NS_WEIGHT_NVFP4 */
+  int32_t reserved;
+  uint8_t* codes;              /* E4M3: [M] codes (4-byte aligned); NVFP4: [(M+1)/2]
+                                  bytes, even edge in the low nibble (8-byte aligned) */
+  uint8_t* block_scales;       /* NVFP4: [(M+15)/16] e4m3 codes; E4M3: unused */
+  float* global_scale;         /* device float32[1] */
+  uint32_t* workspace;         /* ns_encode_workspace_bytes() bytes, contents ignored */
+} ns_encode_args;
+
 /* ABI version of the loaded library (NS_ABI_VERSION). */
 int ns_abi_version(void);
 
@@ -244,6 +257,18 @@ int ns_dendritic_event(const ns_event_args* args, void* stream);
  * Replaces MatrixRuntime._propagate (reference: runtime.py:78-79) for device
  * float32 operands, e.g. the persistent current W @ emitted of runtime.py:124,220. */
 int ns_csr_spmm(const ns_spmm_args* args, void* stream);
+
+/* Bytes of the workspace ns_encode_weights needs (independent of M). */
+int64_t ns_encode_workspace_bytes(void);
+
+/* Encodes float32 CSR weights into the fp8 (per-tensor scale) or NVFP4
+ * (16-edge e4m3 block scales, float32 global scale) payload that
+ * ns_dendritic_step decodes, bit-exact with the reference's encoders.
+ * Replaces encode_sparse_weights (reference: src/neurosim_gpu/precision.py:76-90,
+ * with _encode_e4m3 :45-49 and _encode_e2m1 :52-73) as called on a weight
+ * change (native_compartmental.py:114-124).  Two launches on `stream`, no
+ * allocation, no host synchronisation; parity is defined for finite weights. */
+int ns_encode_weights(const ns_encode_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -35,7 +35,7 @@ import numpy as np
 import torch
 
 _LIB_NAME = "libneurosim_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 WEIGHT_F32, WEIGHT_F16, WEIGHT_E4M3, WEIGHT_NVFP4 = 0, 1, 2, 3
 _PLAN_CACHE = 64   # row plans kept per extension (one per live topology and batch width)
@@ -106,6 +106,12 @@ class _SpmmArgs(ctypes.Structure):
                 ("matrix", _Csr), ("plan", _RowPlan), ("out", _OutPlane)]
 
 
+class _EncodeArgs(ctypes.Structure):
+    _fields_ = [("weight", _c_ptr), ("n_edges", _c_i64), ("format", ctypes.c_int32),
+                ("reserved", ctypes.c_int32), ("codes", _c_ptr), ("block_scales", _c_ptr),
+                ("global_scale", _c_ptr), ("workspace", _c_ptr)]
+
+
 def library_path() -> Path:
     override = os.environ.get("NEUROSIM_HIP_LIB")
     if override:
@@ -137,8 +143,10 @@ def load_library() -> ctypes.CDLL:
     lib.ns_plan_panels.argtypes = [_c_ptr, _c_ptr, _c_i64, ctypes.c_int32, ctypes.c_int32,
                                    ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(_PanelPlan),
                                    ctypes.POINTER(_c_i64)] + [_c_ptr] * 7
+    lib.ns_encode_workspace_bytes.restype = _c_i64
+    lib.ns_encode_workspace_bytes.argtypes = []
     for name, kind in (("ns_dendritic_step", _StepArgs), ("ns_dendritic_event", _EventArgs),
-                       ("ns_csr_spmm", _SpmmArgs)):
+                       ("ns_csr_spmm", _SpmmArgs), ("ns_encode_weights", _EncodeArgs)):
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int
         fn.argtypes = [ctypes.POINTER(kind), _c_ptr]
@@ -152,6 +160,44 @@ def _raise_on(code: int, lib: ctypes.CDLL) -> None:
     if code != 0:
         message = lib.ns_last_error().decode("utf-8", "replace")
         raise RuntimeError(message or f"native call failed with code {code}")
+
+
+def encode_weights(weight: torch.Tensor, precision: str
+                   ) -> tuple[torch.Tensor, torch.Tensor | None, torch.Tensor]:
+    """Device encoding of float32 CSR weights (ns_encode_weights).
+
+    Same contract as precision.encode_sparse_weights (reference precision.py:76-90):
+    returns (packed codes uint8, block scales uint8 or None, float32 global
+    scale, 0-d) on the weights' device, launched on the current stream.
+    """
+    if weight.ndim != 1 or weight.dtype != torch.float32:
+        raise ValueError("encoding requires a vector of FP32 CSR weights")
+    if precision not in ("fp8", "nvfp4"):
+        raise ValueError("compressed CSR encoding requires fp8 or nvfp4")
+    if weight.device.type != "cuda":
+        raise ValueError("the device encoder needs the weights on a GPU")
+    lib = load_library()
+    m = weight.numel()
+    source = weight.detach()
+    if m and (not source.is_contiguous() or source.data_ptr() % 16):
+        source = source.contiguous().clone()
+    device = weight.device
+    nvfp4 = precision == "nvfp4"
+    # Codes are allocated in whole 8-byte words (the kernels store whole words)
+    # and returned as views of exactly the payload's length.
+    payload = (m + 1) // 2 if nvfp4 else m
+    codes = torch.empty(-(-max(payload, 1) // 8) * 8, dtype=torch.uint8, device=device)
+    scales = torch.empty((m + 15) // 16, dtype=torch.uint8, device=device) if nvfp4 else None
+    scale = torch.empty(1, dtype=torch.float32, device=device)
+    workspace = torch.empty(int(lib.ns_encode_workspace_bytes()) // 4, dtype=torch.int32,
+                            device=device)
+    args = _EncodeArgs(source.data_ptr() if m else None, m,
+                       WEIGHT_NVFP4 if nvfp4 else WEIGHT_E4M3, 0, codes.data_ptr(),
+                       scales.data_ptr() if scales is not None and scales.numel() else None,
+                       scale.data_ptr(), workspace.data_ptr())
+    stream = torch.cuda.current_stream(device).cuda_stream
+    _raise_on(lib.ns_encode_weights(ctypes.byref(args), stream), lib)
+    return codes[:payload], scales, scale.view(())
 
 
 def plan_row_blocks(rowptr: torch.Tensor, batch: int, device: torch.device) -> tuple[torch.Tensor, int, int]:

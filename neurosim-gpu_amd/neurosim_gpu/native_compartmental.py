@@ -21,7 +21,7 @@ from __future__ import annotations
 import torch
 
 from .compartmental import DendriticDynamics, DendriticMatrixRuntime, DendriticPELSRuntime
-from .native import NativeExtension, PanelLayout, load_native_extension
+from .native import NativeExtension, PanelLayout, encode_weights, load_native_extension
 from .topology import SparseTopology
 
 
@@ -166,6 +166,10 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
             with torch.no_grad():
                 if self.weight_format is None:
                     self._packed_weight = (weight.detach().to(torch.float16),)
+                elif isinstance(self.extension, NativeExtension):
+                    # On the device in two launches (ns_encode_weights), bit-exact
+                    # with precision.encode_sparse_weights.
+                    self._packed_weight = encode_weights(weight.detach(), self.weight_format)
                 else:
                     from .precision import encode_sparse_weights
                     self._packed_weight = encode_sparse_weights(weight.detach(), self.weight_format)

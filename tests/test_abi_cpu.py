@@ -31,7 +31,8 @@ def test_every_declared_symbol_is_exported(lib):
     names = declared_functions()
     assert set(names) == {"ns_abi_version", "ns_last_error", "ns_block_edges",
                           "ns_plan_row_blocks", "ns_dendritic_step", "ns_dendritic_event",
-                          "ns_csr_spmm", "ns_plan_panels", "ns_panel_geometry"}
+                          "ns_csr_spmm", "ns_plan_panels", "ns_panel_geometry",
+                          "ns_encode_workspace_bytes", "ns_encode_weights"}
     for name in names:
         assert hasattr(lib, name), name
     assert lib.ns_abi_version() == native.ABI_VERSION
@@ -142,3 +143,31 @@ def test_step_validation_messages(lib):
 def test_empty_batch_is_a_no_op(lib):
     args, keep = fake_step_args(batch=0)
     assert call(lib, args) == (0, "")
+
+
+def test_encoder_validation_messages(lib):
+    """ns_encode_weights rejects bad arguments before any launch."""
+    assert lib.ns_encode_workspace_bytes() == 4096
+
+    def call(**fields):
+        base = dict(weight=None, n_edges=0, format=native.WEIGHT_E4M3, reserved=0, codes=None,
+                    block_scales=None, global_scale=16, workspace=16)
+        base.update(fields)
+        args = native._EncodeArgs(**base)
+        rc = lib.ns_encode_weights(ctypes.byref(args), None)
+        return rc, lib.ns_last_error().decode()
+
+    rc, message = call(format=native.WEIGHT_F32)
+    assert rc != 0 and "E4M3 or NVFP4" in message
+    rc, message = call(global_scale=None)
+    assert rc != 0 and "global_scale and workspace" in message
+    rc, message = call(n_edges=10)
+    assert rc != 0 and "weight and codes" in message
+    rc, message = call(n_edges=10, weight=16, codes=16, format=native.WEIGHT_NVFP4)
+    assert rc != 0 and "block_scales" in message
+    rc, message = call(n_edges=10, weight=20, codes=16)
+    assert rc != 0 and "16-byte aligned" in message
+    rc, message = call(n_edges=10, weight=16, codes=18)
+    assert rc != 0 and "4-byte aligned" in message
+    rc, message = call(n_edges=-1)
+    assert rc != 0 and "n_edges" in message

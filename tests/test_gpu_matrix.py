@@ -266,6 +266,21 @@ def test_device_encoder_is_bitwise_the_oracle_at_25m_edges(gpu, large_case, fmt)
         assert np.array_equal(scales.cpu().numpy(), want_scales)
 
 
+@pytest.mark.parametrize("fmt", ["fp8", "nvfp4"])
+def test_hip_encoder_is_bitwise_the_oracle_at_25m_edges(gpu, large_case, fmt):
+    """ns_encode_weights on the headline graph's 25M weights == the CPU oracle's payload."""
+    from neurosim_gpu.native import encode_weights
+
+    print(f"case hip encode N=166000 M=25M fmt={fmt}", flush=True)
+    weight = large_case.graph.in_weight
+    codes, scales, scale = encode_weights(torch.from_numpy(weight).to(gpu), fmt)
+    want_codes, want_scales, want_scale = op.encode_sparse_weights(weight, fmt)
+    assert np.float32(scale.item()).tobytes() == np.float32(want_scale).tobytes()
+    assert np.array_equal(codes.cpu().numpy(), want_codes)
+    if fmt == "nvfp4":
+        assert np.array_equal(scales.cpu().numpy(), want_scales)
+
+
 @pytest.mark.parametrize("fmt", ["fp32", "fp16", "fp8", "nvfp4"])
 def test_cfg3_large_1000_ticks(gpu, large_case, fmt):
     """N=166000, M~25M, B=1: fp32 vs oracle; fp16/fp8/nvfp4 vs oracle on decoded weights."""
