@@ -183,10 +183,8 @@ def encode_weights(weight: torch.Tensor, precision: str
         source = source.contiguous().clone()
     device = weight.device
     nvfp4 = precision == "nvfp4"
-    # Codes are allocated in whole 8-byte words (the kernels store whole words)
-    # and returned as views of exactly the payload's length.
     payload = (m + 1) // 2 if nvfp4 else m
-    codes = torch.empty(-(-max(payload, 1) // 8) * 8, dtype=torch.uint8, device=device)
+    codes = torch.empty(max(payload, 1), dtype=torch.uint8, device=device)
     scales = torch.empty((m + 15) // 16, dtype=torch.uint8, device=device) if nvfp4 else None
     scale = torch.empty(1, dtype=torch.float32, device=device)
     workspace = torch.empty(int(lib.ns_encode_workspace_bytes()) // 4, dtype=torch.int32,
