@@ -345,12 +345,17 @@ def measure_scaleout(device, cpu_sample: bool) -> dict:
     """N=1000000, M~100M, B=16, drive [16,1] U(0,.4) (seed 1), fp8 e4m3 weights,
     200 graph-captured ticks; CPU oracle (fp32, decoded weights) on 10 ticks."""
     n, candidates, batch = 1_000_000, 100_000_000, 16
-    log("scale-out: building N=1000000 M=100M graph on the host")
-    topology_cpu = random_topology(n, candidates, device="cpu", seed=0)
-    m = topology_cpu.n_edges
+    log("scale-out: drawing N=1000000 M=100M candidates on the host, coalescing on the GPU")
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    topology = random_topology(n, candidates, device="cpu", seed=0, build_device=device)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - start
+    topology_cpu = topology_to(topology, "cpu") if cpu_sample else None
+    m = topology.n_edges
     model_cpu, model = standard_model(n, device)
-    runtime = NativeDendriticMatrixRuntime(topology_to(topology_cpu, device), model,
-                                           torch.zeros(batch, n, device=device), weight_format="fp8")
+    runtime = NativeDendriticMatrixRuntime(topology, model, torch.zeros(batch, n, device=device),
+                                           weight_format="fp8")
     drive = column_drive(batch)
     ms = rollout_ms(runtime, 100, 2, drive.to(device), 0.1)
     alg = algorithmic_bytes("fp8", n, m, batch) + 4 * batch
@@ -358,7 +363,9 @@ def measure_scaleout(device, cpu_sample: bool) -> dict:
                           "per-column drive", "kernel": runtime.kernel, "ticks": 200,
               "ms_per_tick": round(ms, 5), "algorithmic_bytes": alg,
               "achieved_GBps": round(alg / ms / 1e6, 1),
-              "pct_hbm_peak": round(100 * alg / ms / 1e6 / HBM_PEAK_GBPS, 1)}
+              "pct_hbm_peak": round(100 * alg / ms / 1e6 / HBM_PEAK_GBPS, 1),
+              "graph_build_s": round(build_s, 2),
+              "graph_build": "host draws (torch CPU generator), ns_build_topology on the GPU"}
     if cpu_sample:
         log("scale-out: timing the CPU oracle on 10 ticks")
         from neurosim_gpu.precision import quantize_dequantize

@@ -193,6 +193,27 @@ typedef struct ns_encode_args {
   uint32_t* workspace;         /* ns_encode_workspace_bytes() bytes, contents ignored */
 } ns_encode_args;
 
+/* Arguments of one graph build (coalescing and both CSR views) on the device. */
+typedef struct ns_topology_args {
+  int64_t n_neurons;           /* N in [1, 2^31] */
+  int64_t n_candidates;        /* Mc in [0, 2^31): candidate edges, duplicates allowed */
+  const int64_t* src;          /* [Mc] device, each in [0, N) (not checked on the device) */
+  const int64_t* dst;          /* [Mc] device, each in [0, N) */
+  const float* weight;         /* [Mc] device */
+  /* Outputs, device, sized for Mc edges; the first *n_edges entries are the graph. */
+  int32_t* out_src;            /* [Mc] canonical (src, dst)-ordered sources */
+  int32_t* out_dst;            /* [Mc] */
+  float* out_weight;           /* [Mc] summed weights */
+  int32_t* out_rowptr;         /* [N+1] source-major offsets */
+  int32_t* in_rowptr;          /* [N+1] destination-major offsets */
+  int32_t* in_col;             /* [Mc] source of each destination-major edge */
+  float* in_weight;            /* [Mc] */
+  int32_t* out_weight_index;   /* [Mc] canonical edge -> destination-major position */
+  int64_t* n_edges;            /* device int64[1]: the coalesced edge count M */
+  void* workspace;             /* ns_topology_workspace_bytes(N, Mc) bytes, 256-byte aligned */
+  int64_t workspace_bytes;
+} ns_topology_args;
+
 /* ABI version of the loaded library (NS_ABI_VERSION). */
 int ns_abi_version(void);
 
@@ -269,6 +290,20 @@ int64_t ns_encode_workspace_bytes(void);
  * change (native_compartmental.py:114-124).  Two launches on `stream`, no
  * allocation, no host synchronisation; parity is defined for finite weights. */
 int ns_encode_weights(const ns_encode_args* args, void* stream);
+
+/* Bytes of workspace ns_build_topology needs for N neurons and Mc candidates
+ * (-1 on invalid sizes, with ns_last_error set). */
+int64_t ns_topology_workspace_bytes(int64_t n_neurons, int64_t n_candidates);
+
+/* Coalesces candidate edges (duplicates summed from zero in input order) and
+ * builds both CSR views on the device, bitwise equal to the reference's
+ * SparseTopology.from_edges on the CPU (reference:
+ * src/neurosim_gpu/topology.py:32-115).  Stable radix sorts and one lane per
+ * run of equal keys make the sums deterministic (the reference's GPU path
+ * sums duplicates with atomics).  Launches on `stream`; the caller reads
+ * *n_edges back to trim the outputs.  Indices must lie in [0, N): the caller
+ * checks them, as the reference's from_edges does before building. */
+int ns_build_topology(const ns_topology_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -112,6 +112,14 @@ class _EncodeArgs(ctypes.Structure):
                 ("global_scale", _c_ptr), ("workspace", _c_ptr)]
 
 
+class _TopologyArgs(ctypes.Structure):
+    _fields_ = [("n_neurons", _c_i64), ("n_candidates", _c_i64), ("src", _c_ptr),
+                ("dst", _c_ptr), ("weight", _c_ptr), ("out_src", _c_ptr), ("out_dst", _c_ptr),
+                ("out_weight", _c_ptr), ("out_rowptr", _c_ptr), ("in_rowptr", _c_ptr),
+                ("in_col", _c_ptr), ("in_weight", _c_ptr), ("out_weight_index", _c_ptr),
+                ("n_edges", _c_ptr), ("workspace", _c_ptr), ("workspace_bytes", _c_i64)]
+
+
 def library_path() -> Path:
     override = os.environ.get("NEUROSIM_HIP_LIB")
     if override:
@@ -145,8 +153,11 @@ def load_library() -> ctypes.CDLL:
                                    ctypes.POINTER(_c_i64)] + [_c_ptr] * 7
     lib.ns_encode_workspace_bytes.restype = _c_i64
     lib.ns_encode_workspace_bytes.argtypes = []
+    lib.ns_topology_workspace_bytes.restype = _c_i64
+    lib.ns_topology_workspace_bytes.argtypes = [_c_i64, _c_i64]
     for name, kind in (("ns_dendritic_step", _StepArgs), ("ns_dendritic_event", _EventArgs),
-                       ("ns_csr_spmm", _SpmmArgs), ("ns_encode_weights", _EncodeArgs)):
+                       ("ns_csr_spmm", _SpmmArgs), ("ns_encode_weights", _EncodeArgs),
+                       ("ns_build_topology", _TopologyArgs)):
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int
         fn.argtypes = [ctypes.POINTER(kind), _c_ptr]
@@ -196,6 +207,48 @@ def encode_weights(weight: torch.Tensor, precision: str
     stream = torch.cuda.current_stream(device).cuda_stream
     _raise_on(lib.ns_encode_weights(ctypes.byref(args), stream), lib)
     return codes[:payload], scales, scale.view(())
+
+
+def build_topology(n_neurons: int, src: torch.Tensor, dst: torch.Tensor,
+                   weight: torch.Tensor) -> dict:
+    """Coalesced graph and both CSR views built on the device (ns_build_topology).
+
+    ``src``/``dst`` are int64 and ``weight`` float32 device vectors of candidate
+    edges whose indices the caller has checked to lie in [0, n_neurons).
+    Returns the SparseTopology fields, bitwise equal to the CPU build
+    (reference topology.py:32-115).  Reads the edge count back (one sync).
+    """
+    lib = load_library()
+    device = weight.device
+    m = int(weight.numel())
+    src = src.to(torch.int64).contiguous()
+    dst = dst.to(torch.int64).contiguous()
+    weight = weight.contiguous()
+    size = int(lib.ns_topology_workspace_bytes(int(n_neurons), m))
+    if size < 0:
+        _raise_on(1, lib)
+    workspace = torch.empty(size + 256, dtype=torch.uint8, device=device)
+    base = workspace.data_ptr()
+    aligned = base + (-base) % 256
+    cap = max(m, 1)
+    out = {name: torch.empty(cap, dtype=dtype, device=device) for name, dtype in (
+        ("src", torch.int32), ("dst", torch.int32), ("weight", torch.float32),
+        ("in_col", torch.int32), ("in_weight", torch.float32), ("out_weight_index", torch.int32))}
+    out["out_rowptr"] = torch.empty(n_neurons + 1, dtype=torch.int32, device=device)
+    out["in_rowptr"] = torch.empty(n_neurons + 1, dtype=torch.int32, device=device)
+    count = torch.empty(1, dtype=torch.int64, device=device)
+    ptr = (lambda t: t.data_ptr() if m else None)
+    args = _TopologyArgs(int(n_neurons), m, ptr(src), ptr(dst), ptr(weight), out["src"].data_ptr(),
+                         out["dst"].data_ptr(), out["weight"].data_ptr(),
+                         out["out_rowptr"].data_ptr(), out["in_rowptr"].data_ptr(),
+                         out["in_col"].data_ptr(), out["in_weight"].data_ptr(),
+                         out["out_weight_index"].data_ptr(), count.data_ptr(), aligned, size)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    _raise_on(lib.ns_build_topology(ctypes.byref(args), stream), lib)
+    edges = int(count.item())
+    for name in ("src", "dst", "weight", "in_col", "in_weight", "out_weight_index"):
+        out[name] = out[name][:edges]
+    return out
 
 
 def plan_row_blocks(rowptr: torch.Tensor, batch: int, device: torch.device) -> tuple[torch.Tensor, int, int]:

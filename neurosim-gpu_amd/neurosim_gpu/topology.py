@@ -64,6 +64,14 @@ class SparseTopology:
         if source.numel() >= 2**31:
             raise ValueError("this compact topology supports fewer than 2^31 edges")
 
+        if weight.device.type == "cuda" and weight.dtype == torch.float32:
+            # On the GPU: ns_build_topology (stable sorts, each run of duplicates
+            # summed in order by one lane), bitwise equal to the CPU build below.
+            # Other weight dtypes take the torch ops below, as in the reference.
+            from .native import build_topology
+
+            return cls(n_neurons=n_neurons, **build_topology(n_neurons, source, target, weight))
+
         key = source * n_neurons + target
         # unique(sorted) + index_add in input order == stable sort then ordered sum.
         unique_key, inverse = torch.unique(key, sorted=True, return_inverse=True)
@@ -149,13 +157,17 @@ class SparseTopology:
 
 def random_topology(n_neurons: int, n_edges: int, *, device: torch.device | str,
                     dtype: torch.dtype = torch.float32, seed: int = 0,
-                    weight_scale: float = 0.15) -> SparseTopology:
+                    weight_scale: float = 0.15,
+                    build_device: torch.device | str | None = None) -> SparseTopology:
     """Uniform random sources/targets and N(0, (scale/sqrt(mean degree))^2) weights.
 
     Draw order on one generator seeded with ``seed``: src, dst, weights
     (reference topology.py:224-246).  The generator lives on ``device``, so a
     CPU graph and a GPU graph from the same seed differ; build on the CPU and
-    move the tensors for cross-device comparisons.
+    move the tensors for cross-device comparisons.  ``build_device`` (an
+    addition to the reference's signature) moves the drawn candidates there
+    before coalescing: device="cpu", build_device="cuda" gives the CPU graph's
+    exact bits, built by the GPU.
     """
     if n_neurons <= 0 or n_edges < 0:
         raise ValueError("n_neurons must be positive and n_edges non-negative")
@@ -166,6 +178,8 @@ def random_topology(n_neurons: int, n_edges: int, *, device: torch.device | str,
     dst = torch.randint(n_neurons, (n_edges,), **draw)
     scale = weight_scale / max(n_edges / n_neurons, 1.0) ** 0.5
     weight = torch.randn(n_edges, dtype=dtype, device=device, generator=generator) * scale
+    if build_device is not None:
+        src, dst, weight = src.to(build_device), dst.to(build_device), weight.to(build_device)
     return SparseTopology.from_edges(n_neurons, src, dst, weight)
 
 

@@ -92,9 +92,10 @@ def build(n: int, src: np.ndarray, dst: np.ndarray, weight: np.ndarray) -> Graph
     unique_key = sorted_key[first]
     starts = np.flatnonzero(first)
     sizes = np.diff(np.append(starts, sorted_key.size))
-    # Strictly sequential sums per run of equal keys: the j-th element of
-    # every run with more than j elements is added in round j.
-    canonical_weight = sorted_weight[starts].copy()
+    # Strictly sequential sums from zero per run of equal keys (the reference's
+    # zeros(...).index_add: a lone -0.0 weight becomes +0.0): the j-th element
+    # of every run with more than j elements is added in round j.
+    canonical_weight = np.zeros(starts.size, dtype=sorted_weight.dtype) + sorted_weight[starts]
     for j in range(1, int(sizes.max()) if sizes.size else 0):
         runs = np.flatnonzero(sizes > j)
         canonical_weight[runs] = canonical_weight[runs] + sorted_weight[starts[runs] + j]

@@ -34,3 +34,12 @@ def gpu():
 
     load_library()  # a missing library fails the GPU tests loudly
     return torch.device("cuda:0")
+
+
+@pytest.fixture(scope="session")
+def large_case(gpu):
+    """The headline graph: random_topology(166000, 25M candidates, seed 0), built once."""
+    from cases import make_case
+
+    print("building N=166000 M=25000000 graph", flush=True)
+    return make_case(166_000, 25_000_000, 0, gpu)

@@ -32,7 +32,8 @@ def test_every_declared_symbol_is_exported(lib):
     assert set(names) == {"ns_abi_version", "ns_last_error", "ns_block_edges",
                           "ns_plan_row_blocks", "ns_dendritic_step", "ns_dendritic_event",
                           "ns_csr_spmm", "ns_plan_panels", "ns_panel_geometry",
-                          "ns_encode_workspace_bytes", "ns_encode_weights"}
+                          "ns_encode_workspace_bytes", "ns_encode_weights",
+                          "ns_topology_workspace_bytes", "ns_build_topology"}
     for name in names:
         assert hasattr(lib, name), name
     assert lib.ns_abi_version() == native.ABI_VERSION
@@ -171,3 +172,30 @@ def test_encoder_validation_messages(lib):
     assert rc != 0 and "4-byte aligned" in message
     rc, message = call(n_edges=-1)
     assert rc != 0 and "n_edges" in message
+
+
+def test_topology_builder_validation(lib):
+    """ns_build_topology and its workspace query reject bad sizes before any launch."""
+    assert lib.ns_topology_workspace_bytes(0, 10) == -1
+    assert b"N must be" in lib.ns_last_error()
+    assert lib.ns_topology_workspace_bytes(10, -1) == -1
+    # The sort's scratch size comes from the device, so without a GPU the
+    # query reports that instead of a size.
+    small = lib.ns_topology_workspace_bytes(1000, 20_000)
+    assert small > 0 or b"temporary storage" in lib.ns_last_error()
+
+    def call(**fields):
+        base = dict(n_neurons=10, n_candidates=0, out_rowptr=256, in_rowptr=256, n_edges=256,
+                    workspace=256, workspace_bytes=1 << 30)
+        base.update(fields)
+        rc = lib.ns_build_topology(ctypes.byref(native._TopologyArgs(**base)), None)
+        return rc, lib.ns_last_error().decode()
+
+    rc, message = call(n_candidates=1 << 31)
+    assert rc != 0 and "2^31 edges" in message
+    rc, message = call(n_candidates=5)
+    assert rc != 0 and "src, dst and weight" in message
+    rc, message = call(n_candidates=5, src=256, dst=256, weight=256)
+    assert rc != 0 and "every edge output" in message
+    rc, message = call(workspace_bytes=16)
+    assert rc != 0 and ("workspace" in message or "temporary storage" in message)

@@ -242,12 +242,6 @@ def test_cfg2_batched_fp32_1000_ticks(gpu):
     assert worst <= 1e-5
 
 
-@pytest.fixture(scope="module")
-def large_case(gpu):
-    print("building N=166000 M=25000000 graph", flush=True)
-    return make_case(166_000, 25_000_000, 0, gpu)
-
-
 @pytest.mark.parametrize("fmt", ["fp8", "nvfp4"])
 def test_device_encoder_is_bitwise_the_oracle_at_25m_edges(gpu, large_case, fmt):
     """Codes, block scales and global scale encoded on the GPU == the CPU oracle's.
@@ -307,7 +301,7 @@ def test_cfg5_scaleout_fp8_10_ticks(gpu):
     """N=1000000, M~100M, B=16, drive [16,1] U(0,.4) seed 1, fp8 weights: 10 ticks vs
     the oracle's float32 run on the decoded weights (the graph's two constructions
     are compared bitwise at the smaller sizes; here the oracle reads the product's
-    host CSR arrays)."""
+    host CSR arrays, and the device build of the graph is checked against them)."""
     print("case cfg5 N=1000000 M=100M B=16 fp8 ticks=10", flush=True)
     n, batch = 1_000_000, 16
     topology_cpu = random_topology(n, 100_000_000, device="cpu", seed=0)
@@ -317,8 +311,13 @@ def test_cfg5_scaleout_fp8_10_ticks(gpu):
                        in_rowptr=topology_cpu.in_rowptr.numpy(), in_col=topology_cpu.in_col.numpy(),
                        in_weight=topology_cpu.in_weight.numpy(),
                        out_weight_index=topology_cpu.out_weight_index.numpy())
+    # The same candidates coalesced on the GPU (ns_build_topology) give the same graph.
+    topology = random_topology(n, 100_000_000, device="cpu", seed=0, build_device=gpu)
+    for name in ("src", "dst", "weight", "out_rowptr", "in_rowptr", "in_col", "in_weight",
+                 "out_weight_index"):
+        assert torch.equal(getattr(topology, name).cpu(), getattr(topology_cpu, name)), name
     model, params = standard_model(n)
-    native = NativeDendriticMatrixRuntime(topology_to(topology_cpu, gpu), model_to(model, gpu),
+    native = NativeDendriticMatrixRuntime(topology, model_to(model, gpu),
                                           torch.zeros(batch, n, device=gpu), weight_format="fp8")
     oracle = ort.MatrixOracle(graph, params, torch.zeros(batch, n),
                               in_weight=op.quantize_dequantize(graph.in_weight, "fp8"))

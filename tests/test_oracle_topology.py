@@ -71,6 +71,19 @@ def test_duplicates_sum_in_input_order():
     assert graph.weight[0] == expected
 
 
+def test_sums_start_from_zero():
+    """zeros(...).index_add (topology.py:76-80): a lone -0.0 weight is stored as +0.0,
+    in the oracle and in the product's CPU build alike."""
+    src = np.array([0, 1, 1], np.int64)
+    dst = np.array([1, 2, 2], np.int64)
+    weight = np.array([-0.0, -0.0, -0.0], np.float32)
+    graph = otop.build(3, src, dst, weight)
+    product = SparseTopology.from_edges(3, torch.from_numpy(src), torch.from_numpy(dst),
+                                        torch.from_numpy(weight))
+    assert not np.signbit(graph.weight).any()
+    assert graph.weight.tobytes() == product.weight.numpy().tobytes()
+
+
 def test_product_topology_equals_oracle_bitwise():
     for n, m, seed in ((97, 600, 83), (1024, 20480, 23), (50, 3000, 1)):
         product = random_topology(n, m, device="cpu", seed=seed)
