@@ -180,6 +180,34 @@ typedef struct ns_spmm_args {
   ns_out_plane out;            /* J, [B,N]; must not overlap `source` */
 } ns_spmm_args;
 
+/* Arguments of the backward of one fused matrix tick (float32 weights). */
+typedef struct ns_step_grad_args {
+  int64_t n_neurons;           /* N > 0 */
+  int64_t batch;               /* B >= 0; B == 0 launches nothing */
+  ns_plane state;              /* the forward's inputs, as passed to ns_dendritic_step */
+  ns_plane dendrite;
+  ns_plane adaptation;
+  ns_plane drive;
+  ns_plane dendritic_drive;
+  ns_vector params[6];
+  ns_csr matrix;               /* NS_WEIGHT_F32 only */
+  ns_row_plan plan;            /* row plan of `matrix` for batch width B */
+  const int32_t* out_rowptr;   /* source-major view of the same graph: [N+1] */
+  const int32_t* dst;          /* [M] */
+  const int32_t* out_weight_index;  /* [M]: canonical edge -> CSR position */
+  ns_plane grad_state;         /* upstream gradients of s', d', a'; a NULL plane with */
+  ns_plane grad_dendrite;      /* scalar 0 means zero */
+  ns_plane grad_adaptation;
+  ns_out_plane d_state;        /* required */
+  ns_out_plane d_dendrite;     /* required */
+  ns_out_plane d_adaptation;   /* required */
+  ns_out_plane d_drive;        /* data NULL: not computed */
+  ns_out_plane d_dendritic_drive;
+  float* d_weight;             /* [M] in CSR order; NULL: not computed */
+  float* d_params[6];          /* [N] each, per neuron; NULL: not computed */
+  float* workspace;            /* ns_step_backward_workspace_floats(N, B) floats */
+} ns_step_grad_args;
+
 /* Arguments of one weight encoding (fp8 e4m3 or NVFP4 CSR payload). */
 typedef struct ns_encode_args {
   const float* weight;         /* [n_edges] float32 in CSR order, 16-byte aligned */
@@ -278,6 +306,19 @@ int ns_dendritic_event(const ns_event_args* args, void* stream);
  * Replaces MatrixRuntime._propagate (reference: runtime.py:78-79) for device
  * float32 operands, e.g. the persistent current W @ emitted of runtime.py:124,220. */
 int ns_csr_spmm(const ns_spmm_args* args, void* stream);
+
+/* Floats of workspace ns_dendritic_step_backward needs (2*N*B). */
+int64_t ns_step_backward_workspace_floats(int64_t n_neurons, int64_t batch);
+
+/* Gradients of one fused float32 matrix tick: given the forward's inputs and
+ * upstream gradients of (s', d', a'), writes the gradients of the three
+ * states, of tensor drives, of the six parameter vectors (per neuron) and of
+ * the CSR weights.  Replaces autograd through the reference's torch step,
+ * which the reference's native runtime falls back to whenever a gradient is
+ * needed (reference: src/neurosim_gpu/native_compartmental.py:104-108; the
+ * step compartmental.py:152-183 and runtime.py:78-79, the CSR gradients as
+ * in compartmental.py:40-56).  No atomics: results are deterministic. */
+int ns_dendritic_step_backward(const ns_step_grad_args* args, void* stream);
 
 /* Bytes of the workspace ns_encode_weights needs (independent of M). */
 int64_t ns_encode_workspace_bytes(void);

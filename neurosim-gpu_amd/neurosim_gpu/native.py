@@ -106,6 +106,18 @@ class _SpmmArgs(ctypes.Structure):
                 ("matrix", _Csr), ("plan", _RowPlan), ("out", _OutPlane)]
 
 
+class _StepGradArgs(ctypes.Structure):
+    _fields_ = [("n_neurons", _c_i64), ("batch", _c_i64),
+                ("state", _Plane), ("dendrite", _Plane), ("adaptation", _Plane),
+                ("drive", _Plane), ("dendritic_drive", _Plane),
+                ("params", _Vector * 6), ("matrix", _Csr), ("plan", _RowPlan),
+                ("out_rowptr", _c_ptr), ("dst", _c_ptr), ("out_weight_index", _c_ptr),
+                ("grad_state", _Plane), ("grad_dendrite", _Plane), ("grad_adaptation", _Plane),
+                ("d_state", _OutPlane), ("d_dendrite", _OutPlane), ("d_adaptation", _OutPlane),
+                ("d_drive", _OutPlane), ("d_dendritic_drive", _OutPlane),
+                ("d_weight", _c_ptr), ("d_params", _c_ptr * 6), ("workspace", _c_ptr)]
+
+
 class _EncodeArgs(ctypes.Structure):
     _fields_ = [("weight", _c_ptr), ("n_edges", _c_i64), ("format", ctypes.c_int32),
                 ("reserved", ctypes.c_int32), ("codes", _c_ptr), ("block_scales", _c_ptr),
@@ -153,11 +165,14 @@ def load_library() -> ctypes.CDLL:
                                    ctypes.POINTER(_c_i64)] + [_c_ptr] * 7
     lib.ns_encode_workspace_bytes.restype = _c_i64
     lib.ns_encode_workspace_bytes.argtypes = []
+    lib.ns_step_backward_workspace_floats.restype = _c_i64
+    lib.ns_step_backward_workspace_floats.argtypes = [_c_i64, _c_i64]
     lib.ns_topology_workspace_bytes.restype = _c_i64
     lib.ns_topology_workspace_bytes.argtypes = [_c_i64, _c_i64]
     for name, kind in (("ns_dendritic_step", _StepArgs), ("ns_dendritic_event", _EventArgs),
                        ("ns_csr_spmm", _SpmmArgs), ("ns_encode_weights", _EncodeArgs),
-                       ("ns_build_topology", _TopologyArgs)):
+                       ("ns_build_topology", _TopologyArgs),
+                       ("ns_dendritic_step_backward", _StepGradArgs)):
         fn = getattr(lib, name)
         fn.restype = ctypes.c_int
         fn.argtypes = [ctypes.POINTER(kind), _c_ptr]
@@ -605,6 +620,62 @@ class NativeExtension:
         stream = torch.cuda.current_stream(state.device).cuda_stream
         _raise_on(self.lib.ns_dendritic_event(ctypes.byref(args), stream), self.lib)
         return outs
+
+    def dendritic_step_backward(self, state, dendrite, adaptation, params, rowptr, source,
+                                weight, input, input_scalar, dendritic_input, dendritic_scalar,
+                                out_rowptr, dst, weight_index, grad_state, grad_dendrite,
+                                grad_adaptation, *, need_drive=False, need_dendritic=False,
+                                need_weight=False, need_params=(False,) * 6):
+        """Gradients of one float32 tick (ns_dendritic_step_backward).
+
+        Returns (d_state, d_dendrite, d_adaptation, d_drive, d_dendritic_drive,
+        d_weight, [d_param x 6]); entries not asked for are None.  Upstream
+        gradients may be None (zero).
+        """
+        _check_state(state)
+        batch, n = state.shape
+        args = _StepGradArgs()
+        args.n_neurons, args.batch = n, batch
+        args.state = _plane(state, state, "state")
+        args.dendrite = _plane(dendrite, state, "dendrite")
+        args.adaptation = _plane(adaptation, state, "adaptation")
+        args.params = _params(params, state)
+        args.drive = _drive(input, input_scalar, state)
+        args.dendritic_drive = _drive(dendritic_input, dendritic_scalar, state)
+        if weight.dtype != torch.float32:
+            raise RuntimeError("the tick backward needs float32 weights")
+        args.matrix = self._csr(state, rowptr, source, weight, None, None)
+        args.plan = self.plan_for(rowptr, batch)
+        for index in (out_rowptr, dst, weight_index):
+            _index(index, state)
+        if out_rowptr.numel() != n + 1 or dst.numel() != weight.numel() or \
+                weight_index.numel() != weight.numel():
+            raise RuntimeError("invalid source-major topology geometry")
+        args.out_rowptr, args.dst = out_rowptr.data_ptr(), dst.data_ptr()
+        args.out_weight_index = weight_index.data_ptr()
+        args.grad_state = _drive(grad_state, 0.0, state)
+        args.grad_dendrite = _drive(grad_dendrite, 0.0, state)
+        args.grad_adaptation = _drive(grad_adaptation, 0.0, state)
+        planes = new_planes(3 + int(need_drive) + int(need_dendritic), batch, n, state)
+        args.d_state, args.d_dendrite, args.d_adaptation = (_out(o) for o in planes[:3])
+        rest = iter(planes[3:])
+        d_drive = next(rest) if need_drive else None
+        d_dendritic = next(rest) if need_dendritic else None
+        args.d_drive = _out(d_drive) if d_drive is not None else _OutPlane(None, 0, 0)
+        args.d_dendritic_drive = (_out(d_dendritic) if d_dendritic is not None
+                                  else _OutPlane(None, 0, 0))
+        d_weight = torch.empty_like(weight) if need_weight else None
+        args.d_weight = d_weight.data_ptr() if d_weight is not None and weight.numel() else None
+        d_params = [torch.empty(n, dtype=torch.float32, device=state.device) if want else None
+                    for want in need_params]
+        for i, value in enumerate(d_params):
+            args.d_params[i] = value.data_ptr() if value is not None else None
+        workspace = torch.empty(int(self.lib.ns_step_backward_workspace_floats(n, batch)),
+                                dtype=torch.float32, device=state.device)
+        args.workspace = workspace.data_ptr() if workspace.numel() else None
+        stream = torch.cuda.current_stream(state.device).cuda_stream
+        _raise_on(self.lib.ns_dendritic_step_backward(ctypes.byref(args), stream), self.lib)
+        return (*planes[:3], d_drive, d_dendritic, d_weight, d_params)
 
     def csr_spmm(self, source, rowptr, col, weight, block_scales=None, global_scale=None):
         _check_state(source)

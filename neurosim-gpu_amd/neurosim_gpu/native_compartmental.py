@@ -9,10 +9,13 @@ API of the reference's native_compartmental module
 * NativeDendriticPELSRuntime -- two kernels per tick: advance + emission
   threshold, then the emitters' out-edge scatter into the persistent current.
 
-Requests that need autograd (any tensor with requires_grad under grad mode)
-or PELS statistics run the PyTorch reference step instead and say so in
-``last_backend`` ("reference-autograd" / "reference-stats"); reduced weight
-storage is inference-only.  The native library must be present: a missing
+Matrix ticks that need autograd (any tensor with requires_grad under grad
+mode) run the same native forward with a native backward
+(ns_dendritic_step_backward; ``last_backend`` "native-autograd"), where the
+reference falls back to its torch step.  PELS ticks that need autograd or
+statistics run the PyTorch reference step and say so in ``last_backend``
+("reference-autograd" / "reference-stats"); reduced weight storage is
+inference-only.  The native library must be present: a missing
 library raises at construction, nothing falls back silently.
 """
 
@@ -67,6 +70,47 @@ class _NativeCompartments:
         topology = self.topology
         return self.extension.csr_spmm(source.detach(), topology.in_rowptr, topology.in_col,
                                        topology.in_weight.detach())
+
+
+class _NativeTick(torch.autograd.Function):
+    """One float32 fused tick (ns_dendritic_step) whose backward is native too
+    (ns_dendritic_step_backward): gradients of the states, tensor drives, the
+    six parameter vectors and the CSR weights, as autograd through the
+    reference's torch step would give them."""
+
+    @staticmethod
+    def forward(ctx, info, state, dendrite, adaptation, weight, drive, dendritic_drive, *params):
+        extension, topology, us, vs, width, extra = info
+        outs = extension.dendritic_step(state, dendrite, adaptation, list(params),
+                                        topology.in_rowptr, topology.in_col, weight,
+                                        drive, us, dendritic_drive, vs, width, **extra)
+        ctx.info = info
+        ctx.has_drive = (drive is not None, dendritic_drive is not None)
+        saved = [state, dendrite, adaptation, weight, *params]
+        saved += [t for t in (drive, dendritic_drive) if t is not None]
+        ctx.save_for_backward(*saved)
+        ctx.set_materialize_grads(False)
+        return tuple(outs)
+
+    @staticmethod
+    def backward(ctx, grad_state, grad_dendrite, grad_adaptation):
+        extension, topology, us, vs, _, _ = ctx.info
+        saved = list(ctx.saved_tensors)
+        state, dendrite, adaptation, weight = saved[:4]
+        params = saved[4:10]
+        rest = iter(saved[10:])
+        drive = next(rest) if ctx.has_drive[0] else None
+        dendritic_drive = next(rest) if ctx.has_drive[1] else None
+        needs = ctx.needs_input_grad
+        (d_state, d_dendrite, d_adaptation, d_drive, d_dendritic, d_weight,
+         d_params) = extension.dendritic_step_backward(
+            state, dendrite, adaptation, params, topology.in_rowptr, topology.in_col, weight,
+            drive, us, dendritic_drive, vs, topology.out_rowptr, topology.dst,
+            topology.out_weight_index, grad_state, grad_dendrite, grad_adaptation,
+            need_drive=bool(needs[5]), need_dendritic=bool(needs[6]), need_weight=bool(needs[4]),
+            need_params=tuple(bool(x) for x in needs[7:13]))
+        return (None, d_state if needs[1] else None, d_dendrite if needs[2] else None,
+                d_adaptation if needs[3] else None, d_weight, d_drive, d_dendritic, *d_params)
 
 
 class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
@@ -182,8 +226,10 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         if self._needs_autograd(drive, dendritic_drive):
             if self.weight_format is not None or self.weight_dtype == torch.float16:
                 raise RuntimeError("native reduced-precision weight storage is inference-only")
-            self.last_backend = "reference-autograd"
-            return super().step(drive, dendritic_drive=dendritic_drive)
+            if not isinstance(self.extension, NativeExtension):
+                self.last_backend = "reference-autograd"
+                return super().step(drive, dendritic_drive=dendritic_drive)
+            return self._autograd_step(drive, dendritic_drive)
         u, us = self._drive(drive)
         v, vs = self._drive(dendritic_drive)
         weight, scales, backend = self._weights()
@@ -195,6 +241,21 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
             self.topology.in_rowptr, self.topology.in_col, weight,
             u, us, v, vs, self.threads_per_row, *scales, **extra)
         self.last_backend = backend
+        return self.state
+
+
+    def _autograd_step(self, drive, dendritic_drive) -> torch.Tensor:
+        """A float32 tick recorded for autograd, native forward and backward."""
+        u, us = self._drive(drive)
+        v, vs = self._drive(dendritic_drive)
+        weight = self.topology.in_weight
+        # The row kernel reads in_weight itself on every tick, so weights an
+        # optimizer updates in place are never served from a slot-order copy.
+        info = (self.extension, self.topology, us, vs, self.threads_per_row, {})
+        self.state, self.dendritic_state, self.adaptation_state = _NativeTick.apply(
+            info, self.state, self.dendritic_state, self.adaptation_state, weight, u, v,
+            *self._parameters())
+        self.last_backend = "native-autograd"
         return self.state
 
 

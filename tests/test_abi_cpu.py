@@ -33,7 +33,8 @@ def test_every_declared_symbol_is_exported(lib):
                           "ns_plan_row_blocks", "ns_dendritic_step", "ns_dendritic_event",
                           "ns_csr_spmm", "ns_plan_panels", "ns_panel_geometry",
                           "ns_encode_workspace_bytes", "ns_encode_weights",
-                          "ns_topology_workspace_bytes", "ns_build_topology"}
+                          "ns_topology_workspace_bytes", "ns_build_topology",
+                          "ns_step_backward_workspace_floats", "ns_dendritic_step_backward"}
     for name in names:
         assert hasattr(lib, name), name
     assert lib.ns_abi_version() == native.ABI_VERSION
@@ -199,3 +200,31 @@ def test_topology_builder_validation(lib):
     assert rc != 0 and "every edge output" in message
     rc, message = call(workspace_bytes=16)
     assert rc != 0 and ("workspace" in message or "temporary storage" in message)
+
+
+def test_backward_validation_messages(lib):
+    """ns_dendritic_step_backward rejects bad arguments before any launch."""
+    assert lib.ns_step_backward_workspace_floats(100, 3) == 600
+
+    def call(**fields):
+        args = native._StepGradArgs()
+        args.n_neurons, args.batch = 10, 1
+        for i in range(6):
+            args.params[i] = native._Vector(256, 1)
+        args.matrix = native._Csr(10, 0, 256, None, 256, native.WEIGHT_F32, None, None)
+        for name, value in fields.items():
+            setattr(args, name, value)
+        rc = lib.ns_dendritic_step_backward(ctypes.byref(args), None)
+        return rc, lib.ns_last_error().decode()
+
+    rc, message = call(n_neurons=0)
+    assert rc != 0 and "N must be" in message
+    rc, message = call(matrix=native._Csr(10, 0, 256, None, 256, native.WEIGHT_E4M3, None, None))
+    assert rc != 0 and "float32 weights" in message
+    params = (native._Vector * 6)(*[native._Vector(256, 1)] * 5, native._Vector(None, 0))
+    rc, message = call(params=params)
+    assert rc != 0 and "parameter" in message
+    rc, message = call(batch=0)
+    assert rc == 0
+    rc, message = call()
+    assert rc != 0 and "state, dendrite and adaptation" in message

@@ -52,7 +52,11 @@ def test_parameter_and_drive_gradients_use_reference(gpu):
         for a, e in zip(actual, expected):
             torch.testing.assert_close(a, e, atol=2e-5, rtol=2e-4)
             assert float(a.abs().sum()) > 0
-        assert native.last_backend == "reference-autograd"
+        # The reference's native runtimes both fall back to the torch step here;
+        # the matrix runtime here differentiates its own kernels instead.
+        expected_backend = ("native-autograd" if kind is NativeDendriticMatrixRuntime
+                            else "reference-autograd")
+        assert native.last_backend == expected_backend
 
 
 def test_parameters_remain_live_under_no_grad(gpu):

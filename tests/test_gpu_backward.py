@@ -1,0 +1,164 @@
+"""Native float32 backward of the matrix tick (ns_dendritic_step_backward)
+against autograd through the PyTorch reference step.
+
+The reference's native runtime records no graph of its own: whenever a
+gradient is needed it runs its torch step (native_compartmental.py:104-108),
+and autograd differentiates torch.sparse.mm and the update ops.  Here the
+same gradients come from HIP kernels.  The reference for the comparison is
+that torch step run by autograd in float64 on the CPU on the same inputs, so
+the tolerance (1e-4 of the largest gradient of each tensor) covers only the
+native float32 arithmetic.  Covers one tick with every input requiring a
+gradient (states, [B,N] and [B,1] drives, the six parameters, the weights),
+eight-tick backpropagation through time, scalar drives, stride-0 parameters,
+and repeatability.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import topology as otop
+from neurosim_gpu import (DendriticDynamics, DendriticMatrixRuntime, Dynamics,
+                          NativeDendriticMatrixRuntime, SparseTopology)
+
+pytestmark = pytest.mark.gpu
+
+
+def graph(n: int, m: int, seed: int) -> otop.Graph:
+    return otop.random_graph(n, m, seed=seed)
+
+
+def topology(g: otop.Graph, dtype, device) -> SparseTopology:
+    fields = dict(src=g.src, dst=g.dst, weight=g.weight, out_rowptr=g.out_rowptr,
+                  in_rowptr=g.in_rowptr, in_col=g.in_col, out_weight_index=g.out_weight_index,
+                  in_weight=g.in_weight)
+    tensors = {k: torch.from_numpy(np.asarray(v)) for k, v in fields.items()}
+    for k in ("weight", "in_weight"):
+        tensors[k] = tensors[k].to(dtype)
+    return SparseTopology(n_neurons=g.n, **{k: v.to(device) for k, v in tensors.items()})
+
+
+def leaf(value: np.ndarray, dtype, device) -> torch.Tensor:
+    return torch.tensor(value, dtype=dtype, device=device).requires_grad_(True)
+
+
+def model(values: dict, dtype, device, expanded: bool) -> DendriticDynamics:
+    def vec(name):
+        if expanded and name in ("coupling", "strength"):
+            return leaf(values[name][:1], dtype, device)[0].expand(values["alpha"].size)
+        return leaf(values[name], dtype, device)
+    return DendriticDynamics(Dynamics(vec("alpha"), vec("gain")), vec("rho_d"), vec("rho_a"),
+                             vec("coupling"), vec("strength"))
+
+
+def params_of(m: DendriticDynamics):
+    return [m.soma.alpha, m.soma.gain, m.dendrite_decay, m.adaptation_decay, m.coupling,
+            m.adaptation_strength]
+
+
+def base(p):
+    """The leaf behind a parameter (an expanded scalar's 0-d base)."""
+    return p._base if p._base is not None else p
+
+
+def run(runtime_cls, g, inputs, dtype, device, ticks, *, scalar_drives, expanded, **kw):
+    topo = topology(g, dtype, device)
+    topo.in_weight.requires_grad_(True)
+    mdl = model(inputs["params"], dtype, device, expanded)
+    state0 = leaf(inputs["state"], dtype, device)
+    rt = runtime_cls(topo, mdl, state0.detach(), **kw)
+    rt.state = state0
+    rt.dendritic_state = leaf(inputs["dendrite"], dtype, device)
+    rt.adaptation_state = leaf(inputs["adaptation"], dtype, device)
+    dendrite0, adaptation0 = rt.dendritic_state, rt.adaptation_state
+    if scalar_drives:
+        drive, dendritic = 0.2, 0.1
+    else:
+        drive = leaf(inputs["drive"], dtype, device)
+        dendritic = leaf(inputs["dendritic"], dtype, device)
+    for _ in range(ticks):
+        rt.step(drive, dendritic_drive=dendritic)
+    r = {k: torch.tensor(v, dtype=dtype, device=device) for k, v in inputs["probe"].items()}
+    loss = (rt.state * r["s"]).sum() + (rt.dendritic_state * r["d"]).sum() + \
+        (rt.adaptation_state * r["a"]).sum()
+    loss.backward()
+    grads = {"weight": topo.in_weight.grad, "state": state0.grad, "dendrite": dendrite0.grad,
+             "adaptation": adaptation0.grad}
+    if not scalar_drives:
+        grads["drive"], grads["dendritic"] = drive.grad, dendritic.grad
+    for name, p in zip(("alpha", "gain", "rho_d", "rho_a", "coupling", "strength"), params_of(mdl)):
+        grads[name] = base(p).grad
+    return grads, rt
+
+
+def inputs_for(g, batch, seed):
+    rng = np.random.default_rng(seed)
+    n = g.n
+    return {
+        "state": rng.uniform(0, 1, (batch, n)), "dendrite": rng.uniform(-1, 1, (batch, n)),
+        "adaptation": rng.uniform(0, 1, (batch, n)),
+        "drive": rng.uniform(-0.5, 0.8, (batch, n)), "dendritic": rng.uniform(-0.3, 0.3, (batch, 1)),
+        "params": {"alpha": rng.uniform(0.5, 0.9, n), "gain": rng.uniform(0.5, 1.5, n),
+                   "rho_d": rng.uniform(0.5, 0.95, n), "rho_a": rng.uniform(0.8, 0.99, n),
+                   "coupling": rng.uniform(0.2, 0.8, n), "strength": rng.uniform(0.05, 0.4, n)},
+        "probe": {"s": rng.standard_normal((batch, n)), "d": rng.standard_normal((batch, n)),
+                  "a": rng.standard_normal((batch, n))},
+    }
+
+
+def compare(native: dict, reference: dict, rtol: float = 1e-4) -> None:
+    assert native.keys() == reference.keys()
+    for name, want in reference.items():
+        got = native[name]
+        assert got is not None and want is not None, name
+        got = got.detach().double().cpu().reshape(want.shape)
+        scale = float(want.abs().max())
+        err = float((got - want.cpu()).abs().max())
+        assert err <= rtol * max(scale, 1e-12), f"{name}: max error {err:.3e}, scale {scale:.3e}"
+
+
+@pytest.mark.parametrize("ticks,batch,scalar_drives,expanded", [
+    (1, 3, False, False), (1, 1, True, True), (8, 2, False, True), (8, 4, True, False)])
+def test_gradients_match_autograd_of_the_torch_step(gpu, ticks, batch, scalar_drives, expanded):
+    print(f"case backward ticks={ticks} batch={batch} scalar_drives={scalar_drives} "
+          f"expanded={expanded}", flush=True)
+    g = graph(600, 12_000, 9)
+    inputs = inputs_for(g, batch, ticks * 10 + batch)
+    kw = dict(scalar_drives=scalar_drives, expanded=expanded)
+    native, rt = run(NativeDendriticMatrixRuntime, g, inputs, torch.float32, gpu, ticks, **kw)
+    assert rt.last_backend == "native-autograd"
+    reference, _ = run(DendriticMatrixRuntime, g, inputs, torch.float64, "cpu", ticks, **kw)
+    compare(native, reference)
+
+
+def test_backward_is_repeatable(gpu):
+    print("case backward repeatable", flush=True)
+    g = graph(2000, 60_000, 3)
+    inputs = inputs_for(g, 2, 5)
+    first, _ = run(NativeDendriticMatrixRuntime, g, inputs, torch.float32, gpu, 4,
+                   scalar_drives=False, expanded=False)
+    second, _ = run(NativeDendriticMatrixRuntime, g, inputs, torch.float32, gpu, 4,
+                    scalar_drives=False, expanded=False)
+    for name in first:
+        assert torch.equal(first[name], second[name]), name
+
+
+def test_forward_of_a_recorded_tick_equals_the_inference_tick(gpu):
+    """Recording for autograd changes nothing in the forward values."""
+    print("case backward forward values", flush=True)
+    g = graph(1000, 20_000, 0)
+    topo = topology(g, torch.float32, gpu)
+    soma = Dynamics(torch.full((1000,), .72, device=gpu), torch.full((1000,), .8, device=gpu))
+    mdl = DendriticDynamics.from_time_constants(soma, dt=1., tau_dendrite=4., tau_adaptation=25.)
+    plain = NativeDendriticMatrixRuntime(topo, mdl, torch.zeros(2, 1000, device=gpu), kernel="rows")
+    recorded = NativeDendriticMatrixRuntime(topo, mdl, torch.zeros(2, 1000, device=gpu), kernel="rows")
+    drive = torch.full((2, 1000), 0.2, device=gpu, requires_grad=True)
+    for _ in range(5):
+        with torch.no_grad():
+            plain.step(drive.detach(), dendritic_drive=0.1)
+        recorded.step(drive, dendritic_drive=0.1)
+    assert recorded.last_backend == "native-autograd"
+    assert torch.equal(plain.state, recorded.state.detach())
+    assert torch.equal(plain.dendritic_state, recorded.dendritic_state.detach())
