@@ -16,8 +16,9 @@ adds the other workloads, each timed the same way: the batched tick
 (N=50000, M~1M, B=8, per-column drive), the PELS event tick (N=50000, M~1M,
 B=1, theta 0.02, driven and with inputs withdrawn), the scale-out tick
 (N=1000000, M~100M, B=16, fp8 weights, 200 graph-captured ticks, with the
-CPU oracle on a 10-tick sample), and the fp8/NVFP4 device encoding of the
-headline graph's weights.
+CPU oracle on a 10-tick sample), the fp8/NVFP4 device encoding of the
+headline graph's weights, and one recorded tick plus its native backward on
+the headline graph next to autograd through the torch step.
 
     python bench.py [--gpus 1] [--steps 1000] [--warmup 50]
 """
@@ -25,6 +26,7 @@ headline graph's weights.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import sys
@@ -249,6 +251,57 @@ def measure_encode(weight: torch.Tensor, repeats: int = 20) -> dict:
     return out
 
 
+def measure_backward(topology, model, repeats: int = 10) -> dict:
+    """One recorded fp32 tick plus its backward on the headline graph (B=1,
+    every parameter, the weights and the state requiring gradients, loss =
+    sum of the new state): the native backward against autograd through the
+    torch step that the reference runs for such ticks, each timed with HIP
+    events over ``repeats`` forward+backward passes."""
+    from neurosim_gpu import DendriticMatrixRuntime
+
+    n = topology.n_neurons
+    weight = topology.in_weight.detach().clone().requires_grad_(True)
+    trained = dataclasses.replace(topology, in_weight=weight)
+    params = [p.detach().clone().requires_grad_(True) for p in (
+        model.soma.alpha, model.soma.gain, model.dendrite_decay, model.adaptation_decay,
+        model.coupling, model.adaptation_strength)]
+    dyn = DendriticDynamics(Dynamics(params[0], params[1]), *params[2:])
+    out = {"workload": f"one fp32 tick + backward, N={n} M={topology.n_edges} B=1, gradients of "
+                       "the weights, the six parameters and the state", "repeats": repeats}
+    for name, cls in (("native", NativeDendriticMatrixRuntime), ("torch_autograd", DendriticMatrixRuntime)):
+        state = torch.full((1, n), 0.2, device=weight.device)
+        runtime = cls(trained, dyn, state)
+
+        def once():
+            runtime.state = state.clone().requires_grad_(True)
+            runtime.dendritic_state = torch.zeros_like(state)
+            runtime.adaptation_state = torch.zeros_like(state)
+            runtime.step(0.2, dendritic_drive=0.1)
+            runtime.state.sum().backward()
+
+        try:
+            for _ in range(2):
+                once()
+        except RuntimeError as error:      # a torch sparse backward this ROCm build lacks
+            out[f"{name}_ms"] = None
+            out[f"{name}_error"] = str(error).splitlines()[0][:200]
+            del runtime
+            continue
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(repeats):
+            once()
+        end.record()
+        torch.cuda.synchronize()
+        out[f"{name}_ms"] = round(start.elapsed_time(end) / repeats, 4)
+        weight.grad = None
+        for p in params:
+            p.grad = None
+        del runtime
+    return out
+
+
 def measure_batched(device) -> dict:
     """N=50000, M~1M, B=8, drive [8,1] U(0,.4) (seed 1), dendritic .1, fp32, 1000 ticks."""
     n, candidates, batch = 50_000, 1_000_000, 8
@@ -392,7 +445,7 @@ def main() -> None:
                      help="tick kernel: LDS column panels (batch 1-2) or CSR row blocks")
     cli.add_argument("--copy-calibration", action="store_true",
                      help="only run 256 MiB device copies (PMC byte-counter calibration)")
-    cli.add_argument("--configs", default="encode,batched,pels,scaleout",
+    cli.add_argument("--configs", default="encode,backward,batched,pels,scaleout",
                      help="other workloads to time after the headline one ('none' for none)")
     args = cli.parse_args()
     if args.gpus != 1:
@@ -459,9 +512,13 @@ def main() -> None:
         log("timing encode")
         extra["encode"] = measure_encode(topology.in_weight)
         log(f"encode: {extra['encode']}")
+    if "backward" in configs:
+        log("timing backward")
+        extra["backward"] = measure_backward(topology, model)
+        log(f"backward: {extra['backward']}")
     del topology
     torch.cuda.empty_cache()
-    for name in [c for c in configs if c != "encode"]:
+    for name in [c for c in configs if c not in ("encode", "backward")]:
         log(f"timing {name}")
         if name == "batched":
             extra[name] = measure_batched(device)
