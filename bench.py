@@ -114,12 +114,15 @@ def time_ticks(runtime, steps: int, warmup: int) -> tuple[float, MatrixRollout]:
 
 
 def mall_flushed_ms(rollout: MatrixRollout, ticks: int = 20) -> float:
-    """ms per tick when a 1 GiB write first evicts the graph from the 256 MB last-level cache."""
-    scratch = torch.empty(256 * 1024 * 1024, dtype=torch.float32, device="cuda")
+    """ms per tick when reading 1 GiB first evicts the graph from the 256 MB last-level
+    cache.  The eviction reads (a sum), so it leaves clean lines: no write-back of it
+    competes with the tick for HBM."""
+    scratch = torch.ones(256 * 1024 * 1024, dtype=torch.float32, device="cuda")
+    total_out = torch.empty((), dtype=torch.float32, device="cuda")
     launch, planes = rollout._launch, rollout._sets
     total = 0.0
     for i in range(ticks):
-        scratch.fill_(float(i))          # ~0.13 ms of writes keeps the queue ahead of the host
+        torch.sum(scratch, dim=0, out=total_out)   # ~0.15 ms of reads keeps the queue ahead of the host
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         launch(planes[0], planes[1])
