@@ -323,13 +323,34 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
     const_i32_ptr head = (const_i32_ptr)(A.groups + 4 * static_cast<int64_t>(wg[0]));
     const_i32_ptr last = (const_i32_ptr)(A.groups + 4 * static_cast<int64_t>(g_end - 1));
     const int e_begin = head[3], e_end = last[3] + (last[2] >> 8);
-    for (int e = e_begin + lane; e < e_end; e += 64) {
-      const int64_t row = row0 + static_cast<int64_t>(A.rows[e]);
+    if (A.n_panels == 1) {
+      for (int e = e_begin + lane; e < e_end; e += 64) {
+        const int64_t row = row0 + static_cast<int64_t>(A.rows[e]);
 #pragma unroll
-      for (int j = 0; j < BT; ++j) {
-        const float value = A.sorted[static_cast<int64_t>(e) * BT + j];
-        if (A.n_panels == 1) update(A, row, j, value);
-        else A.partials[(static_cast<int64_t>(panel) * A.N + row) * BT + j] = value;
+        for (int j = 0; j < BT; ++j) update(A, row, j, A.sorted[static_cast<int64_t>(e) * BT + j]);
+      }
+    } else {
+      // kMapUnroll entries per lane per round: every load of a round is issued
+      // before its first store (an entry past the end rereads the last one and
+      // is not stored), so a round waits on memory once.
+      constexpr int kMapUnroll = 4;
+      float* const out = A.partials + static_cast<int64_t>(panel) * A.N * BT;
+      for (int e0 = e_begin + lane; e0 < e_end; e0 += 64 * kMapUnroll) {
+        int64_t row[kMapUnroll];
+        float value[kMapUnroll][BT];
+#pragma unroll
+        for (int u = 0; u < kMapUnroll; ++u) {
+          const int e = min(e0 + 64 * u, e_end - 1);
+          row[u] = row0 + static_cast<int64_t>(A.rows[e]);
+#pragma unroll
+          for (int j = 0; j < BT; ++j) value[u][j] = A.sorted[static_cast<int64_t>(e) * BT + j];
+        }
+#pragma unroll
+        for (int u = 0; u < kMapUnroll; ++u)
+          if (e0 + 64 * u < e_end) {
+#pragma unroll
+            for (int j = 0; j < BT; ++j) out[row[u] * BT + j] = value[u][j];
+          }
       }
     }
   }
