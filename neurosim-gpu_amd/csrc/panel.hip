@@ -116,20 +116,23 @@ __device__ __forceinline__ const __attribute__((address_space(1))) T* scalar_bas
 }
 
 // One register block of D steps starting at slot block0 (a multiple of 64).
-// For float32 weights the loads take a scalar base per block and the lane
-// offset: with per-lane 64-bit addresses the compiler reuses a register of
-// the block in flight for the next block's address and so waits for that
-// block before issuing the next one.  The narrower encodings keep per-lane
-// addresses, which compile without that wait.
+// For float32 weights the loads take a scalar base per block and a 32-bit
+// lane offset: with per-lane 64-bit addresses the compiler reuses a register
+// of the block in flight for the next block's address and so waits for that
+// block before issuing the next one.  lane32 is the lane made opaque once per
+// kernel, so it stays in one register for the whole stream (neither a 64-bit
+// copy nor a register a load may target).  The narrower encodings keep
+// per-lane addresses: they compile without the wait, or (e4m3) measure no
+// faster without it.
 template <int FMT, int D>
 __device__ __forceinline__ void load_block(const PanelArgs& A, int64_t block0, int lane,
-                                           Slot (&dst)[D]) {
+                                           uint32_t lane32, Slot (&dst)[D]) {
   if constexpr (FMT == NS_WEIGHT_F32) {
     const auto col = scalar_base(A.col + block0);
     const auto weight = scalar_base(static_cast<const uint32_t*>(A.weight) + block0);
 #pragma unroll
     for (int k = 0; k < D; ++k) {
-      const uint32_t at = static_cast<uint32_t>(lane) + 64u * k;
+      const uint32_t at = lane32 + 64u * k;
       dst[k].c = col[at];
       dst[k].w = weight[at];
       dst[k].sc = 0u;
@@ -190,6 +193,9 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
+  uint32_t lane32 = static_cast<uint32_t>(lane);
+  asm volatile("" : "+v"(lane32));
+  __builtin_assume(lane32 < 64u);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const_i32_ptr tile = (const_i32_ptr)(A.tiles + 4 * static_cast<int64_t>(blockIdx.x));
   const int panel = tile[0], row0 = tile[1];
@@ -226,7 +232,7 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
 
   // First register block in flight while the panel is staged.
   Slot buf_a[D], buf_b[D];
-  load_block<FMT, D>(A, first, lane, buf_a);
+  load_block<FMT, D>(A, first, lane, lane32, buf_a);
   uint32_t bits = boundary_bits<D>(A, first / 64);
   Group now{0, 0, 0}, next{0, 0, 0};
   if (g < g_end) now = load_group(A, g);
@@ -256,7 +262,7 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
   // made of scalars and the lane id, so closing waits on no vector load).
   auto block = [&](Slot (&here)[D], Slot (&ahead)[D], int b) {
     const int64_t ahead0 = first + static_cast<int64_t>(b + 1) * D * 64;
-    load_block<FMT, D>(A, ahead0, lane, ahead);
+    load_block<FMT, D>(A, ahead0, lane, lane32, ahead);
     const int rem = total - b * D;
     uint32_t ends = rem < D ? bits & ((1u << rem) - 1u) : bits;
     bits = boundary_bits<D>(A, ahead0 / 64);
