@@ -410,8 +410,11 @@ def measure_scaleout(device, cpu_sample: bool) -> dict:
     topology_cpu = topology_to(topology, "cpu") if cpu_sample else None
     m = topology.n_edges
     model_cpu, model = standard_model(n, device)
+    start = time.perf_counter()
     runtime = NativeDendriticMatrixRuntime(topology, model, torch.zeros(batch, n, device=device),
                                            weight_format="fp8")
+    torch.cuda.synchronize()
+    layout_s = time.perf_counter() - start
     drive = column_drive(batch)
     ms = rollout_ms(runtime, 100, 2, drive.to(device), 0.1)
     alg = algorithmic_bytes("fp8", n, m, batch) + 4 * batch
@@ -421,7 +424,14 @@ def measure_scaleout(device, cpu_sample: bool) -> dict:
               "achieved_GBps": round(alg / ms / 1e6, 1),
               "pct_hbm_peak": round(100 * alg / ms / 1e6 / HBM_PEAK_GBPS, 1),
               "graph_build_s": round(build_s, 2),
-              "graph_build": "host draws (torch CPU generator), ns_build_topology on the GPU"}
+              "graph_build": "host draws (torch CPU generator), ns_build_topology on the GPU",
+              "layout_build_s": round(layout_s, 2)}
+    if runtime.kernel != "rows":
+        del runtime
+        rows = NativeDendriticMatrixRuntime(topology, model, torch.zeros(batch, n, device=device),
+                                            weight_format="fp8", kernel="rows")
+        result["rows_kernel_ms_per_tick"] = round(rollout_ms(rows, 100, 2, drive.to(device), 0.1), 5)
+        runtime = rows
     if cpu_sample:
         log("scale-out: timing the CPU oracle on 10 ticks")
         from neurosim_gpu.precision import quantize_dequantize
@@ -444,8 +454,9 @@ def main() -> None:
     cli.add_argument("--formats", default="fp32,fp16,fp8,nvfp4")
     cli.add_argument("--no-cpu-baseline", action="store_true")
     cli.add_argument("--no-mall-flush", action="store_true")
-    cli.add_argument("--kernel", default="auto", choices=("auto", "rows", "panels"),
-                     help="tick kernel: LDS column panels (batch 1-2) or CSR row blocks")
+    cli.add_argument("--kernel", default="auto", choices=("auto", "rows", "panels", "bands"),
+                     help="headline tick kernel: LDS column panels (batch 1-2), source bands "
+                          "(batch a multiple of 16) or CSR row blocks")
     cli.add_argument("--copy-calibration", action="store_true",
                      help="only run 256 MiB device copies (PMC byte-counter calibration)")
     cli.add_argument("--configs", default="encode,backward,batched,pels,scaleout",

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 5
+#define NS_ABI_VERSION 6
 
 /* Return codes. */
 #define NS_OK 0
@@ -127,6 +127,46 @@ typedef struct ns_panel_plan {
                                   per-panel row sums by row (several panels), added in
                                   panel order by a second kernel */
 } ns_panel_plan;
+
+/* Source-band layout of a CSR matrix for wide batches (batch a multiple of
+ * 16, neuron-major state), built by ns_plan_bands.  Sources are cut into
+ * `n_bands` bands of `band_width` neurons; a band of the state (band_width x
+ * 16 floats per column tile) is sized to stay resident in one XCD's L2 while
+ * every workgroup on that XCD gathers from it.  Destination rows are cut into
+ * `n_row_blocks` blocks of `block_rows` rows; one workgroup owns one block
+ * (and one 16-column tile), keeps the block's row sums in LDS, walks the
+ * bands in order and finally applies the update.  Each of its 4 wavefronts
+ * owns a fixed set of the block's rows (dealt by degree, longest first onto
+ * the least-loaded wavefront).  Per band, a wavefront's rows with edges in
+ * the band are sorted by segment length and cut into groups of 64 rows, one
+ * row per lane; a group's slots are step-major (slot (step k, lane l) is
+ * 64*first_step + 64*k + l) and lane l takes its row's segment in CSR order.
+ * A group is cut into register blocks of at most `block_steps` steps; the
+ * wavefront's blocks are consecutive in `blocks` and their slots contiguous.
+ * Padding slots have source index 0xFFFF and weight code 0.  Slot k is
+ * original CSR edge perm[k] (or padding).  The kernel reads one block record
+ * and one register block of slots ahead, so the tables end with a sentinel
+ * block record (whose group is a last group of 64 padding rows) and 8*64
+ * padding slots. */
+typedef struct ns_band_plan {
+  int32_t band_width;          /* source neurons per band, at most 65535 */
+  int32_t n_bands;
+  int32_t block_rows;          /* destination rows per workgroup */
+  int32_t n_row_blocks;
+  int32_t n_blocks;            /* register blocks over all wavefronts (sentinel excluded) */
+  int32_t n_groups;
+  int32_t block_steps;         /* steps per register block the plan was cut for */
+  int32_t reserved;
+  int64_t n_slots;
+  const int32_t* wave_blocks;  /* [n_row_blocks*4 + 1]: wavefront w of row block q owns
+                                  blocks wave_blocks[4q+w] .. wave_blocks[4q+w+1]-1 */
+  const int32_t* blocks;       /* [n_blocks+1][4]: first step, band, steps | last << 8
+                                  (last: the block ends its group), group */
+  const uint16_t* rows;        /* [n_groups][64]: block-local row of each lane, 0xFFFF none */
+  const uint16_t* col;         /* [n_slots] source index minus the band's first neuron */
+  const void* weight;          /* [n_slots] weights in slot order, encoding of the matrix */
+  const uint8_t* slot_scales;  /* NVFP4: e4m3 block-scale code of each slot's edge */
+} ns_band_plan;
 
 /* Arguments of one fused matrix tick. */
 typedef struct ns_step_args {
@@ -293,6 +333,32 @@ int ns_panel_geometry(int64_t batch, int32_t* max_panel_width, int32_t* waves);
  * (reference: csrc/bindings.cpp:3-7,137-142; csrc/compartmental.cu:176-236),
  * except that the caller supplies the output planes and the row plan. */
 int ns_dendritic_step(const ns_step_args* args, void* stream);
+
+/* Host-side band planner for a host copy of (rowptr, col): `band_width`
+ * sources per band (1..65535), `block_rows` destination rows per workgroup
+ * (1..ns_band_max_block_rows()), register blocks of at most `block_steps`
+ * steps (1..8).  Call once with all output pointers NULL to get the sizes in
+ * *plan (n_bands, n_row_blocks, n_blocks, n_groups, n_slots), then again with
+ * wave_blocks int32[4*n_row_blocks+1], blocks int32[4*(n_blocks+1)], rows
+ * uint16[64*n_groups], perm int32[n_slots] (-1 for padding), col
+ * uint16[n_slots].  Pointer fields of *plan are not touched.  blocks holds
+ * n_blocks records plus the sentinel, rows n_groups groups including the
+ * sentinel group, and the slots end with 8*64 padding slots. */
+int ns_plan_bands(const int32_t* rowptr_host, const int32_t* col_host, int64_t n_rows,
+                  int32_t band_width, int32_t block_rows, int32_t block_steps,
+                  ns_band_plan* plan, int32_t* wave_blocks, int32_t* blocks, uint16_t* rows,
+                  int32_t* perm, uint16_t* col);
+
+/* Largest block_rows the band kernel's LDS holds. */
+int32_t ns_band_max_block_rows(void);
+
+/* Fused matrix tick over a band layout (batch a multiple of 16, state
+ * neuron-major with 16-byte aligned rows).  Same semantics and arguments as
+ * ns_dendritic_step (it replaces the same reference entry,
+ * csrc/bindings.cpp:3-7,137-142; csrc/compartmental.cu:176-236); `args->plan`
+ * and `args->panels` are ignored, the CSR in `args->matrix` gives only the
+ * weight format and global scale, and the slots come from `plan`. */
+int ns_dendritic_step_bands(const ns_step_args* args, const ns_band_plan* plan, void* stream);
 
 /* PELS event tick: advance + emission threshold, then scatter of each
  * emitter's out-edges into `current` with float32 atomics.  Replaces

@@ -1,0 +1,314 @@
+// Fused dendritic matrix tick over source bands, for wide batches (16 state
+// columns per workgroup) whose state is larger than an XCD's L2.
+//
+// Semantics follow the reference's fused kernel (csrc/compartmental.cu:121-140
+// and :72-90): j = W @ s over the batch columns, then the three-state update.
+// The work decomposition is this library's own (ns_plan_bands):
+//
+//  * A gather of one source's 16 columns is a 64-byte row of the neuron-major
+//    state.  Random 64-byte gathers over a state far larger than L2 are served
+//    by the MALL; confined to a band of a few MB they hit the XCD's L2 and run
+//    about twice as fast.  So sources are cut into bands, and every
+//    workgroup walks the bands in the same order: the workgroups resident on
+//    one XCD gather from about one band at a time.
+//  * One 256-lane workgroup owns a block of destination rows and one 16-column
+//    tile.  Its row sums live in LDS for the whole tick, so no partial sums
+//    leave the compute unit.  Each wavefront owns a fixed set of the block's
+//    rows, so its LDS updates race with no other wavefront.
+//  * Per band a wavefront's rows are grouped 64 at a time, one row per lane,
+//    longest segment first; lane l walks its row's segment, gathering the
+//    whole 64-byte source row with four 16-byte loads per edge and keeping
+//    16 running sums in registers.  At the group's end the lane adds them to
+//    its row's LDS sums.
+//  * Register blocks of up to D steps are software-pipelined: the slots of
+//    block b+1 are loaded while block b's gathers are in flight.
+//  * After the last band the workgroup applies the update to its rows.
+//
+// Summation order: per row, bands in order; within a band, the row's edges in
+// CSR order, accumulated one at a time.  It depends only on the plan, so the
+// tick is bitwise repeatable and identical across weight encodings that decode
+// to the same float32 values.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "ns_common.h"
+#include "ns_host.h"
+
+namespace ns {
+
+struct BandArgs {
+  int64_t N, B;
+  Plane s, d, a, u, v;
+  Params p;
+  const float* s_rows;   // neuron-major state: source n's columns at s_rows + n * s_stride
+  int64_t s_stride;
+  int32_t band_width, block_rows;
+  const int32_t* wave_blocks;
+  const int32_t* blocks;
+  const uint16_t* rows;
+  const uint16_t* col;
+  const void* weight;
+  const uint8_t* slot_scales;
+  const float* gscale;
+  OutPlane os, od, oa;
+};
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kBandPad = 0xFFFFu;
+
+struct BandSlot {
+  uint32_t c, w, sc;
+};
+
+struct BandBlock {
+  int32_t step0, band, steps, last, group;
+};
+
+__device__ __forceinline__ BandBlock load_band_block(const BandArgs& A, int32_t b) {
+  const int32_t* q = A.blocks + 4 * static_cast<int64_t>(b);
+  const int32_t info = q[2];
+  return BandBlock{q[0], q[1], info & 0xFF, info >> 8, q[3]};
+}
+
+// This lane's D slots from the block's first step, and its row in the block's
+// group.  The loads do not depend on the block's step count (the slot array
+// has D padding steps past its end, the block table a sentinel record), so
+// the compiler can count them and wait for exactly the ones it needs.
+template <int FMT, int D>
+__device__ __forceinline__ void load_band_slots(const BandArgs& A, const BandBlock& blk, int lane,
+                                                BandSlot (&x)[D], uint32_t& row) {
+  const int64_t q0 = int64_t{64} * blk.step0 + lane;
+#pragma unroll
+  for (int k = 0; k < D; ++k) {
+    const int64_t q = q0 + 64 * k;
+    x[k].c = A.col[q];
+    x[k].sc = 0u;
+    if constexpr (FMT == NS_WEIGHT_F32) x[k].w = static_cast<const uint32_t*>(A.weight)[q];
+    else if constexpr (FMT == NS_WEIGHT_F16) x[k].w = static_cast<const uint16_t*>(A.weight)[q];
+    else if constexpr (FMT == NS_WEIGHT_E4M3) x[k].w = static_cast<const uint8_t*>(A.weight)[q];
+    else {
+      x[k].w = static_cast<const uint8_t*>(A.weight)[q >> 1];
+      x[k].sc = A.slot_scales[q];
+    }
+  }
+  row = A.rows[int64_t{64} * blk.group + lane];
+}
+
+// Source of padding slots and of steps past a block's end: 16 zeros.
+__device__ __attribute__((aligned(16))) float kBandZeroRow[16] = {};
+
+typedef const __attribute__((address_space(1))) v4f* global_v4f_ptr;
+
+// Slots start at multiples of 64, so an NVFP4 slot's nibble half is the lane's parity.
+template <int FMT>
+__device__ __forceinline__ float decode_band(const BandSlot& x, int lane, float gscale) {
+  if constexpr (FMT == NS_WEIGHT_F32) {
+    return __builtin_bit_cast(float, x.w);
+  } else if constexpr (FMT == NS_WEIGHT_F16) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x.w)));
+  } else if constexpr (FMT == NS_WEIGHT_E4M3) {
+    return e4m3_to_float(x.w) * gscale;
+  } else {
+    const ns_v2f pair = e2m1_pair(x.w & 0xFFu);
+    return ((lane & 1) ? pair.y : pair.x) * (e4m3_to_float(x.sc) * gscale);
+  }
+}
+
+template <int FMT, int D>
+__global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) {
+  extern __shared__ __attribute__((aligned(16))) float sums[];   // [block_rows][16]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * A.block_rows;
+  const int nrows = static_cast<int>(min<int64_t>(A.block_rows, A.N - r0));
+  const int64_t b0 = int64_t{16} * blockIdx.y;
+  const float gscale = (FMT == NS_WEIGHT_E4M3 || FMT == NS_WEIGHT_NVFP4) ? *A.gscale : 1.0f;
+  v4f* const sums4 = reinterpret_cast<v4f*>(sums);
+  for (int i = tid; i < nrows * 4; i += kBandWaves * 64) sums4[i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  __syncthreads();
+
+  const int32_t* wb = A.wave_blocks + static_cast<int64_t>(blockIdx.x) * kBandWaves + wave;
+  const int32_t b_begin = wb[0], b_end = wb[1];
+  const float* const srow = A.s_rows + b0;
+  const uint64_t zero_row = reinterpret_cast<uint64_t>(&kBandZeroRow[0]);
+  float acc[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+
+  BandBlock cur{0, 0, 0, 0, 0};
+  BandSlot here[D];
+  uint32_t row = kBandPad;
+  if (b_begin < b_end) {
+    cur = load_band_block(A, b_begin);
+    load_band_slots<FMT, D>(A, cur, lane, here, row);
+  }
+  for (int32_t b = b_begin; b < b_end; ++b) {
+    // Gathers of this block: the whole 16-column row of each slot's source.
+    const int64_t base = static_cast<int64_t>(cur.band) * A.band_width;
+    // A padding slot (or a step past the block's end) reads the zero row: the
+    // two global addresses are blended by a mask, so the choice stays a
+    // select and the loads stay global loads.
+    v4f g[D][4];
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+      const bool real = k < cur.steps && here[k].c != kBandPad;
+      const uint64_t mask = 0ull - static_cast<uint64_t>(real);
+      const uint64_t at = reinterpret_cast<uint64_t>(srow + (base + here[k].c) * A.s_stride);
+      const uint64_t src = (at & mask) | (zero_row & ~mask);
+      const global_v4f_ptr p = reinterpret_cast<global_v4f_ptr>(src);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) g[k][q] = p[q];
+    }
+    // The next block's slots load while the gathers are in flight (past the
+    // wavefront's last block this reads the next wavefront's first block or
+    // the sentinel; those values go unused).
+    const BandBlock nxt = load_band_block(A, b + 1);
+    BandSlot ahead[D];
+    uint32_t row_ahead;
+    load_band_slots<FMT, D>(A, nxt, lane, ahead, row_ahead);
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+      if (k < cur.steps) {
+        const float w = decode_band<FMT>(here[k], lane, gscale);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          acc[4 * q + 0] += w * g[k][q].x;
+          acc[4 * q + 1] += w * g[k][q].y;
+          acc[4 * q + 2] += w * g[k][q].z;
+          acc[4 * q + 3] += w * g[k][q].w;
+        }
+      }
+    }
+    if (cur.last) {
+      if (row != kBandPad) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          v4f t = sums4[row * 4 + q];
+          t.x += acc[4 * q + 0]; t.y += acc[4 * q + 1];
+          t.z += acc[4 * q + 2]; t.w += acc[4 * q + 3];
+          sums4[row * 4 + q] = t;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+    }
+    cur = nxt;
+    row = row_ahead;
+#pragma unroll
+    for (int k = 0; k < D; ++k) here[k] = ahead[k];
+  }
+  __syncthreads();
+
+  // The update: consecutive lanes take consecutive columns of a row.
+  for (int i = tid; i < nrows * 16; i += kBandWaves * 64) {
+    const int64_t n = r0 + (i >> 4);
+    const int64_t b = b0 + (i & 15);
+    const NextState x = advance_one(A.p, n, sums[i], A.s.get(b, n), A.d.get(b, n),
+                                    A.a.get(b, n), A.u.get(b, n), A.v.get(b, n));
+    A.os.put(b, n, x.soma);
+    A.od.put(b, n, x.dendrite);
+    A.oa.put(b, n, x.adaptation);
+  }
+}
+
+template <int D>
+hipError_t launch_bands(const BandArgs& A, int fmt, int n_row_blocks, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(n_row_blocks), static_cast<unsigned>(A.B / 16));
+  const dim3 block(kBandWaves * 64);
+  const size_t lds = static_cast<size_t>(A.block_rows) * 16 * sizeof(float);
+  switch (fmt) {
+    case NS_WEIGHT_F32: band_tick_kernel<NS_WEIGHT_F32, D><<<grid, block, lds, stream>>>(A); break;
+    case NS_WEIGHT_F16: band_tick_kernel<NS_WEIGHT_F16, D><<<grid, block, lds, stream>>>(A); break;
+    case NS_WEIGHT_E4M3: band_tick_kernel<NS_WEIGHT_E4M3, D><<<grid, block, lds, stream>>>(A); break;
+    default: band_tick_kernel<NS_WEIGHT_NVFP4, D><<<grid, block, lds, stream>>>(A); break;
+  }
+  return hipGetLastError();
+}
+
+template <int D>
+hipError_t allow_band_lds() {
+  const int bytes = kBandMaxBlockRows * 16 * static_cast<int>(sizeof(float));
+  const void* kernels[4] = {reinterpret_cast<const void*>(&band_tick_kernel<NS_WEIGHT_F32, D>),
+                            reinterpret_cast<const void*>(&band_tick_kernel<NS_WEIGHT_F16, D>),
+                            reinterpret_cast<const void*>(&band_tick_kernel<NS_WEIGHT_E4M3, D>),
+                            reinterpret_cast<const void*>(&band_tick_kernel<NS_WEIGHT_NVFP4, D>)};
+  for (const void* k : kernels) {
+    const hipError_t err =
+        hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (err != hipSuccess) return err;
+  }
+  return hipSuccess;
+}
+
+int check_step_head(const ns_step_args& a);
+int check_step_planes(const ns_step_args& a);
+
+int band_step(const ns_step_args& a, const ns_band_plan& pl, hipStream_t stream) {
+  if (a.batch % 16) return fail("the band kernel needs a batch that is a multiple of 16, not %lld",
+                                (long long)a.batch);
+  if (a.state.stride_b != 1 || a.state.stride_n < a.batch || a.state.stride_n % 4 ||
+      reinterpret_cast<uintptr_t>(a.state.data) % 16)
+    return fail("the band kernel needs a neuron-major state with 16-byte aligned rows");
+  if (pl.band_width < 1 || pl.band_width > 65535) return fail("band width must be in [1, 65535]");
+  if (pl.n_bands != (a.n_neurons + pl.band_width - 1) / pl.band_width)
+    return fail("%d bands of width %d do not cover N=%lld", pl.n_bands, pl.band_width,
+                (long long)a.n_neurons);
+  if (pl.block_rows < 1 || pl.block_rows > kBandMaxBlockRows)
+    return fail("block_rows must be in [1, %d]", kBandMaxBlockRows);
+  if (pl.n_row_blocks != (a.n_neurons + pl.block_rows - 1) / pl.block_rows)
+    return fail("%d row blocks of %d rows do not cover N=%lld", pl.n_row_blocks, pl.block_rows,
+                (long long)a.n_neurons);
+  if (pl.block_steps != 4 && pl.block_steps != 8)
+    return fail("band plans are cut into register blocks of 4 or 8 steps, not %d", pl.block_steps);
+  if (pl.n_blocks < 0 || pl.n_groups < 1 || pl.n_slots < int64_t{kBandMaxBlockSteps} * 64)
+    return fail("band plan lacks its sentinel group or tail padding");
+  if (!pl.wave_blocks || !pl.blocks || !pl.rows || !pl.col || !pl.weight)
+    return fail("band plan tables are required");
+  if (a.matrix.format == NS_WEIGHT_NVFP4 && !pl.slot_scales)
+    return fail("NVFP4 bands require per-slot block scales");
+  const uintptr_t need = a.matrix.format == NS_WEIGHT_F32 ? 4 : a.matrix.format == NS_WEIGHT_F16 ? 2 : 1;
+  if (reinterpret_cast<uintptr_t>(pl.col) % 2 || reinterpret_cast<uintptr_t>(pl.weight) % need)
+    return fail("band arrays are misaligned");
+  if (static_cast<int64_t>(pl.n_row_blocks) > 0x7FFFFFFF || a.batch / 16 > 65535)
+    return fail("band grid too large");
+
+  BandArgs A{};
+  A.N = a.n_neurons; A.B = a.batch;
+  A.s = plane(a.state, a.state.data); A.d = plane(a.dendrite, a.state.data);
+  A.a = plane(a.adaptation, a.state.data);
+  A.u = plane(a.drive, a.state.data); A.v = plane(a.dendritic_drive, a.state.data);
+  for (int i = 0; i < 6; ++i) A.p.v[i] = Vec{a.params[i].data, a.params[i].stride};
+  A.s_rows = a.state.data; A.s_stride = a.state.stride_n;
+  A.band_width = pl.band_width; A.block_rows = pl.block_rows;
+  A.wave_blocks = pl.wave_blocks; A.blocks = pl.blocks; A.rows = pl.rows; A.col = pl.col;
+  A.weight = pl.weight; A.slot_scales = pl.slot_scales; A.gscale = a.matrix.global_scale;
+  A.os = out_plane(a.out_state); A.od = out_plane(a.out_dendrite);
+  A.oa = out_plane(a.out_adaptation);
+  static const hipError_t lds_ok = [] {
+    const hipError_t e4 = allow_band_lds<4>();
+    return e4 != hipSuccess ? e4 : allow_band_lds<8>();
+  }();
+  if (lds_ok != hipSuccess) return fail_launch("band tick (LDS limit)", lds_ok);
+  const hipError_t err = pl.block_steps == 4
+                             ? launch_bands<4>(A, a.matrix.format, pl.n_row_blocks, stream)
+                             : launch_bands<8>(A, a.matrix.format, pl.n_row_blocks, stream);
+  if (err != hipSuccess) return fail_launch("band tick", err);
+  return NS_OK;
+}
+
+}  // namespace ns
+
+using namespace ns;
+
+extern "C" int ns_dendritic_step_bands(const ns_step_args* args, const ns_band_plan* plan,
+                                       void* stream) {
+  clear_error();
+  if (!args || !plan) return fail("arguments and a band plan are required");
+  if (int rc = check_step_head(*args)) return rc;
+  if (args->batch == 0) return NS_OK;  // empty planes may carry null pointers
+  if (int rc = check_step_planes(*args)) return rc;
+  return band_step(*args, *plan, static_cast<hipStream_t>(stream));
+}

@@ -24,6 +24,9 @@ constexpr int kPanelWaves = 16;
 constexpr int kPanelThreads = kPanelWaves * 64;
 constexpr int kPanelMaxPrefetch = 16;                  // steps per register block, at most
 constexpr int kPanelTailSlots = 2 * kPanelMaxPrefetch * 64;
+constexpr int kBandWaves = 4;                           // wavefronts per band workgroup
+constexpr int kBandMaxBlockRows = 2496;                 // 16 float row sums each in LDS (156 KB)
+constexpr int kBandMaxBlockSteps = 8;                   // steps per register block, at most
 
 // A [B, N] operand that is either a strided tensor or one scalar.  `data` is
 // never null: a scalar plane points at some valid float with zero strides, so

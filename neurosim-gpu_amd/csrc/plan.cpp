@@ -278,3 +278,169 @@ extern "C" int ns_plan_panels(const int32_t* rowptr, const int32_t* col, int64_t
   if (col_out) std::copy(layout.col.begin(), layout.col.end(), col_out);
   return NS_OK;
 }
+
+namespace {
+
+// The band layout of one graph, in host vectors (built twice: size query, then fill).
+struct BandLayout {
+  int64_t n_groups = 0, n_slots = 0;
+  std::vector<int32_t> wave_blocks, blocks, perm;
+  std::vector<uint16_t> rows, col;
+};
+
+
+// Lays out row block [r0, r1): rows dealt to the wavefronts by degree, then
+// per wavefront and band the rows with edges in the band, longest segment
+// first (ties by row), in groups of 64 rows cut into register blocks.
+void append_band_block(BandLayout& out, const int32_t* rowptr, const int32_t* col,
+                       int64_t r0, int64_t r1, int32_t band_width, int32_t n_bands,
+                       int32_t block_steps, bool fill) {
+  const int64_t nr = r1 - r0;
+  std::vector<int32_t> by_degree(nr);
+  for (int64_t i = 0; i < nr; ++i) by_degree[i] = static_cast<int32_t>(i);
+  auto degree = [&](int64_t i) -> int64_t { return rowptr[r0 + i + 1] - rowptr[r0 + i]; };
+  std::stable_sort(by_degree.begin(), by_degree.end(),
+                   [&](int32_t x, int32_t y) { return degree(x) > degree(y); });
+  std::vector<int64_t> load(kBandWaves, 0);
+  std::vector<std::vector<int32_t>> mine(kBandWaves);
+  for (int32_t i : by_degree) {
+    const int32_t w = static_cast<int32_t>(std::min_element(load.begin(), load.end()) - load.begin());
+    load[w] += degree(i) + 1;
+    mine[w].push_back(i);
+  }
+  for (int32_t w = 0; w < kBandWaves; ++w) {
+    out.wave_blocks.push_back(static_cast<int32_t>(out.blocks.size() / 4));
+    std::vector<int32_t>& rows_w = mine[w];
+    std::sort(rows_w.begin(), rows_w.end());
+    const int64_t nw = static_cast<int64_t>(rows_w.size());
+    // Each row's edges grouped by band (stable counting sort): start[i][k].
+    std::vector<int32_t> start(nw * (n_bands + 1), 0);
+    int64_t total = 0;
+    for (int64_t i = 0; i < nw; ++i) {
+      const int64_t r = r0 + rows_w[i];
+      int32_t* st = &start[i * (n_bands + 1)];
+      for (int64_t e = rowptr[r]; e < rowptr[r + 1]; ++e) ++st[col[e] / band_width + 1];
+      for (int32_t k = 0; k < n_bands; ++k) st[k + 1] += st[k];
+      total += rowptr[r + 1] - rowptr[r];
+    }
+    std::vector<int32_t> order;   // per row, its edges in band order (CSR order within a band)
+    std::vector<int64_t> row_base(nw + 1, 0);
+    for (int64_t i = 0; i < nw; ++i) row_base[i + 1] = row_base[i] + (rowptr[r0 + rows_w[i] + 1] - rowptr[r0 + rows_w[i]]);
+    if (fill) {
+      order.assign(total, 0);
+      std::vector<int32_t> at(n_bands);
+      for (int64_t i = 0; i < nw; ++i) {
+        const int64_t r = r0 + rows_w[i];
+        const int32_t* st = &start[i * (n_bands + 1)];
+        for (int32_t k = 0; k < n_bands; ++k) at[k] = st[k];
+        for (int64_t e = rowptr[r]; e < rowptr[r + 1]; ++e)
+          order[row_base[i] + at[col[e] / band_width]++] = static_cast<int32_t>(e);
+      }
+    }
+    std::vector<int32_t> cand;
+    for (int32_t k = 0; k < n_bands; ++k) {
+      auto seg_len = [&](int32_t i) -> int32_t {
+        const int32_t* st = &start[static_cast<int64_t>(i) * (n_bands + 1)];
+        return st[k + 1] - st[k];
+      };
+      cand.clear();
+      for (int64_t i = 0; i < nw; ++i)
+        if (seg_len(static_cast<int32_t>(i)) > 0) cand.push_back(static_cast<int32_t>(i));
+      std::stable_sort(cand.begin(), cand.end(),
+                       [&](int32_t x, int32_t y) { return seg_len(x) > seg_len(y); });
+      for (size_t g0 = 0; g0 < cand.size(); g0 += 64) {
+        const size_t gn = std::min<size_t>(64, cand.size() - g0);
+        const int32_t steps = seg_len(cand[g0]);
+        const int32_t group = static_cast<int32_t>(out.n_groups++);
+        if (fill)
+          for (size_t l = 0; l < 64; ++l)
+            out.rows.push_back(l < gn ? static_cast<uint16_t>(rows_w[cand[g0 + l]]) : uint16_t{0xFFFF});
+        for (int32_t t0 = 0; t0 < steps; t0 += block_steps) {
+          const int32_t nst = std::min(block_steps, steps - t0);
+          const int32_t last = t0 + block_steps >= steps ? 1 : 0;
+          const int32_t rec[4] = {static_cast<int32_t>(out.n_slots / 64), k, nst | (last << 8), group};
+          out.blocks.insert(out.blocks.end(), rec, rec + 4);
+          out.n_slots += int64_t{64} * nst;
+          if (!fill) continue;
+          for (int32_t t = t0; t < t0 + nst; ++t)
+            for (size_t l = 0; l < 64; ++l) {
+              int32_t edge = -1;
+              if (l < gn) {
+                const int32_t i = cand[g0 + l];
+                if (t < seg_len(i)) edge = order[row_base[i] + start[static_cast<int64_t>(i) * (n_bands + 1) + k] + t];
+              }
+              out.perm.push_back(edge);
+              out.col.push_back(edge < 0 ? uint16_t{0xFFFF}
+                                         : static_cast<uint16_t>(col[edge] - int64_t{k} * band_width));
+            }
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" int32_t ns_band_max_block_rows(void) { return kBandMaxBlockRows; }
+
+extern "C" int ns_plan_bands(const int32_t* rowptr, const int32_t* col, int64_t n_rows,
+                             int32_t band_width, int32_t block_rows, int32_t block_steps,
+                             ns_band_plan* plan, int32_t* wave_blocks, int32_t* blocks,
+                             uint16_t* rows, int32_t* perm, uint16_t* col_out) {
+  clear_error();
+  if (!rowptr || !plan) return fail("rowptr and plan are required");
+  if (n_rows <= 0 || n_rows >= (int64_t{1} << 31)) return fail("N must be in [1, 2^31)");
+  if (rowptr[0] != 0) return fail("rowptr[0] must be 0");
+  for (int64_t r = 0; r < n_rows; ++r)
+    if (rowptr[r + 1] < rowptr[r]) return fail("rowptr must be non-decreasing");
+  if (rowptr[n_rows] > 0 && !col) return fail("col is required");
+  if (band_width < 1 || band_width > 65535) return fail("band_width must be in [1, 65535]");
+  if (block_rows < 1 || block_rows > kBandMaxBlockRows)
+    return fail("block_rows must be in [1, %d]", kBandMaxBlockRows);
+  if (block_steps < 1 || block_steps > kBandMaxBlockSteps)
+    return fail("block_steps must be in [1, %d]", kBandMaxBlockSteps);
+  for (int64_t e = 0; e < rowptr[n_rows]; ++e)
+    if (col[e] < 0 || col[e] >= n_rows) return fail("CSR column %lld out of range", (long long)col[e]);
+  const int64_t n_bands = (n_rows + band_width - 1) / band_width;
+  const int64_t n_row_blocks = (n_rows + block_rows - 1) / block_rows;
+  const bool fill = wave_blocks || blocks || rows || perm || col_out;
+  if (fill && !(wave_blocks && blocks && rows && perm && col_out))
+    return fail("all output arrays are required together");
+  BandLayout layout;
+  for (int64_t q = 0; q < n_row_blocks; ++q) {
+    const int64_t r0 = q * block_rows, r1 = std::min<int64_t>(n_rows, r0 + block_rows);
+    append_band_block(layout, rowptr, col, r0, r1, band_width, static_cast<int32_t>(n_bands),
+                      block_steps, fill);
+    if (layout.n_slots >= (int64_t{1} << 37) || layout.blocks.size() / 4 >= (size_t{1} << 31))
+      return fail("band layout needs too many slots");
+  }
+  layout.wave_blocks.push_back(static_cast<int32_t>(layout.blocks.size() / 4));
+  const int32_t n_blocks = static_cast<int32_t>(layout.blocks.size() / 4);
+  // Sentinel group (no rows) and block record, then the tail padding: the
+  // kernel loads one block ahead and a whole register block of slots.
+  const int32_t sentinel[4] = {0, 0, 0, static_cast<int32_t>(layout.n_groups++)};
+  layout.blocks.insert(layout.blocks.end(), sentinel, sentinel + 4);
+  layout.n_slots += int64_t{kBandMaxBlockSteps} * 64;
+  if (fill) {
+    layout.rows.insert(layout.rows.end(), 64, uint16_t{0xFFFF});
+    layout.perm.insert(layout.perm.end(), kBandMaxBlockSteps * 64, -1);
+    layout.col.insert(layout.col.end(), kBandMaxBlockSteps * 64, uint16_t{0xFFFF});
+  }
+  plan->band_width = band_width;
+  plan->n_bands = static_cast<int32_t>(n_bands);
+  plan->block_rows = block_rows;
+  plan->n_row_blocks = static_cast<int32_t>(n_row_blocks);
+  plan->n_blocks = n_blocks;
+  plan->n_groups = static_cast<int32_t>(layout.n_groups);
+  plan->block_steps = block_steps;
+  plan->reserved = 0;
+  plan->n_slots = layout.n_slots;
+  if (fill) {
+    std::copy(layout.wave_blocks.begin(), layout.wave_blocks.end(), wave_blocks);
+    std::copy(layout.blocks.begin(), layout.blocks.end(), blocks);
+    std::copy(layout.rows.begin(), layout.rows.end(), rows);
+    std::copy(layout.perm.begin(), layout.perm.end(), perm);
+    std::copy(layout.col.begin(), layout.col.end(), col_out);
+  }
+  return NS_OK;
+}

@@ -401,21 +401,21 @@ using namespace ns;
 
 extern "C" int32_t ns_block_edges(int64_t batch) { return capacity_for(batch); }
 
-extern "C" int ns_dendritic_step(const ns_step_args* args, void* stream) {
-  clear_error();
-  if (!args) return fail("arguments are required");
-  const ns_step_args& a = *args;
+namespace ns {
+
+// Checks shared by every matrix-tick entry: sizes, parameters and the CSR's
+// weight encoding (check_step_head), then the planes, which must be present
+// and must not overlap where outputs are concerned (check_step_planes).
+int check_step_head(const ns_step_args& a) {
   if (a.n_neurons <= 0) return fail("state must be [B,N], N > 0");
   if (a.batch < 0) return fail("batch must be non-negative");
   if (a.n_neurons >= (int64_t{1} << 31)) return fail("N must be below 2^31");
   for (int i = 0; i < 6; ++i)
     if (!a.params[i].data) return fail("six neuron parameter vectors are required");
-  if (a.panels) {
-    if (int rc = check_csr(a.matrix, a.n_neurons)) return rc;
-  } else if (int rc = check_matrix(a.matrix, a.n_neurons, a.plan, a.batch)) {
-    return rc;
-  }
-  if (a.batch == 0) return NS_OK;  // empty planes may carry null pointers
+  return check_csr(a.matrix, a.n_neurons);
+}
+
+int check_step_planes(const ns_step_args& a) {
   if (!a.state.data || !a.dendrite.data || !a.adaptation.data)
     return fail("state, dendrite and adaptation data are required");
   if (!a.out_state.data || !a.out_dendrite.data || !a.out_adaptation.data)
@@ -434,6 +434,20 @@ extern "C" int ns_dendritic_step(const ns_step_args* args, void* stream) {
     for (int p = o + 1; p < 3; ++p)
       if (overlaps(outs[o], outs[p])) return fail("output planes must not overlap each other");
   }
+  return NS_OK;
+}
+
+}  // namespace ns
+
+extern "C" int ns_dendritic_step(const ns_step_args* args, void* stream) {
+  clear_error();
+  if (!args) return fail("arguments are required");
+  const ns_step_args& a = *args;
+  if (int rc = check_step_head(a)) return rc;
+  if (!a.panels)
+    if (int rc = check_matrix(a.matrix, a.n_neurons, a.plan, a.batch)) return rc;
+  if (a.batch == 0) return NS_OK;  // empty planes may carry null pointers
+  if (int rc = check_step_planes(a)) return rc;
   if (a.panels) return panel_step(a, static_cast<hipStream_t>(stream));
 
   TickArgs A{};

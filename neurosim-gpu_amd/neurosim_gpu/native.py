@@ -35,7 +35,7 @@ import numpy as np
 import torch
 
 _LIB_NAME = "libneurosim_hip.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 WEIGHT_F32, WEIGHT_F16, WEIGHT_E4M3, WEIGHT_NVFP4 = 0, 1, 2, 3
 _PLAN_CACHE = 64   # row plans kept per extension (one per live topology and batch width)
@@ -75,6 +75,15 @@ class _PanelPlan(ctypes.Structure):
                 ("n_step_words", _c_i64), ("tiles", _c_ptr), ("wave_groups", _c_ptr),
                 ("groups", _c_ptr), ("rows", _c_ptr), ("last_steps", _c_ptr), ("col", _c_ptr),
                 ("weight", _c_ptr), ("slot_scales", _c_ptr), ("partials", _c_ptr)]
+
+
+class _BandPlan(ctypes.Structure):
+    _fields_ = [("band_width", ctypes.c_int32), ("n_bands", ctypes.c_int32),
+                ("block_rows", ctypes.c_int32), ("n_row_blocks", ctypes.c_int32),
+                ("n_blocks", ctypes.c_int32), ("n_groups", ctypes.c_int32),
+                ("block_steps", ctypes.c_int32), ("reserved", ctypes.c_int32), ("n_slots", _c_i64),
+                ("wave_blocks", _c_ptr), ("blocks", _c_ptr), ("rows", _c_ptr), ("col", _c_ptr),
+                ("weight", _c_ptr), ("slot_scales", _c_ptr)]
 
 
 class _StepArgs(ctypes.Structure):
@@ -163,6 +172,14 @@ def load_library() -> ctypes.CDLL:
     lib.ns_plan_panels.argtypes = [_c_ptr, _c_ptr, _c_i64, ctypes.c_int32, ctypes.c_int32,
                                    ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(_PanelPlan),
                                    ctypes.POINTER(_c_i64)] + [_c_ptr] * 7
+    lib.ns_plan_bands.restype = ctypes.c_int
+    lib.ns_plan_bands.argtypes = [_c_ptr, _c_ptr, _c_i64, ctypes.c_int32, ctypes.c_int32,
+                                  ctypes.c_int32, ctypes.POINTER(_BandPlan)] + [_c_ptr] * 5
+    lib.ns_band_max_block_rows.restype = ctypes.c_int32
+    lib.ns_band_max_block_rows.argtypes = []
+    lib.ns_dendritic_step_bands.restype = ctypes.c_int
+    lib.ns_dendritic_step_bands.argtypes = [ctypes.POINTER(_StepArgs), ctypes.POINTER(_BandPlan),
+                                            _c_ptr]
     lib.ns_encode_workspace_bytes.restype = _c_i64
     lib.ns_encode_workspace_bytes.argtypes = []
     lib.ns_step_backward_workspace_floats.restype = _c_i64
@@ -383,13 +400,82 @@ def plan_panels_host(rowptr: torch.Tensor, col: torch.Tensor, batch: int, tiles_
     return plan, tiles, wave_groups, groups, rows, last_steps, perm, cols
 
 
+def plan_bands_host(rowptr: torch.Tensor, col: torch.Tensor, band_width: int, block_rows: int,
+                    block_steps: int = 8):
+    """Host band layout of a CSR (numpy arrays): see ns_plan_bands."""
+    lib = load_library()
+    rowptr = np.ascontiguousarray(rowptr.detach().to("cpu", torch.int32).numpy())
+    col = np.ascontiguousarray(col.detach().to("cpu", torch.int32).numpy())
+    n = rowptr.size - 1
+    plan = _BandPlan()
+    args = (rowptr.ctypes.data, col.ctypes.data if col.size else None, n, int(band_width),
+            int(block_rows), int(block_steps), ctypes.byref(plan))
+    _raise_on(lib.ns_plan_bands(*args, *([None] * 5)), lib)
+    wave_blocks = np.empty(4 * plan.n_row_blocks + 1, np.int32)
+    blocks = np.empty(4 * (plan.n_blocks + 1), np.int32)
+    rows = np.empty(64 * plan.n_groups, np.uint16)
+    perm = np.empty(plan.n_slots, np.int32)
+    cols = np.empty(plan.n_slots, np.uint16)
+    _raise_on(lib.ns_plan_bands(*args, wave_blocks.ctypes.data, blocks.ctypes.data,
+                                rows.ctypes.data, perm.ctypes.data, cols.ctypes.data), lib)
+    return plan, wave_blocks, blocks, rows, perm, cols
+
+
+def band_max_block_rows() -> int:
+    return int(load_library().ns_band_max_block_rows())
+
+
 def _device_tensor(array: np.ndarray, device) -> torch.Tensor:
     if array.dtype == np.uint16:
         array = array.view(np.int16)
     return torch.from_numpy(np.ascontiguousarray(array)).to(device)
 
 
-class PanelLayout:
+class _SlotLayout:
+    """Weights of a CSR payload rearranged into a layout's slot order.
+
+    Subclasses set ``n_slots``, ``perm`` (int64 edge of each slot, 0 for
+    padding) and ``valid`` (slot holds an edge); padding slots get code 0.
+    """
+
+    n_slots: int
+    perm: torch.Tensor
+    valid: torch.Tensor
+    _slot_weights: tuple | None = None
+    _slot_key = None
+
+    def slot_weights(self, key, weight: torch.Tensor, block_scales: torch.Tensor | None):
+        """Weights of the CSR payload (original edge order) rearranged into slot order."""
+        if self._slot_key == key and self._slot_weights is not None:
+            return self._slot_weights
+        with torch.no_grad():
+            if weight.numel() == 0:           # no edges: every slot is padding (code 0)
+                nibbles = block_scales is not None
+                slots = torch.zeros(self.n_slots // 2 if nibbles else self.n_slots,
+                                    dtype=weight.dtype, device=weight.device)
+                scales = (torch.zeros(self.n_slots, dtype=torch.uint8, device=weight.device)
+                          if nibbles else None)
+            elif weight.dtype in (torch.float32, torch.float16):
+                slots = torch.where(self.valid, weight[self.perm], torch.zeros((), dtype=weight.dtype,
+                                                                               device=weight.device))
+                scales = None
+            elif block_scales is None:        # fp8 e4m3 codes
+                slots = torch.where(self.valid, weight[self.perm], torch.zeros((), dtype=torch.uint8,
+                                                                               device=weight.device))
+                scales = None
+            else:                             # nvfp4: one nibble and one block-scale code per slot
+                edge = self.perm
+                nibble = (weight[edge >> 1] >> ((edge & 1) * 4).to(torch.uint8)) & 15
+                nibble = torch.where(self.valid, nibble, torch.zeros_like(nibble))
+                slots = (nibble[0::2] | (nibble[1::2] << 4)).contiguous()
+                scales = torch.where(self.valid, block_scales[edge >> 4],
+                                     torch.zeros((), dtype=torch.uint8, device=weight.device))
+            self._slot_weights = (slots.contiguous(), None if scales is None else scales.contiguous())
+            self._slot_key = key
+        return self._slot_weights
+
+
+class PanelLayout(_SlotLayout):
     """Column-panel layout of one graph for batch width 1 or 2 (see ns_plan_panels).
 
     Built once per graph structure on the host from copies of in_rowptr and
@@ -431,36 +517,6 @@ class PanelLayout:
         self._slot_weights: tuple | None = None
         self._slot_key = None
 
-    def slot_weights(self, key, weight: torch.Tensor, block_scales: torch.Tensor | None):
-        """Weights of the CSR payload (original edge order) rearranged into slot order."""
-        if self._slot_key == key and self._slot_weights is not None:
-            return self._slot_weights
-        with torch.no_grad():
-            if weight.numel() == 0:           # no edges: every slot is padding (code 0)
-                nibbles = block_scales is not None
-                slots = torch.zeros(self.n_slots // 2 if nibbles else self.n_slots,
-                                    dtype=weight.dtype, device=weight.device)
-                scales = (torch.zeros(self.n_slots, dtype=torch.uint8, device=weight.device)
-                          if nibbles else None)
-            elif weight.dtype in (torch.float32, torch.float16):
-                slots = torch.where(self.valid, weight[self.perm], torch.zeros((), dtype=weight.dtype,
-                                                                               device=weight.device))
-                scales = None
-            elif block_scales is None:        # fp8 e4m3 codes
-                slots = torch.where(self.valid, weight[self.perm], torch.zeros((), dtype=torch.uint8,
-                                                                               device=weight.device))
-                scales = None
-            else:                             # nvfp4: one nibble and one block-scale code per slot
-                edge = self.perm
-                nibble = (weight[edge >> 1] >> ((edge & 1) * 4).to(torch.uint8)) & 15
-                nibble = torch.where(self.valid, nibble, torch.zeros_like(nibble))
-                slots = (nibble[0::2] | (nibble[1::2] << 4)).contiguous()
-                scales = torch.where(self.valid, block_scales[edge >> 4],
-                                     torch.zeros((), dtype=torch.uint8, device=weight.device))
-            self._slot_weights = (slots.contiguous(), None if scales is None else scales.contiguous())
-            self._slot_key = key
-        return self._slot_weights
-
     def plan_struct(self, slot_weight: torch.Tensor, slot_scales: torch.Tensor | None) -> _PanelPlan:
         plan = _PanelPlan()
         ctypes.memmove(ctypes.addressof(plan), ctypes.addressof(self._plan), ctypes.sizeof(plan))
@@ -471,6 +527,54 @@ class PanelLayout:
         plan.weight = slot_weight.data_ptr()
         plan.slot_scales = slot_scales.data_ptr() if slot_scales is not None else None
         plan.partials = self.partials.data_ptr()
+        return plan
+
+
+# Sources per band: 32768 neurons x 16 columns x 4 bytes = 2 MB of state, which
+# stays resident in one XCD's 4 MB L2 beside the streamed slots.
+BAND_WIDTH = 32768
+
+
+class BandLayout(_SlotLayout):
+    """Source-band layout of one graph for batches that are multiples of 16 (see ns_plan_bands).
+
+    Built once per graph structure on the host from copies of in_rowptr and
+    in_col (a synchronisation; set-up only).  Holds the device tables, the
+    slot permutation and, per weight version and encoding, the weights
+    rearranged into slot order on the device.  ``block_rows`` defaults to
+    enough rows for two workgroups per compute unit over the whole graph.
+    """
+
+    def __init__(self, topology, device, *, band_width: int = BAND_WIDTH,
+                 block_rows: int | None = None, block_steps: int = 8) -> None:
+        n = topology.n_neurons
+        if block_rows is None:
+            units = torch.cuda.get_device_properties(device).multi_processor_count
+            block_rows = min(band_max_block_rows(), max(64, -(-n // (2 * units))))
+        plan, wave_blocks, blocks, rows, perm, cols = plan_bands_host(
+            topology.in_rowptr, topology.in_col, band_width, block_rows, block_steps)
+        self.n = n
+        self.band_width, self.n_bands = plan.band_width, plan.n_bands
+        self.block_rows, self.n_row_blocks = plan.block_rows, plan.n_row_blocks
+        self.n_blocks, self.n_groups, self.n_slots = plan.n_blocks, plan.n_groups, plan.n_slots
+        self.wave_blocks = _device_tensor(wave_blocks, device)
+        self.blocks = _device_tensor(blocks, device)
+        self.rows = _device_tensor(rows, device)
+        self.col = _device_tensor(cols, device)
+        perm_t = torch.from_numpy(perm).to(device)
+        self.valid = perm_t >= 0
+        self.perm = perm_t.clamp_min(0).to(torch.int64)
+        self._plan = plan
+        self._slot_weights = None
+        self._slot_key = None
+
+    def plan_struct(self, slot_weight: torch.Tensor, slot_scales: torch.Tensor | None) -> _BandPlan:
+        plan = _BandPlan()
+        ctypes.memmove(ctypes.addressof(plan), ctypes.addressof(self._plan), ctypes.sizeof(plan))
+        plan.wave_blocks, plan.blocks = self.wave_blocks.data_ptr(), self.blocks.data_ptr()
+        plan.rows, plan.col = self.rows.data_ptr(), self.col.data_ptr()
+        plan.weight = slot_weight.data_ptr()
+        plan.slot_scales = slot_scales.data_ptr() if slot_scales is not None else None
         return plan
 
 
@@ -550,7 +654,7 @@ class NativeExtension:
     # -- ops ----------------------------------------------------------------
     def dendritic_step(self, state, dendrite, adaptation, params, rowptr, source, weight,
                        input, input_scalar, dendritic_input, dendritic_scalar, width,
-                       block_scales=None, global_scale=None, panels=None):
+                       block_scales=None, global_scale=None, panels=None, bands=None):
         _check_state(state)
         args = _StepArgs()
         args.state = _plane(state, state, "state")
@@ -565,7 +669,15 @@ class NativeExtension:
         batch, n = state.shape
         args.n_neurons, args.batch = n, batch
         panel_struct = None
-        if panels is not None:
+        if bands is not None:              # a _BandPlan built by BandLayout.plan_struct
+            if panels is not None:
+                raise RuntimeError("pass a panel or a band layout, not both")
+            if not (state.stride(0) == 1 and state.stride(1) >= batch and state.stride(1) % 4 == 0
+                    and state.data_ptr() % 16 == 0):
+                # The band kernel gathers whole neuron rows of s: a neuron-major copy.
+                state = new_planes(1, batch, n, state)[0].copy_(state)
+                args.state = _plane(state, state, "state")
+        elif panels is not None:
             panel_struct = panels          # a _PanelPlan built by PanelLayout.plan_struct
             args.panels = ctypes.addressof(panel_struct)
         else:
@@ -573,7 +685,11 @@ class NativeExtension:
         outs = new_planes(3, batch, n, state)
         args.out_state, args.out_dendrite, args.out_adaptation = (_out(o) for o in outs)
         stream = torch.cuda.current_stream(state.device).cuda_stream
-        _raise_on(self.lib.ns_dendritic_step(ctypes.byref(args), stream), self.lib)
+        if bands is not None:
+            _raise_on(self.lib.ns_dendritic_step_bands(ctypes.byref(args), ctypes.byref(bands),
+                                                       stream), self.lib)
+        else:
+            _raise_on(self.lib.ns_dendritic_step(ctypes.byref(args), stream), self.lib)
         return outs
 
     def dendritic_event(self, state, dendrite, adaptation, params, current, emitted, theta,
@@ -702,7 +818,7 @@ class TickLauncher:
 
     def __init__(self, extension: "NativeExtension", state_like: torch.Tensor, params, rowptr,
                  col, weight, drive, dendritic_drive, block_scales=None, global_scale=None,
-                 panels=None):
+                 panels=None, bands=None):
         _check_state(state_like)
         self.lib = extension.lib
         args = _StepArgs()
@@ -720,15 +836,20 @@ class TickLauncher:
         batch, n = state_like.shape
         args.n_neurons, args.batch = n, batch
         bounds = None
-        if panels is not None:
+        if bands is not None and panels is not None:
+            raise RuntimeError("pass a panel or a band layout, not both")
+        if bands is not None:
+            pass                            # the band plan goes with each launch
+        elif panels is not None:
             args.panels = ctypes.addressof(panels)
         else:
             bounds, blocks, capacity = extension.plan_tensors(rowptr, batch)
             args.plan = _RowPlan(bounds.data_ptr(), blocks, capacity, 0)
         self.args = args
+        self.bands = bands
         self.batch, self.n = batch, n
         self._keep = (list(params), rowptr, col, weight, drive_t, ddrive_t, block_scales,
-                      global_scale, bounds, panels)
+                      global_scale, bounds, panels, bands)
 
     def __call__(self, source: tuple, target: tuple, stream: int | None = None) -> None:
         """One tick from planes (s, d, a) into planes (s', d', a') (all [B,N] views)."""
@@ -740,7 +861,11 @@ class TickLauncher:
         args.out_state, args.out_dendrite, args.out_adaptation = (_out(t) for t in target)
         if stream is None:
             stream = torch.cuda.current_stream(source[0].device).cuda_stream
-        _raise_on(self.lib.ns_dendritic_step(ctypes.byref(args), stream), self.lib)
+        if self.bands is not None:
+            _raise_on(self.lib.ns_dendritic_step_bands(ctypes.byref(args), ctypes.byref(self.bands),
+                                                       stream), self.lib)
+        else:
+            _raise_on(self.lib.ns_dendritic_step(ctypes.byref(args), stream), self.lib)
 
 
 @lru_cache(maxsize=1)

@@ -24,7 +24,7 @@ from __future__ import annotations
 import torch
 
 from .compartmental import DendriticDynamics, DendriticMatrixRuntime, DendriticPELSRuntime
-from .native import NativeExtension, PanelLayout, encode_weights, load_native_extension
+from .native import BAND_WIDTH, BandLayout, NativeExtension, PanelLayout, encode_weights, load_native_extension
 from .topology import SparseTopology
 
 
@@ -113,6 +113,12 @@ class _NativeTick(torch.autograd.Function):
                 d_adaptation if needs[3] else None, d_weight, d_drive, d_dendritic, *d_params)
 
 
+# Fewest source bands (of BAND_WIDTH neurons) for which "auto" picks the band
+# kernel: below that the whole 16-column state is a few L2s and the row kernel
+# gathers it from cache as well.
+BAND_AUTO_MIN_BANDS = 4
+
+
 class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
     """One HIP launch per tick for CSR propagation plus all three neuron states.
 
@@ -125,20 +131,28 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
 
     ``kernel`` picks the tick kernel: "panels" stages column panels of the
     state in LDS and streams a panel-sorted copy of the graph (batch 1 or 2;
-    built once, at construction), "rows" streams the CSR as is and gathers
-    the state from cache, "auto" uses panels whenever the batch allows.
-    ``panel_width`` caps the neurons per panel (default: what LDS holds) and
-    ``panel_tiles`` sets the workgroups per panel (default: compute units /
-    panels).
+    built once, at construction), "bands" streams a band-sorted copy of the
+    graph whose gathers stay within an L2-sized band of sources at a time
+    (batch a multiple of 16; built once), "rows" streams the CSR as is and
+    gathers the state from cache.  "auto" uses panels whenever the batch
+    allows, bands when the batch is a multiple of 16 and the graph spans at
+    least ``BAND_AUTO_MIN_BANDS`` bands, rows otherwise.  ``panel_width`` caps
+    the neurons per panel (default: what LDS holds) and ``panel_tiles`` sets
+    the workgroups per panel (default: compute units / panels).
+    ``band_width`` sets the sources per band (default ``BAND_WIDTH``),
+    ``band_rows`` the destination rows per band workgroup (default: two
+    workgroups per compute unit) and ``band_steps`` the register block (4 or 8).
     """
 
     def __init__(self, topology: SparseTopology, dynamics: DendriticDynamics,
                  initial_state: torch.Tensor, *, threads_per_row: int | None = None,
                  extension=None, weight_dtype: torch.dtype = torch.float32,
                  weight_format: str | None = None, kernel: str = "auto",
-                 panel_width: int | None = None, panel_tiles: int | None = None) -> None:
-        if kernel not in ("auto", "rows", "panels"):
-            raise ValueError("kernel must be 'auto', 'rows' or 'panels'")
+                 panel_width: int | None = None, panel_tiles: int | None = None,
+                 band_width: int | None = None, band_rows: int | None = None,
+                 band_steps: int = 8) -> None:
+        if kernel not in ("auto", "rows", "panels", "bands"):
+            raise ValueError("kernel must be 'auto', 'rows', 'panels' or 'bands'")
         if threads_per_row not in (None, 8, 16, 32):
             raise ValueError("threads_per_row must be 8, 16, 32 or None")
         _require_gpu_float32(initial_state)
@@ -159,17 +173,37 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         native = isinstance(self.extension, NativeExtension)
         if kernel == "panels" and (batch not in (1, 2) or not native):
             raise ValueError("the panel kernel needs batch 1 or 2 and the native extension")
+        if kernel == "bands" and (batch % 16 or batch == 0 or not native):
+            raise ValueError("the band kernel needs a batch that is a multiple of 16 and the "
+                             "native extension")
         use_panels = kernel == "panels" or (kernel == "auto" and batch in (1, 2) and native)
-        self.kernel = "panels" if use_panels else "rows"
+        use_bands = kernel == "bands" or (
+            kernel == "auto" and native and batch > 0 and batch % 16 == 0
+            and topology.n_neurons >= BAND_AUTO_MIN_BANDS * BAND_WIDTH)
+        self.kernel = "panels" if use_panels else "bands" if use_bands else "rows"
         self._panels = (PanelLayout(topology, batch, initial_state.device,
                                     tiles_per_panel=panel_tiles, max_panel_width=panel_width)
                         if use_panels else None)
+        self._bands = (BandLayout(topology, initial_state.device,
+                                  band_width=band_width or BAND_WIDTH, block_rows=band_rows,
+                                  block_steps=band_steps)
+                       if use_bands else None)
 
     def _invalidate_precision_cache(self) -> None:
         self._packed_weight = None
         self._packed_weight_version = -1
         self._panel_struct = None
         self._panel_struct_key = None
+
+    def _band_plan(self, weight: torch.Tensor, scales: tuple):
+        """ctypes band plan for this tick's weights (rebuilt when the weights change)."""
+        key = (self.topology.weight_version, self.checkpoint_precision, weight.data_ptr())
+        if self._panel_struct_key != key:
+            block = scales[0] if len(scales) == 2 else None
+            slots, slot_scales = self._bands.slot_weights(key, weight, block)
+            self._panel_struct = self._bands.plan_struct(slots, slot_scales)
+            self._panel_struct_key = key
+        return self._panel_struct
 
     def _panel_plan(self, weight: torch.Tensor, scales: tuple):
         """ctypes panel plan for this tick's weights (rebuilt when the weights change)."""
@@ -236,6 +270,8 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         extra = {}
         if self._panels is not None:
             extra["panels"] = self._panel_plan(weight, scales)
+        elif self._bands is not None:
+            extra["bands"] = self._band_plan(weight, scales)
         self.state, self.dendritic_state, self.adaptation_state = self.extension.dendritic_step(
             self.state, self.dendritic_state, self.adaptation_state, self._parameters(),
             self.topology.in_rowptr, self.topology.in_col, weight,

@@ -38,9 +38,10 @@ class MatrixRollout:
         weight, scales, self.backend = runtime._weights()
         topology = runtime.topology
         panels = runtime._panel_plan(weight, scales) if runtime._panels is not None else None
+        bands = runtime._band_plan(weight, scales) if runtime._bands is not None else None
         self._launch = TickLauncher(extension, runtime.state, runtime._parameters(),
                                     topology.in_rowptr, topology.in_col, weight, drive,
-                                    dendritic_drive, *scales, panels=panels)
+                                    dendritic_drive, *scales, panels=panels, bands=bands)
         self._sets = (tuple(new_planes(3, batch, n, runtime.state)),
                       tuple(new_planes(3, batch, n, runtime.state)))
         self.reset_from_runtime()

@@ -34,7 +34,8 @@ def test_every_declared_symbol_is_exported(lib):
                           "ns_csr_spmm", "ns_plan_panels", "ns_panel_geometry",
                           "ns_encode_workspace_bytes", "ns_encode_weights",
                           "ns_topology_workspace_bytes", "ns_build_topology",
-                          "ns_step_backward_workspace_floats", "ns_dendritic_step_backward"}
+                          "ns_step_backward_workspace_floats", "ns_dendritic_step_backward",
+                          "ns_plan_bands", "ns_band_max_block_rows", "ns_dendritic_step_bands"}
     for name in names:
         assert hasattr(lib, name), name
     assert lib.ns_abi_version() == native.ABI_VERSION
@@ -140,6 +141,48 @@ def test_step_validation_messages(lib):
     args, keep = fake_step_args()
     args.matrix.n_rows = 7
     assert "row count" in call(lib, args)[1]
+
+
+def fake_band_plan(n, width=4, rows=4):
+    tables = [np.zeros(4 * (-(-n // rows)) + 1, np.int32), np.zeros(4, np.int32),
+              np.full(64, 0xFFFF, np.uint16), np.full(8 * 64, 0xFFFF, np.uint16),
+              np.zeros(8 * 64, np.float32)]
+    plan = native._BandPlan()
+    plan.band_width, plan.n_bands = width, -(-n // width)
+    plan.block_rows, plan.n_row_blocks = rows, -(-n // rows)
+    plan.n_blocks, plan.n_groups, plan.block_steps, plan.n_slots = 0, 1, 8, 8 * 64
+    plan.wave_blocks, plan.blocks, plan.rows, plan.col, plan.weight = (t.ctypes.data for t in tables)
+    return plan, tables
+
+
+def test_band_step_validation_messages(lib):
+    """Rejections of ns_dendritic_step_bands, all before anything is launched."""
+    def band_call(args, plan):
+        rc = lib.ns_dendritic_step_bands(ctypes.byref(args), ctypes.byref(plan), None)
+        return rc, lib.ns_last_error().decode()
+
+    args, keep = fake_step_args(n=8, batch=2)
+    plan, tables = fake_band_plan(8)
+    assert "multiple of 16" in band_call(args, plan)[1]
+    args, keep = fake_step_args(n=8, batch=16)
+    assert "neuron-major" in band_call(args, plan)[1]
+    # neuron-major [16,8] planes from here on
+    args.state = native._Plane(args.state.data, 1, 16, 0.0)
+    for bad, message in (({"band_width": 0}, "band width"), ({"n_bands": 3}, "do not cover"),
+                         ({"block_rows": 0}, "block_rows"), ({"n_row_blocks": 1}, "do not cover"),
+                         ({"block_steps": 5}, "register blocks"), ({"n_groups": 0}, "sentinel"),
+                         ({"n_slots": 64}, "tail padding"), ({"rows": None}, "tables")):
+        plan, tables = fake_band_plan(8)
+        for field, value in bad.items():
+            setattr(plan, field, value)
+        rc, text = band_call(args, plan)
+        assert rc != 0 and message in text, (bad, text)
+    plan, tables = fake_band_plan(8)
+    args.matrix.format = native.WEIGHT_E4M3
+    assert "global scale" in band_call(args, plan)[1]
+    args, keep = fake_step_args(n=8, batch=0)
+    assert band_call(args, plan) == (0, "")
+    assert lib.ns_band_max_block_rows() == 2496
 
 
 def test_empty_batch_is_a_no_op(lib):

@@ -1,0 +1,195 @@
+"""The source-band layout (ns_plan_bands) on the host: invariants, and a numpy
+emulation of the band kernel's decomposition against the plain CSR product.
+
+The invariants: every edge lands in exactly one slot, with its band-local
+source index; a wavefront's register blocks walk the bands in order, their
+slots contiguous; a group's lane keeps one row, takes the row's segment of the
+band in CSR order, and the group's last block is marked; each row of a block
+belongs to one wavefront and meets each band at most once; the tables end with
+the sentinel block, the sentinel group and the tail padding.  The emulation
+follows the kernel's summation order (per row: bands in order, within a band
+the segment's edges one at a time) and must reproduce the CSR product.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from neurosim_gpu import native
+from neurosim_gpu.native import band_max_block_rows, plan_bands_host
+
+PAD = 0xFFFF
+TAIL = 8 * 64
+
+
+def random_csr(n, m, seed, hubs=()):
+    rng = np.random.default_rng(seed)
+    dst = [rng.integers(0, n, m)]
+    src = [rng.integers(0, n, m)]
+    for row, length in hubs:
+        dst.append(np.full(length, row))
+        src.append(rng.integers(0, n, length))
+    dst, src = np.concatenate(dst), np.concatenate(src)
+    order = np.argsort(dst, kind="stable")
+    dst, src = dst[order], src[order]
+    rowptr = np.zeros(n + 1, np.int64)
+    rowptr[1:] = np.cumsum(np.bincount(dst, minlength=n))
+    return rowptr.astype(np.int32), src.astype(np.int32)
+
+
+def layout(rowptr, col, width, rows, steps):
+    plan, wave_blocks, blocks, group_rows, perm, cols = plan_bands_host(
+        torch.from_numpy(rowptr), torch.from_numpy(col), width, rows, steps)
+    return plan, wave_blocks, blocks.reshape(-1, 4), group_rows.reshape(-1, 64), perm, cols
+
+
+CASES = [
+    (500, 6000, 3, (), 64, 100, 8),
+    (3000, 40000, 4, ((7, 900), (2999, 2500)), 333, 257, 4),
+    (2000, 30000, 5, ((0, 4000),), 2000, 2000, 8),      # one band, one block
+    (1000, 0, 6, (), 100, 64, 8),                       # no edges
+    (4000, 20000, 7, (), 50, 1, 8),                     # one row per block
+]
+
+
+@pytest.mark.parametrize("n,m,seed,hubs,width,rows,steps", CASES)
+def test_band_layout_invariants(n, m, seed, hubs, width, rows, steps):
+    rowptr, col = random_csr(n, m, seed, hubs)
+    edges = int(rowptr[-1])
+    plan, wave_blocks, blocks, group_rows, perm, cols = layout(rowptr, col, width, rows, steps)
+    n_bands = -(-n // width)
+    n_row_blocks = -(-n // rows)
+    assert (plan.n_bands, plan.n_row_blocks, plan.block_rows, plan.band_width) == (
+        n_bands, n_row_blocks, rows, width)
+    assert wave_blocks.size == 4 * n_row_blocks + 1 and wave_blocks[0] == 0
+    assert wave_blocks[-1] == plan.n_blocks and np.all(np.diff(wave_blocks) >= 0)
+    assert blocks.shape == (plan.n_blocks + 1, 4) and group_rows.shape == (plan.n_groups, 64)
+    assert perm.size == cols.size == plan.n_slots
+
+    # every edge in exactly one slot, with its band-local source index
+    real = perm >= 0
+    assert np.array_equal(np.sort(perm[real]), np.arange(edges))
+    assert np.all(cols[~real] == PAD)
+
+    # sentinel block, sentinel group, tail padding
+    assert tuple(blocks[-1]) == (0, 0, 0, plan.n_groups - 1)
+    assert np.all(group_rows[-1] == PAD)
+    assert np.all(perm[-TAIL:] == -1)
+
+    row_of_edge = np.repeat(np.arange(n), np.diff(rowptr))
+    segments = {}
+    for e in range(edges):
+        segments.setdefault((int(row_of_edge[e]), int(col[e]) // width), []).append(e)
+    step = 0
+    owner = {}
+    for q in range(n_row_blocks):
+        r0 = q * rows
+        for w in range(4):
+            seen_bands = {}
+            prev_band = -1
+            b = wave_blocks[4 * q + w]
+            while b < wave_blocks[4 * q + w + 1]:
+                # one group: consecutive blocks of one group and band, the last marked
+                group, band = blocks[b, 3], blocks[b, 1]
+                assert band >= prev_band
+                prev_band = band
+                lanes = group_rows[group]
+                members = [int(r) for r in lanes if r != PAD]
+                assert len(set(members)) == len(members)
+                for r in members:
+                    assert 0 <= r < min(rows, n - r0)
+                    assert owner.setdefault(r0 + r, (q, w)) == (q, w)       # one wavefront per row
+                    assert (r0 + r, band) not in seen_bands                 # one group per band
+                    seen_bands[(r0 + r, band)] = True
+                t = 0
+                while True:
+                    start, bband, info, bgroup = blocks[b]
+                    assert (bband, bgroup) == (band, group) and start == step
+                    count, last = info & 0xFF, info >> 8
+                    assert 1 <= count <= steps
+                    for k in range(count):
+                        slots = np.arange(64) + 64 * (start + k)
+                        for lane in range(64):
+                            e = perm[slots[lane]]
+                            if lanes[lane] == PAD:
+                                assert e == -1
+                                continue
+                            row = r0 + int(lanes[lane])
+                            seg = segments.get((row, int(band)), [])
+                            if t + k < len(seg):
+                                assert e == seg[t + k]
+                                assert cols[slots[lane]] == col[e] - band * width
+                                assert row_of_edge[e] == row
+                            else:
+                                assert e == -1
+                    step += count
+                    t += count
+                    b += 1
+                    if last:
+                        break
+                # the group's longest segment fills its blocks exactly
+                lengths = [len(segments.get((r0 + r, int(band)), [])) for r in members]
+                assert min(lengths) > 0 and t == max(lengths)
+    assert 64 * step + TAIL == plan.n_slots
+
+
+@pytest.mark.parametrize("n,m,seed,hubs,width,rows,steps", CASES)
+def test_band_emulation_matches_csr_product(n, m, seed, hubs, width, rows, steps):
+    rowptr, col = random_csr(n, m, seed, hubs)
+    rng = np.random.default_rng(seed + 100)
+    weight = (rng.standard_normal(col.size) * 0.05).astype(np.float32)
+    s = rng.random((n, 16), dtype=np.float32)
+    plan, wave_blocks, blocks, group_rows, perm, cols = layout(rowptr, col, width, rows, steps)
+    padded = np.concatenate([weight, np.zeros(1, np.float32)])     # index -1: padding weight 0
+    slot_w = padded[perm]
+    sums = np.zeros((n, 16), np.float32)
+    for q in range(plan.n_row_blocks):
+        r0 = q * rows
+        for w in range(4):
+            acc = np.zeros((64, 16), np.float32)
+            for b in range(wave_blocks[4 * q + w], wave_blocks[4 * q + w + 1]):
+                start, band, info, group = blocks[b]
+                for k in range(info & 0xFF):
+                    slots = np.arange(64) + 64 * (start + k)
+                    c = cols[slots].astype(np.int64)
+                    real = c != PAD
+                    g = np.zeros((64, 16), np.float32)
+                    g[real] = s[band * width + c[real]]
+                    acc += slot_w[slots][:, None] * g
+                if info >> 8:
+                    lanes = group_rows[group]
+                    for lane in np.nonzero(lanes != PAD)[0]:
+                        sums[r0 + lanes[lane]] += acc[lane]
+                    acc[:] = 0
+    expected = np.zeros((n, 16), np.float64)
+    np.add.at(expected, np.repeat(np.arange(n), np.diff(rowptr)),
+              weight.astype(np.float64)[:, None] * s.astype(np.float64)[col])
+    assert np.allclose(sums, expected, rtol=1e-5, atol=1e-5)
+
+
+def test_band_planner_rejects_bad_arguments():
+    lib = native.load_library()
+    rowptr, col = random_csr(100, 500, 1)
+    plan = native._BandPlan()
+
+    def rc(rp=rowptr, c=col, n=100, width=10, rows=16, steps=8):
+        code = lib.ns_plan_bands(rp.ctypes.data, c.ctypes.data, n, width, rows, steps,
+                                 ctypes.byref(plan), None, None, None, None, None)
+        return code, lib.ns_last_error().decode()
+
+    assert rc()[0] == 0
+    assert "band_width" in rc(width=0)[1] and "band_width" in rc(width=65536)[1]
+    assert "block_rows" in rc(rows=0)[1]
+    assert "block_rows" in rc(rows=band_max_block_rows() + 1)[1]
+    assert "block_steps" in rc(steps=0)[1] and "block_steps" in rc(steps=9)[1]
+    bad = rowptr.copy()
+    bad[5] = bad[6] + 1
+    assert "non-decreasing" in rc(rp=bad)[1]
+    bad_col = col.copy()
+    bad_col[3] = 100
+    assert "out of range" in rc(c=bad_col)[1]
+    assert "N must be" in rc(n=0)[1]
