@@ -261,8 +261,9 @@ int band_step(const ns_step_args& a, const ns_band_plan& pl, hipStream_t stream)
   if (pl.n_row_blocks != (a.n_neurons + pl.block_rows - 1) / pl.block_rows)
     return fail("%d row blocks of %d rows do not cover N=%lld", pl.n_row_blocks, pl.block_rows,
                 (long long)a.n_neurons);
-  if (pl.block_steps != 4 && pl.block_steps != 8)
-    return fail("band plans are cut into register blocks of 4 or 8 steps, not %d", pl.block_steps);
+  if (pl.block_steps != 2 && pl.block_steps != 4 && pl.block_steps != 8)
+    return fail("band plans are cut into register blocks of 2, 4 or 8 steps, not %d",
+                pl.block_steps);
   if (pl.n_blocks < 0 || pl.n_groups < 1 || pl.n_slots < int64_t{kBandMaxBlockSteps} * 64)
     return fail("band plan lacks its sentinel group or tail padding");
   if (!pl.wave_blocks || !pl.blocks || !pl.rows || !pl.col || !pl.weight)
@@ -288,13 +289,15 @@ int band_step(const ns_step_args& a, const ns_band_plan& pl, hipStream_t stream)
   A.os = out_plane(a.out_state); A.od = out_plane(a.out_dendrite);
   A.oa = out_plane(a.out_adaptation);
   static const hipError_t lds_ok = [] {
-    const hipError_t e4 = allow_band_lds<4>();
-    return e4 != hipSuccess ? e4 : allow_band_lds<8>();
+    hipError_t e = allow_band_lds<2>();
+    if (e == hipSuccess) e = allow_band_lds<4>();
+    return e != hipSuccess ? e : allow_band_lds<8>();
   }();
   if (lds_ok != hipSuccess) return fail_launch("band tick (LDS limit)", lds_ok);
-  const hipError_t err = pl.block_steps == 4
-                             ? launch_bands<4>(A, a.matrix.format, pl.n_row_blocks, stream)
-                             : launch_bands<8>(A, a.matrix.format, pl.n_row_blocks, stream);
+  const hipError_t err =
+      pl.block_steps == 2   ? launch_bands<2>(A, a.matrix.format, pl.n_row_blocks, stream)
+      : pl.block_steps == 4 ? launch_bands<4>(A, a.matrix.format, pl.n_row_blocks, stream)
+                            : launch_bands<8>(A, a.matrix.format, pl.n_row_blocks, stream);
   if (err != hipSuccess) return fail_launch("band tick", err);
   return NS_OK;
 }

@@ -401,7 +401,7 @@ def plan_panels_host(rowptr: torch.Tensor, col: torch.Tensor, batch: int, tiles_
 
 
 def plan_bands_host(rowptr: torch.Tensor, col: torch.Tensor, band_width: int, block_rows: int,
-                    block_steps: int = 8):
+                    block_steps: int = 4):
     """Host band layout of a CSR (numpy arrays): see ns_plan_bands."""
     lib = load_library()
     rowptr = np.ascontiguousarray(rowptr.detach().to("cpu", torch.int32).numpy())
@@ -533,6 +533,18 @@ class PanelLayout(_SlotLayout):
 # Sources per band: 32768 neurons x 16 columns x 4 bytes = 2 MB of state, which
 # stays resident in one XCD's 4 MB L2 beside the streamed slots.
 BAND_WIDTH = 32768
+# Rows per band workgroup such that two workgroups fit one compute unit's LDS.
+BAND_ROWS_TWO_PER_UNIT = 1248
+
+
+def default_band_rows(n: int, units: int) -> int:
+    """Destination rows per band workgroup: two workgroups per compute unit, in
+    whole rounds (the grid is a multiple of 2 * units), as few rounds as fit LDS.
+    Workgroups of one round start together and so walk the bands together."""
+    rounds = 1
+    while -(-n // (2 * units * rounds)) > BAND_ROWS_TWO_PER_UNIT:
+        rounds += 1
+    return max(1, -(-n // (2 * units * rounds)))
 
 
 class BandLayout(_SlotLayout):
@@ -542,15 +554,15 @@ class BandLayout(_SlotLayout):
     in_col (a synchronisation; set-up only).  Holds the device tables, the
     slot permutation and, per weight version and encoding, the weights
     rearranged into slot order on the device.  ``block_rows`` defaults to
-    enough rows for two workgroups per compute unit over the whole graph.
+    ``default_band_rows``.
     """
 
     def __init__(self, topology, device, *, band_width: int = BAND_WIDTH,
-                 block_rows: int | None = None, block_steps: int = 8) -> None:
+                 block_rows: int | None = None, block_steps: int = 4) -> None:
         n = topology.n_neurons
         if block_rows is None:
             units = torch.cuda.get_device_properties(device).multi_processor_count
-            block_rows = min(band_max_block_rows(), max(64, -(-n // (2 * units))))
+            block_rows = default_band_rows(n, units)
         plan, wave_blocks, blocks, rows, perm, cols = plan_bands_host(
             topology.in_rowptr, topology.in_col, band_width, block_rows, block_steps)
         self.n = n

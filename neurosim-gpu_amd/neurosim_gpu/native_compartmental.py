@@ -141,7 +141,8 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
     the workgroups per panel (default: compute units / panels).
     ``band_width`` sets the sources per band (default ``BAND_WIDTH``),
     ``band_rows`` the destination rows per band workgroup (default: two
-    workgroups per compute unit) and ``band_steps`` the register block (4 or 8).
+    workgroups per compute unit, ``default_band_rows``) and ``band_steps`` the
+    register block (2, 4 or 8 steps).
     """
 
     def __init__(self, topology: SparseTopology, dynamics: DendriticDynamics,
@@ -150,7 +151,7 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
                  weight_format: str | None = None, kernel: str = "auto",
                  panel_width: int | None = None, panel_tiles: int | None = None,
                  band_width: int | None = None, band_rows: int | None = None,
-                 band_steps: int = 8) -> None:
+                 band_steps: int = 4) -> None:
         if kernel not in ("auto", "rows", "panels", "bands"):
             raise ValueError("kernel must be 'auto', 'rows', 'panels' or 'bands'")
         if threads_per_row not in (None, 8, 16, 32):
