@@ -198,22 +198,22 @@ __global__ __launch_bounds__(kThreads) void tick_kernel(TickArgs A) {
   const int b0 = blockIdx.y * BT;
   const float gscale = (FMT == NS_WEIGHT_E4M3 || FMT == NS_WEIGHT_NVFP4) ? *A.gscale : 1.0f;
 
+  // The plan's boundary pairs carry each block's first row and first edge, so
+  // the edge range needs no rowptr load (clamped into the edge arrays).
   const int32_t* bnd = A.bounds + 2 * blk;
   const int r0 = min(max(bnd[0], 0), static_cast<int>(A.N));
   const int r1 = min(max(bnd[2], r0), static_cast<int>(A.N));
   const int nrows = r1 - r0;
   if (nrows == 0) return;
-  const int e0 = A.rowptr[r0];
-  const int e1 = A.rowptr[r1];
+  const int e0 = static_cast<int>(min<int64_t>(max(bnd[1], 0), A.M));
+  const int e1 = static_cast<int>(min<int64_t>(max(bnd[3], e0), A.M));
   const int base = e0 & ~3;
   if (nrows > kMaxRows || e1 - base > kCap) {
     rows_one_by_one<BT, FMT>(A, r0, r1, b0, gscale, prod);
     return;
   }
 
-  for (int i = tid; i <= nrows; i += kThreads) srow[i] = A.rowptr[r0 + i];
-
-  // Phase 1: stream the block's edges, decode, gather, multiply, stage in LDS.
+  // Phase 1 loads first: the block's col/weight quads.
   int cq[kPasses][4];
   float wq[kPasses][4];
 #pragma unroll
@@ -224,6 +224,39 @@ __global__ __launch_bounds__(kThreads) void tick_kernel(TickArgs A) {
       load_quad<FMT>(A, q, vec, cq[p], wq[p], gscale);
     }
   }
+
+  // Phase 2's geometry depends only on the row count, so each lane's update
+  // operands (its row's parameters and its columns' five planes) load now,
+  // alongside the quads, and the update at the end waits on nothing.
+  int group = kThreads / nrows;                  // lanes per row, power of two, <= 64
+  group = 1 << (31 - __builtin_clz(group));
+  group = group > 64 ? 64 : group;
+  const int cols_at_once = group < BT ? group : BT;
+  const int slices = group / cols_at_once;
+  const int col_rounds = BT / cols_at_once;
+  const int i = tid / group;
+  const int lane = tid & (group - 1);
+  const int cpos = lane & (cols_at_once - 1);
+  const int h = lane / cols_at_once;
+  const bool row_ok = i < nrows;
+  const bool updates = row_ok && h == 0 && !A.spmm_only;
+  const int64_t n = r0 + i;
+  NeuronParams prm{};
+  float us[BT], ud[BT], ua[BT], uu[BT], uv[BT];
+  if (updates) {
+    prm = load_params(A.p, n);
+#pragma unroll
+    for (int round = 0; round < BT; ++round) {
+      const int64_t b = b0 + cpos + round * cols_at_once;
+      if (round < col_rounds && b < A.B) {
+        us[round] = A.s.get(b, n); ud[round] = A.d.get(b, n); ua[round] = A.a.get(b, n);
+        uu[round] = A.u.get(b, n); uv[round] = A.v.get(b, n);
+      }
+    }
+  }
+  for (int r = tid; r <= nrows; r += kThreads) srow[r] = A.rowptr[r0 + r];
+
+  // Phase 1: decode, gather, multiply, stage in LDS.
 #pragma unroll
   for (int p = 0; p < kPasses; ++p) {
     const int q = base + (p * kThreads + tid) * 4;
@@ -264,31 +297,43 @@ __global__ __launch_bounds__(kThreads) void tick_kernel(TickArgs A) {
   __syncthreads();
 
   // Phase 2: per-row reduction from LDS, then the update.
-  int group = kThreads / nrows;                  // lanes per row, power of two, <= 64
-  group = 1 << (31 - __builtin_clz(group));
-  group = group > 64 ? 64 : group;
-  const int cols_at_once = group < BT ? group : BT;
-  const int slices = group / cols_at_once;
-  const int col_rounds = BT / cols_at_once;
-  const int i = tid / group;
-  const int lane = tid & (group - 1);
-  const int cpos = lane & (cols_at_once - 1);
-  const int h = lane / cols_at_once;
-  const bool row_ok = i < nrows;
   int rs = 0, re = 0;
   if (row_ok) {
     rs = max(srow[i], e0);
     re = min(srow[i + 1], e1);
   }
-  for (int round = 0; round < col_rounds; ++round) {
+#pragma unroll
+  for (int round = 0; round < BT; ++round) {
+    if (round >= col_rounds) continue;   // (not break: the loop must fully unroll)
     const int j = cpos + round * cols_at_once;
     float acc = 0.0f;
     if (row_ok) {
+      // Four running sums over interleaved products, so the LDS reads of a
+      // row overlap instead of waiting on one add chain.
       const float* row = prod + j * kStride - base;
-      for (int e = rs + h; e < re; e += slices) acc += row[e];
+      float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+      int e = rs + h;
+      for (; e + 3 * slices < re; e += 4 * slices) {
+        a0 += row[e];
+        a1 += row[e + slices];
+        a2 += row[e + 2 * slices];
+        a3 += row[e + 3 * slices];
+      }
+      for (; e < re; e += slices) a0 += row[e];
+      acc = (a0 + a1) + (a2 + a3);
     }
     for (int off = cols_at_once; off < group; off <<= 1) acc += __shfl_xor(acc, off, 64);
-    if (row_ok && h == 0 && b0 + j < A.B) finish(A, r0 + i, b0 + j, acc);
+    if (row_ok && h == 0 && b0 + j < A.B) {
+      if (A.spmm_only) {
+        A.os.put(b0 + j, n, acc);
+      } else {
+        const NextState x = advance_loaded(prm, acc, us[round], ud[round], ua[round], uu[round],
+                                           uv[round]);
+        A.os.put(b0 + j, n, x.soma);
+        A.od.put(b0 + j, n, x.dendrite);
+        A.oa.put(b0 + j, n, x.adaptation);
+      }
+    }
   }
 }
 
