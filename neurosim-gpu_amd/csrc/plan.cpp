@@ -68,6 +68,9 @@ extern "C" int ns_plan_row_blocks(const int32_t* rowptr, int64_t n_rows, int32_t
 
 namespace {
 
+// XCDs of the target (gfx950): the panel planner orders tiles for them.
+constexpr int64_t kXcds = 8;
+
 // The sliced layout of one graph, in host vectors (built twice: size query, then fill).
 struct PanelLayout {
   int32_t panel_width = 0, n_panels = 0;
@@ -200,6 +203,8 @@ int build_panels(const int32_t* rowptr, const int32_t* col, int64_t n, int32_t m
   const int64_t min_tiles = (n + 65535) / 65536;
   const int64_t T = std::min<int64_t>(n, std::max<int64_t>(tiles_per_panel, min_tiles));
   std::vector<int64_t> cost(n + 1);
+  struct Cut { int32_t p; int64_t r0, r1; };
+  std::vector<Cut> cuts;                 // panel-major
   for (int32_t p = 0; p < P; ++p) {
     cost[0] = 0;
     for (int64_t r = 0; r < n; ++r)
@@ -215,13 +220,26 @@ int build_panels(const int32_t* rowptr, const int32_t* col, int64_t n, int32_t m
       r1 = std::min<int64_t>(r1, std::min<int64_t>(n, r0 + 65536));
       if (t == T) r1 = n;
       while (r1 - r0 > 65536) {          // only possible on the last tile
-        append_tile(out, rowptr, col, order, bucket, P, width, p, r0, r0 + 65536, waves,
-                    lane_target);
+        cuts.push_back(Cut{p, r0, r0 + 65536});
         r0 += 65536;
       }
-      append_tile(out, rowptr, col, order, bucket, P, width, p, r0, r1, waves, lane_target);
+      cuts.push_back(Cut{p, r0, r1});
       r0 = r1;
     }
+  }
+  // Workgroups are dealt to the XCDs round-robin by workgroup id.  Tile k of
+  // the emitted order runs on XCD k % kXcds, so the panel-major list is cut
+  // into runs, one per XCD, that fill that XCD's workgroup ids in turn: the
+  // tiles of one XCD then come from one or two panels, and the workgroups
+  // staging the same panel slice share that XCD's L2.
+  const int64_t nt = static_cast<int64_t>(cuts.size());
+  std::vector<int64_t> slot_tile(nt);
+  int64_t next = 0;
+  for (int64_t x = 0; x < kXcds; ++x)
+    for (int64_t k = x; k < nt; k += kXcds) slot_tile[k] = next++;
+  for (int64_t k = 0; k < nt; ++k) {
+    const Cut& c = cuts[slot_tile[k]];
+    append_tile(out, rowptr, col, order, bucket, P, width, c.p, c.r0, c.r1, waves, lane_target);
   }
   out.wave_groups.push_back(static_cast<int32_t>(out.groups.size() / 4));
   // Trailing padding: prefetches run up to two blocks of steps past a stream's end.
