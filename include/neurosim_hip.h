@@ -101,13 +101,22 @@ typedef struct ns_row_plan {
  * wavefronts owns a run of consecutive groups whose slots are contiguous (its
  * stream).  Padding slots have source index `panel_width` (a zero kept in LDS)
  * and weight code 0.  Edge slot k is original CSR edge perm[k] (or padding). */
+/* Panel layout flag: pair layout.  Every row gets at least two lanes, and
+ * within each (row, panel) segment the edges are grouped by 16-edge weight
+ * block (stable) with each block's run padded to an even length.  Slots 2i and
+ * 2i+1 then hold edges of one block (or padding), and NVFP4 weights take one
+ * uint16 word per slot pair: the two nibbles in the low byte (slot 2i in the
+ * low nibble) and the pair's e4m3 block-scale code in the high byte. */
+#define NS_PANEL_PAIRS 1
+
 typedef struct ns_panel_plan {
   int32_t panel_width;
   int32_t n_panels;
   int32_t n_tiles;
   int32_t n_groups;
   int32_t waves;               /* wavefronts per workgroup the plan was built for */
-  int32_t reserved[3];
+  int32_t flags;               /* NS_PANEL_* layout flags the plan was built with */
+  int32_t reserved[2];
   int64_t n_slots;             /* edge slots including padding and the tail padding */
   int64_t n_step_words;        /* uint32 words of `last_steps` */
   const int32_t* tiles;        /* [n_tiles][4]: panel, first row, end row, first entry of
@@ -120,8 +129,11 @@ typedef struct ns_panel_plan {
   const uint32_t* last_steps;  /* bit k set: step k (slots 64k .. 64k+63) is a group's last */
   const uint16_t* col;         /* [n_slots] source index minus the panel's first neuron */
   const void* weight;          /* [n_slots] weights in slot order, encoding of the matrix:
-                                  F32/F16 values, E4M3 codes, NVFP4 nibbles (two per byte) */
-  const uint8_t* slot_scales;  /* NVFP4: e4m3 block-scale code of each slot's edge */
+                                  F32/F16 values, E4M3 codes, NVFP4 nibbles (two per byte;
+                                  pair layouts: one uint16 word per slot pair, see
+                                  NS_PANEL_PAIRS) */
+  const uint8_t* slot_scales;  /* NVFP4 without NS_PANEL_PAIRS: e4m3 block-scale code of
+                                  each slot's edge (unused with NS_PANEL_PAIRS) */
   float* partials;             /* workspace float[2][n_panels*N*batch]: the second half
                                   holds row sums in row-table order, the first half the
                                   per-panel row sums by row (several panels), added in
@@ -308,7 +320,8 @@ int ns_plan_row_blocks(const int32_t* rowptr_host, int64_t n_rows, int32_t block
  * `tiles_per_panel` tiles of equal cost (segment edges + 1 per row, at most
  * 65536 rows each).  A row whose segment has L edges gets the smallest
  * power-of-two lane count that leaves each lane at most `lane_target` edges
- * (at most 64).  Groups go to the `waves` wavefronts of their tile (which
+ * (at most 64; at least 2 with NS_PANEL_PAIRS in `flags`, where a segment's
+ * length counts its padding items).  Groups go to the `waves` wavefronts of their tile (which
  * must be the kernel's wavefronts per workgroup) longest first onto the
  * least-loaded one.  Call once with all output pointers NULL to get the sizes
  * in *plan (n_panels, panel_width, n_tiles, n_groups, n_slots, waves,
@@ -319,7 +332,8 @@ int ns_plan_row_blocks(const int32_t* rowptr_host, int64_t n_rows, int32_t block
  * uint16[n_slots].  Pointer fields of *plan are not touched. */
 int ns_plan_panels(const int32_t* rowptr_host, const int32_t* col_host, int64_t n_rows,
                    int32_t max_panel_width, int32_t tiles_per_panel, int32_t waves,
-                   int32_t lane_target, ns_panel_plan* plan, int64_t* n_row_entries,
+                   int32_t lane_target, int32_t flags, ns_panel_plan* plan,
+                   int64_t* n_row_entries,
                    int32_t* tiles, int32_t* wave_groups, int32_t* groups, uint16_t* rows,
                    uint32_t* last_steps, int32_t* perm, uint16_t* col);
 

@@ -44,13 +44,18 @@ constexpr int panel_capacity_neurons() {
   return ((163840 - 64) / (4 * BT) - 1) & ~3;
 }
 
+// NVFP4 weights of a pair layout (NS_PANEL_PAIRS): one uint16 word per slot
+// pair, the two nibbles in the low byte and the pair's block-scale code in the
+// high byte.  A kernel template format of its own, next to the NS_WEIGHT_* ones.
+constexpr int kNvfp4Pairs = 4;
+
 // Steps per register block: enough 64-lane loads in flight per wavefront to
 // cover HBM latency with 16 wavefronts per compute unit, within 128 VGPRs.
 template <int BT, int FMT>
 constexpr int block_steps() {
   if constexpr (FMT == NS_WEIGHT_F32) return 8;
   else if constexpr (FMT == NS_WEIGHT_F16) return BT == 1 ? 12 : 8;
-  else if constexpr (FMT == NS_WEIGHT_E4M3) return BT == 1 ? 16 : 12;
+  else if constexpr (FMT == NS_WEIGHT_E4M3 || FMT == kNvfp4Pairs) return BT == 1 ? 16 : 12;
   else return BT == 1 ? 12 : 8;
 }
 
@@ -98,6 +103,8 @@ __device__ __forceinline__ Slot load_slot(const PanelArgs& A, int64_t q0, int k)
     x.w = static_cast<const uint16_t*>(A.weight)[q0 + 64 * k];
   } else if constexpr (FMT == NS_WEIGHT_E4M3) {
     x.w = static_cast<const uint8_t*>(A.weight)[q0 + 64 * k];
+  } else if constexpr (FMT == kNvfp4Pairs) {
+    x.w = static_cast<const uint16_t*>(A.weight)[(q0 >> 1) + 32 * k];
   } else {
     x.w = static_cast<const uint8_t*>(A.weight)[(q0 >> 1) + 32 * k];
   }
@@ -121,9 +128,9 @@ __device__ __forceinline__ const __attribute__((address_space(1))) T* scalar_bas
 // of the block in flight for the next block's address and so waits for that
 // block before issuing the next one.  lane32 is the lane made opaque once per
 // kernel, so it stays in one register for the whole stream (neither a 64-bit
-// copy nor a register a load may target).  The narrower encodings keep
-// per-lane addresses: they compile without the wait, or (e4m3) measure no
-// faster without it.
+// copy nor a register a load may target).  NVFP4 pair words take the same
+// path.  The other narrow encodings keep per-lane addresses: they compile
+// without the wait, or (e4m3) measure no faster without it.
 template <int FMT, int D>
 __device__ __forceinline__ void load_block(const PanelArgs& A, int64_t block0, int lane,
                                            uint32_t lane32, Slot (&dst)[D]) {
@@ -135,6 +142,15 @@ __device__ __forceinline__ void load_block(const PanelArgs& A, int64_t block0, i
       const uint32_t at = lane32 + 64u * k;
       dst[k].c = col[at];
       dst[k].w = weight[at];
+      dst[k].sc = 0u;
+    }
+  } else if constexpr (FMT == kNvfp4Pairs) {
+    const auto col = scalar_base(A.col + block0);
+    const auto words = scalar_base(static_cast<const uint16_t*>(A.weight) + block0 / 2);
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+      dst[k].c = col[lane32 + 64u * k];
+      dst[k].w = words[(lane32 >> 1) + 32u * k];
       dst[k].sc = 0u;
     }
   } else {
@@ -152,6 +168,9 @@ __device__ __forceinline__ float decode_slot(const Slot& x, int lane, float gsca
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x.w)));
   } else if constexpr (FMT == NS_WEIGHT_E4M3) {
     return e4m3_to_float(x.w) * gscale;
+  } else if constexpr (FMT == kNvfp4Pairs) {
+    const ns_v2f pair = e2m1_pair(x.w & 0xFFu);
+    return ((lane & 1) ? pair.y : pair.x) * (e4m3_to_float(x.w >> 8) * gscale);
   } else {
     const ns_v2f pair = e2m1_pair(x.w & 0xFFu);
     return ((lane & 1) ? pair.y : pair.x) * (e4m3_to_float(x.sc) * gscale);
@@ -201,7 +220,8 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
   const int panel = tile[0], row0 = tile[1];
   const int64_t base = static_cast<int64_t>(panel) * A.width;
   const int len = static_cast<int>(min<int64_t>(A.width, A.N - base));
-  const float gscale = (FMT == NS_WEIGHT_E4M3 || FMT == NS_WEIGHT_NVFP4) ? *A.gscale : 1.0f;
+  const float gscale =
+      (FMT == NS_WEIGHT_E4M3 || FMT == NS_WEIGHT_NVFP4 || FMT == kNvfp4Pairs) ? *A.gscale : 1.0f;
 
   // A contiguous slice of s is staged with direct global -> LDS loads, issued
   // first since they need only the panel: wavefront chunk ch covers float4s
@@ -415,6 +435,7 @@ hipError_t launch_panels(const PanelArgs& A, int fmt, int n_tiles, hipStream_t s
     case NS_WEIGHT_F32: panel_tick_kernel<BT, NS_WEIGHT_F32><<<grid, block, 0, stream>>>(A); break;
     case NS_WEIGHT_F16: panel_tick_kernel<BT, NS_WEIGHT_F16><<<grid, block, 0, stream>>>(A); break;
     case NS_WEIGHT_E4M3: panel_tick_kernel<BT, NS_WEIGHT_E4M3><<<grid, block, 0, stream>>>(A); break;
+    case kNvfp4Pairs: panel_tick_kernel<BT, kNvfp4Pairs><<<grid, block, 0, stream>>>(A); break;
     default: panel_tick_kernel<BT, NS_WEIGHT_NVFP4><<<grid, block, 0, stream>>>(A); break;
   }
   hipError_t err = hipGetLastError();
@@ -453,10 +474,14 @@ int panel_step(const ns_step_args& a, hipStream_t stream) {
       !pl.weight)
     return fail("panel plan tables are required");
   if (pl.n_step_words < pl.n_slots / 64 / 32 + 2) return fail("panel plan's step bitmap is short");
-  if (a.matrix.format == NS_WEIGHT_NVFP4 && !pl.slot_scales)
+  if (pl.flags & ~NS_PANEL_PAIRS) return fail("unknown panel layout flags %d", pl.flags);
+  const bool pairs = (pl.flags & NS_PANEL_PAIRS) != 0;
+  if (a.matrix.format == NS_WEIGHT_NVFP4 && !pairs && !pl.slot_scales)
     return fail("NVFP4 panels require per-slot block scales");
   if (!pl.partials) return fail("the panel path needs its partials workspace");
-  const uintptr_t need = a.matrix.format == NS_WEIGHT_F32 ? 4 : a.matrix.format == NS_WEIGHT_F16 ? 2 : 1;
+  const uintptr_t need = a.matrix.format == NS_WEIGHT_F32 ? 4
+                         : (a.matrix.format == NS_WEIGHT_F16 ||
+                            (a.matrix.format == NS_WEIGHT_NVFP4 && pairs)) ? 2 : 1;
   if (reinterpret_cast<uintptr_t>(pl.col) % 2 || reinterpret_cast<uintptr_t>(pl.weight) % need)
     return fail("panel arrays are misaligned");
   {
@@ -486,8 +511,9 @@ int panel_step(const ns_step_args& a, hipStream_t stream) {
   const bool aligned = reinterpret_cast<uintptr_t>(a.state.data) % 16 == 0;
   A.s_vec = aligned && ((a.batch == 1 && a.state.stride_n == 1) ||
                         (a.batch == 2 && a.state.stride_b == 1 && a.state.stride_n == 2));
-  const hipError_t err = a.batch == 1 ? launch_panels<1>(A, a.matrix.format, pl.n_tiles, stream)
-                                      : launch_panels<2>(A, a.matrix.format, pl.n_tiles, stream);
+  const int fmt = a.matrix.format == NS_WEIGHT_NVFP4 && pairs ? kNvfp4Pairs : a.matrix.format;
+  const hipError_t err = a.batch == 1 ? launch_panels<1>(A, fmt, pl.n_tiles, stream)
+                                      : launch_panels<2>(A, fmt, pl.n_tiles, stream);
   if (err != hipSuccess) return fail_launch("panel tick", err);
   return NS_OK;
 }

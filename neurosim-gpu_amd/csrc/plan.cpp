@@ -79,10 +79,10 @@ struct PanelLayout {
   std::vector<uint32_t> last_steps;   // bit k: step k (slots 64k..64k+63) ends a group
 };
 
-int32_t log2_lanes(int64_t len, int32_t lane_target) {
-  // Lanes per row: the smallest power of two that leaves each lane at most
-  // lane_target edges, capped at a whole wavefront.
-  int32_t lg = 0;
+int32_t log2_lanes(int64_t len, int32_t lane_target, int32_t min_lg) {
+  // Lanes per row: the smallest power of two (at least 2^min_lg) that leaves
+  // each lane at most lane_target items, capped at a whole wavefront.
+  int32_t lg = min_lg;
   while (lg < 6 && len > (int64_t{lane_target} << lg)) ++lg;
   return lg;
 }
@@ -91,15 +91,23 @@ struct Group {
   int32_t lg, nrows, steps, first;   // first: index of its first row in the sorted order
 };
 
+// A row's items in one panel: its edges there, in the order lanes take them,
+// plus (for pair layouts) padding items (-1).  Row r's items for panel p are
+// items[base[r] + bucket[r*(P+1)+p] .. base[r] + bucket[r*(P+1)+p+1]).
+struct Items {
+  std::vector<int32_t> items, bucket;
+  std::vector<int64_t> base;
+};
+
 // Lays out tile (panel p, rows [r0, r1)): rows sorted by segment length
 // (descending, ties by row), cut into groups of 64 >> lg rows sharing one
 // lanes-per-row width, groups dealt longest first onto the least-loaded of the
 // tile's wavefronts, then every wavefront's groups emitted back to back.
-void append_tile(PanelLayout& out, const int32_t* rowptr, const int32_t* col,
-                 const std::vector<int32_t>& order, const std::vector<int32_t>& bucket,
-                 int32_t P, int64_t width, int32_t p, int64_t r0, int64_t r1, int32_t waves,
-                 int32_t lane_target) {
+void append_tile(PanelLayout& out, const int32_t* col, const Items& it, int32_t P, int64_t width,
+                 int32_t p, int64_t r0, int64_t r1, int32_t waves, int32_t lane_target,
+                 int32_t min_lg) {
   const int64_t nr = r1 - r0;
+  const std::vector<int32_t>& bucket = it.bucket;
   auto seg_len = [&](int64_t r) -> int64_t {
     const int32_t* b = &bucket[r * (P + 1)];
     return b[p + 1] - b[p];
@@ -111,10 +119,11 @@ void append_tile(PanelLayout& out, const int32_t* rowptr, const int32_t* col,
   std::vector<Group> groups;
   for (int64_t i = 0; i < nr;) {
     const int64_t len = seg_len(sorted[i]);
-    const int32_t lg = log2_lanes(len, lane_target);
+    const int32_t lg = log2_lanes(len, lane_target, min_lg);
     const int64_t cap = 64 >> lg;
     int64_t n = 1;
-    while (n < cap && i + n < nr && log2_lanes(seg_len(sorted[i + n]), lane_target) == lg) ++n;
+    while (n < cap && i + n < nr && log2_lanes(seg_len(sorted[i + n]), lane_target, min_lg) == lg)
+      ++n;
     const int64_t lanes = int64_t{1} << lg;
     // Every group takes at least one step (rows with no edges read one padding
     // step), so each group ends on a step the boundary bitmap can mark.
@@ -160,7 +169,7 @@ void append_tile(PanelLayout& out, const int32_t* rowptr, const int32_t* col,
           if (k < grp.nrows) {
             const int64_t r = sorted[grp.first + k];
             const int64_t idx = int64_t{step} * lanes + j;
-            if (idx < seg_len(r)) edge = order[rowptr[r] + bucket[r * (P + 1) + p] + idx];
+            if (idx < seg_len(r)) edge = it.items[it.base[r] + bucket[r * (P + 1) + p] + idx];
           }
           out.perm.push_back(edge);
           out.col.push_back(edge < 0 ? static_cast<uint16_t>(width)
@@ -172,7 +181,7 @@ void append_tile(PanelLayout& out, const int32_t* rowptr, const int32_t* col,
 }
 
 int build_panels(const int32_t* rowptr, const int32_t* col, int64_t n, int32_t max_width,
-                 int32_t tiles_per_panel, int32_t waves, int32_t lane_target,
+                 int32_t tiles_per_panel, int32_t waves, int32_t lane_target, bool pairs,
                  PanelLayout& out) {
   const int64_t m = rowptr[n];
   max_width &= ~3;                       // panel widths are whole 4-neuron groups
@@ -198,6 +207,41 @@ int build_panels(const int32_t* rowptr, const int32_t* col, int64_t n, int32_t m
       order[rowptr[r] + fill[col[e] / width]++] = static_cast<int32_t>(e);
   }
 
+  // Items.  Plain layouts: the edges as grouped above.  Pair layouts: within
+  // each (row, panel) segment the edges grouped by 16-edge weight block (stable,
+  // so a column-sorted CSR keeps its order) and each block's run padded to an
+  // even length, so items 2i and 2i+1 share a block.  Every row gets at least
+  // two lanes, so lanes 2q and 2q+1 of a step hold items 2i and 2i+1 of one row.
+  Items it;
+  it.base.resize(n + 1);
+  if (!pairs) {
+    it.items = std::move(order);
+    it.bucket = std::move(bucket);
+    for (int64_t r = 0; r <= n; ++r) it.base[r] = rowptr[r];
+  } else {
+    it.bucket.assign(n * (P + 1), 0);
+    it.items.reserve(m + m / 8 + 16);
+    std::vector<int32_t> seg;
+    for (int64_t r = 0; r < n; ++r) {
+      it.base[r] = static_cast<int64_t>(it.items.size());
+      const int32_t* b = &bucket[r * (P + 1)];
+      int32_t* ib = &it.bucket[r * (P + 1)];
+      for (int32_t p = 0; p < P; ++p) {
+        seg.assign(order.begin() + rowptr[r] + b[p], order.begin() + rowptr[r] + b[p + 1]);
+        std::stable_sort(seg.begin(), seg.end(), [](int32_t x, int32_t y) { return (x >> 4) < (y >> 4); });
+        for (size_t i = 0; i < seg.size();) {
+          size_t j = i;
+          while (j < seg.size() && (seg[j] >> 4) == (seg[i] >> 4)) it.items.push_back(seg[j++]);
+          if ((j - i) % 2) it.items.push_back(-1);
+          i = j;
+        }
+        ib[p + 1] = static_cast<int32_t>(static_cast<int64_t>(it.items.size()) - it.base[r]);
+      }
+    }
+    it.base[n] = static_cast<int64_t>(it.items.size());
+  }
+  const int32_t min_lg = pairs ? 1 : 0;
+
   // Tiles of panel p: consecutive row ranges of about equal cost (segment
   // edges + 1 per row), at most 65536 rows each (16-bit tile-local rows).
   const int64_t min_tiles = (n + 65535) / 65536;
@@ -208,7 +252,7 @@ int build_panels(const int32_t* rowptr, const int32_t* col, int64_t n, int32_t m
   for (int32_t p = 0; p < P; ++p) {
     cost[0] = 0;
     for (int64_t r = 0; r < n; ++r)
-      cost[r + 1] = cost[r] + (bucket[r * (P + 1) + p + 1] - bucket[r * (P + 1) + p]) + 1;
+      cost[r + 1] = cost[r] + (it.bucket[r * (P + 1) + p + 1] - it.bucket[r * (P + 1) + p]) + 1;
     int64_t r0 = 0;
     for (int64_t t = 1; t <= T && r0 < n; ++t) {
       int64_t r1 = n;
@@ -239,7 +283,7 @@ int build_panels(const int32_t* rowptr, const int32_t* col, int64_t n, int32_t m
     for (int64_t k = x; k < nt; k += kXcds) slot_tile[k] = next++;
   for (int64_t k = 0; k < nt; ++k) {
     const Cut& c = cuts[slot_tile[k]];
-    append_tile(out, rowptr, col, order, bucket, P, width, c.p, c.r0, c.r1, waves, lane_target);
+    append_tile(out, col, it, P, width, c.p, c.r0, c.r1, waves, lane_target, min_lg);
   }
   out.wave_groups.push_back(static_cast<int32_t>(out.groups.size() / 4));
   // Trailing padding: prefetches run up to two blocks of steps past a stream's end.
@@ -259,7 +303,8 @@ int build_panels(const int32_t* rowptr, const int32_t* col, int64_t n, int32_t m
 
 extern "C" int ns_plan_panels(const int32_t* rowptr, const int32_t* col, int64_t n_rows,
                               int32_t max_panel_width, int32_t tiles_per_panel, int32_t waves,
-                              int32_t lane_target, ns_panel_plan* plan, int64_t* n_row_entries,
+                              int32_t lane_target, int32_t flags, ns_panel_plan* plan,
+                              int64_t* n_row_entries,
                               int32_t* tiles, int32_t* wave_groups, int32_t* groups,
                               uint16_t* rows, uint32_t* last_steps, int32_t* perm,
                               uint16_t* col_out) {
@@ -275,15 +320,17 @@ extern "C" int ns_plan_panels(const int32_t* rowptr, const int32_t* col, int64_t
   if (tiles_per_panel < 1) return fail("tiles_per_panel must be positive");
   if (waves != kPanelWaves) return fail("the panel kernel runs %d wavefronts per workgroup", kPanelWaves);
   if (lane_target < 1) return fail("lane_target must be positive");
+  if (flags & ~NS_PANEL_PAIRS) return fail("unknown panel layout flags %d", flags);
   PanelLayout layout;
   if (int rc = build_panels(rowptr, col, n_rows, max_panel_width, tiles_per_panel, waves,
-                            lane_target, layout))
+                            lane_target, (flags & NS_PANEL_PAIRS) != 0, layout))
     return rc;
   plan->panel_width = layout.panel_width;
   plan->n_panels = layout.n_panels;
   plan->n_tiles = static_cast<int32_t>(layout.tiles.size() / 4);
   plan->n_groups = static_cast<int32_t>(layout.groups.size() / 4);
   plan->waves = waves;
+  plan->flags = flags;
   plan->n_slots = static_cast<int64_t>(layout.perm.size());
   plan->n_step_words = static_cast<int64_t>(layout.last_steps.size());
   *n_row_entries = static_cast<int64_t>(layout.rows.size());

@@ -71,7 +71,8 @@ class _RowPlan(ctypes.Structure):
 class _PanelPlan(ctypes.Structure):
     _fields_ = [("panel_width", ctypes.c_int32), ("n_panels", ctypes.c_int32),
                 ("n_tiles", ctypes.c_int32), ("n_groups", ctypes.c_int32),
-                ("waves", ctypes.c_int32), ("reserved", ctypes.c_int32 * 3), ("n_slots", _c_i64),
+                ("waves", ctypes.c_int32), ("flags", ctypes.c_int32),
+                ("reserved", ctypes.c_int32 * 2), ("n_slots", _c_i64),
                 ("n_step_words", _c_i64), ("tiles", _c_ptr), ("wave_groups", _c_ptr),
                 ("groups", _c_ptr), ("rows", _c_ptr), ("last_steps", _c_ptr), ("col", _c_ptr),
                 ("weight", _c_ptr), ("slot_scales", _c_ptr), ("partials", _c_ptr)]
@@ -170,8 +171,8 @@ def load_library() -> ctypes.CDLL:
                                       ctypes.POINTER(ctypes.c_int32)]
     lib.ns_plan_panels.restype = ctypes.c_int
     lib.ns_plan_panels.argtypes = [_c_ptr, _c_ptr, _c_i64, ctypes.c_int32, ctypes.c_int32,
-                                   ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(_PanelPlan),
-                                   ctypes.POINTER(_c_i64)] + [_c_ptr] * 7
+                                   ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                   ctypes.POINTER(_PanelPlan), ctypes.POINTER(_c_i64)] + [_c_ptr] * 7
     lib.ns_plan_bands.restype = ctypes.c_int
     lib.ns_plan_bands.argtypes = [_c_ptr, _c_ptr, _c_i64, ctypes.c_int32, ctypes.c_int32,
                                   ctypes.c_int32, ctypes.POINTER(_BandPlan)] + [_c_ptr] * 5
@@ -371,8 +372,12 @@ def panel_geometry(batch: int) -> tuple[int, int]:
 LANE_TARGET = 24   # at most this many edges per lane before a row gets more lanes
 
 
+PANEL_PAIRS = 1   # NS_PANEL_PAIRS
+
+
 def plan_panels_host(rowptr: torch.Tensor, col: torch.Tensor, batch: int, tiles_per_panel: int,
-                     max_panel_width: int | None = None, lane_target: int = LANE_TARGET):
+                     max_panel_width: int | None = None, lane_target: int = LANE_TARGET,
+                     pairs: bool = False):
     """Host panel layout of a CSR (numpy arrays): see ns_plan_panels."""
     lib = load_library()
     width, waves = panel_geometry(batch)
@@ -384,8 +389,8 @@ def plan_panels_host(rowptr: torch.Tensor, col: torch.Tensor, batch: int, tiles_
     plan = _PanelPlan()
     entries = _c_i64()
     args = (rowptr.ctypes.data, col.ctypes.data if col.size else None, n, width,
-            int(tiles_per_panel), waves, int(lane_target), ctypes.byref(plan),
-            ctypes.byref(entries))
+            int(tiles_per_panel), waves, int(lane_target), PANEL_PAIRS if pairs else 0,
+            ctypes.byref(plan), ctypes.byref(entries))
     _raise_on(lib.ns_plan_panels(*args, *([None] * 7)), lib)
     tiles = np.empty(4 * plan.n_tiles, np.int32)
     wave_groups = np.empty(plan.n_tiles * plan.waves + 1, np.int32)
@@ -441,6 +446,7 @@ class _SlotLayout:
     n_slots: int
     perm: torch.Tensor
     valid: torch.Tensor
+    pairs: bool = False
     _slot_weights: tuple | None = None
     _slot_key = None
 
@@ -468,8 +474,19 @@ class _SlotLayout:
                 nibble = (weight[edge >> 1] >> ((edge & 1) * 4).to(torch.uint8)) & 15
                 nibble = torch.where(self.valid, nibble, torch.zeros_like(nibble))
                 slots = (nibble[0::2] | (nibble[1::2] << 4)).contiguous()
-                scales = torch.where(self.valid, block_scales[edge >> 4],
-                                     torch.zeros((), dtype=torch.uint8, device=weight.device))
+                if self.pairs:
+                    # Pair layout: both slots of a pair lie in one weight block, so
+                    # the pair's word carries one scale code (the first real slot's).
+                    first_real = self.valid[0::2]
+                    pair_edge = torch.where(first_real, edge[0::2], edge[1::2])
+                    pair_code = torch.where(first_real | self.valid[1::2], block_scales[pair_edge >> 4],
+                                            torch.zeros((), dtype=torch.uint8, device=weight.device))
+                    slots = torch.stack((slots, pair_code), dim=1).contiguous().view(torch.int16)
+                    slots = slots.reshape(-1)
+                    scales = None
+                else:
+                    scales = torch.where(self.valid, block_scales[edge >> 4],
+                                         torch.zeros((), dtype=torch.uint8, device=weight.device))
             self._slot_weights = (slots.contiguous(), None if scales is None else scales.contiguous())
             self._slot_key = key
         return self._slot_weights
@@ -486,7 +503,8 @@ class PanelLayout(_SlotLayout):
     """
 
     def __init__(self, topology, batch: int, device, *, tiles_per_panel: int | None = None,
-                 max_panel_width: int | None = None, lane_target: int = LANE_TARGET) -> None:
+                 max_panel_width: int | None = None, lane_target: int = LANE_TARGET,
+                 pairs: bool = False) -> None:
         n = topology.n_neurons
         width, _ = panel_geometry(batch)
         panels = -(-n // (min(width, max_panel_width or width) & ~3))
@@ -496,7 +514,8 @@ class PanelLayout(_SlotLayout):
             tiles_per_panel = max(1, units // panels)
         plan, tiles, wave_groups, groups, rows, last_steps, perm, cols = plan_panels_host(
             topology.in_rowptr, topology.in_col, batch, tiles_per_panel, max_panel_width,
-            lane_target)
+            lane_target, pairs)
+        self.pairs = bool(pairs)
         self.batch, self.n = int(batch), n
         self.n_panels, self.n_tiles, self.n_slots = plan.n_panels, plan.n_tiles, plan.n_slots
         self.n_groups = plan.n_groups

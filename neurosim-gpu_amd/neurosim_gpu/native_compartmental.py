@@ -139,6 +139,10 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
     least ``BAND_AUTO_MIN_BANDS`` bands, rows otherwise.  ``panel_width`` caps
     the neurons per panel (default: what LDS holds) and ``panel_tiles`` sets
     the workgroups per panel (default: compute units / panels).
+    ``panel_pairs`` builds the pair layout (``NS_PANEL_PAIRS``: every row at least
+    two lanes, edges of one 16-edge weight block in slot pairs), whose NVFP4
+    slots carry one block-scale byte per pair instead of per slot; the default
+    uses it for NVFP4 weights only.
     ``band_width`` sets the sources per band (default ``BAND_WIDTH``),
     ``band_rows`` the destination rows per band workgroup (default: two
     workgroups per compute unit, ``default_band_rows``) and ``band_steps`` the
@@ -151,7 +155,7 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
                  weight_format: str | None = None, kernel: str = "auto",
                  panel_width: int | None = None, panel_tiles: int | None = None,
                  band_width: int | None = None, band_rows: int | None = None,
-                 band_steps: int = 4) -> None:
+                 band_steps: int = 4, panel_pairs: bool | None = None) -> None:
         if kernel not in ("auto", "rows", "panels", "bands"):
             raise ValueError("kernel must be 'auto', 'rows', 'panels' or 'bands'")
         if threads_per_row not in (None, 8, 16, 32):
@@ -182,8 +186,11 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
             kernel == "auto" and native and batch > 0 and batch % 16 == 0
             and topology.n_neurons >= BAND_AUTO_MIN_BANDS * BAND_WIDTH)
         self.kernel = "panels" if use_panels else "bands" if use_bands else "rows"
+        if panel_pairs is None:
+            panel_pairs = weight_format == "nvfp4"
         self._panels = (PanelLayout(topology, batch, initial_state.device,
-                                    tiles_per_panel=panel_tiles, max_panel_width=panel_width)
+                                    tiles_per_panel=panel_tiles, max_panel_width=panel_width,
+                                    pairs=panel_pairs)
                         if use_panels else None)
         self._bands = (BandLayout(topology, initial_state.device,
                                   band_width=band_width or BAND_WIDTH, block_rows=band_rows,

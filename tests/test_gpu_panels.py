@@ -41,14 +41,16 @@ def hub_case(gpu, n=12_000, seed=2):
     return graph, topology_to(topology, gpu), model_to(model, gpu), params
 
 
+@pytest.mark.parametrize("pairs", [False, True])
 @pytest.mark.parametrize("batch", [1, 2])
 @pytest.mark.parametrize("width,tiles", [(None, None), (1000, 7), (256, 2)])
-def test_panels_match_oracle(gpu, batch, width, tiles):
-    print(f"case panels batch={batch} width={width} tiles={tiles}", flush=True)
+def test_panels_match_oracle(gpu, batch, width, tiles, pairs):
+    print(f"case panels batch={batch} width={width} tiles={tiles} pairs={pairs}", flush=True)
     graph, topology, model, params = hub_case(gpu)
     drive = column_drive(batch)
     native = NativeDendriticMatrixRuntime(topology, model, torch.zeros(batch, graph.n, device=gpu),
-                                          kernel="panels", panel_width=width, panel_tiles=tiles)
+                                          kernel="panels", panel_width=width, panel_tiles=tiles,
+                                          panel_pairs=pairs)
     oracle = ort.MatrixOracle(graph, params, torch.zeros(batch, graph.n))
     assert native.kernel == "panels"
     worst = 0.0
@@ -96,8 +98,10 @@ def test_panel_formats_equal_decoded_fp32(gpu, fmt, batch):
     decoded = SparseTopology.from_edges(
         6000, topology.src, topology.dst,
         torch.from_numpy(decoded_host).to(gpu)[topology.out_weight_index.long()])
+    # the same layout as the packed runtime (NVFP4 defaults to the pair layout)
     reference = NativeDendriticMatrixRuntime(decoded, model, torch.zeros(batch, 6000, device=gpu),
-                                             kernel="panels", panel_width=1024, panel_tiles=5)
+                                             kernel="panels", panel_width=1024, panel_tiles=5,
+                                             panel_pairs=native._panels.pairs)
     oracle = ort.MatrixOracle(graph, params, torch.zeros(batch, 6000), in_weight=decoded_host)
     for _ in range(10):
         native.step(0.2, dendritic_drive=0.1)
@@ -106,6 +110,31 @@ def test_panel_formats_equal_decoded_fp32(gpu, fmt, batch):
         for field in FIELDS:
             assert torch.equal(getattr(native, field), getattr(reference, field))
     assert errors(native, oracle) <= 1e-5
+
+
+@pytest.mark.parametrize("batch", [1, 2])
+def test_nvfp4_pair_layout_is_the_default_and_matches_per_slot_scales(gpu, batch):
+    """NVFP4 on the pair layout (one scale byte per slot pair) against NVFP4 on the
+    plain layout (one per slot): the same decoded weights, so the same states up to
+    summation order (the layouts differ), and both within 1e-5 of the oracle."""
+    graph, topology, model, params = hub_case(gpu, n=6000, seed=9)
+    runs = {}
+    for pairs in (None, False):
+        runs[pairs] = NativeDendriticMatrixRuntime(
+            topology, model, torch.zeros(batch, 6000, device=gpu), kernel="panels",
+            panel_width=1024, panel_tiles=5, weight_format="nvfp4", panel_pairs=pairs)
+    assert runs[None]._panels.pairs and not runs[False]._panels.pairs
+    runs[None]._weights()
+    codes, block, scale = runs[None]._packed_weight
+    decoded_host = op.decode_packed(codes.cpu().numpy(), block.cpu().numpy(),
+                                    np.float32(scale.item()), topology.n_edges, "nvfp4")
+    oracle = ort.MatrixOracle(graph, params, torch.zeros(batch, 6000), in_weight=decoded_host)
+    for _ in range(10):
+        for native in runs.values():
+            native.step(0.2, dendritic_drive=0.1)
+        oracle.step(0.2, 0.1)
+    assert errors(runs[None], runs[False]) <= 2e-6
+    assert errors(runs[None], oracle) <= 1e-5
 
 
 def test_panel_weight_refresh_after_mutation(gpu):

@@ -41,10 +41,17 @@ GRAPHS = {
 
 
 def emulate(graph: otop.Graph, batch: int, tiles_per_panel: int, width: int | None,
-            source: np.ndarray, lane_target: int = 24):
+            source: np.ndarray, lane_target: int = 24, pairs: bool = False):
     plan, tiles, wave_groups, groups, rows, last_steps, perm, cols = plan_panels_host(
         torch.from_numpy(graph.in_rowptr), torch.from_numpy(graph.in_col), batch, tiles_per_panel,
-        width, lane_target)
+        width, lane_target, pairs)
+    assert plan.flags == (1 if pairs else 0)
+    if pairs:
+        # slots 2i and 2i+1 hold edges of one 16-edge weight block, or padding
+        pair = perm.reshape(-1, 2)
+        both = (pair >= 0).all(1)
+        assert np.array_equal(pair[both, 0] >> 4, pair[both, 1] >> 4)
+        assert (groups.reshape(-1, 4)[:, 2] & 255).min(initial=1) >= 1, "every row has two lanes"
     n, m = graph.n, graph.n_edges
     cap, waves = panel_geometry(batch)
     W, P = plan.panel_width, plan.n_panels
@@ -130,15 +137,16 @@ def emulate(graph: otop.Graph, batch: int, tiles_per_panel: int, width: int | No
     return plan, partial.sum(0)
 
 
+@pytest.mark.parametrize("pairs", [False, True])
 @pytest.mark.parametrize("name", list(GRAPHS))
 @pytest.mark.parametrize("batch,tiles,width", [(1, 3, None), (1, 5, 256), (2, 2, 1000), (2, 1, 64)])
-def test_panel_layout_reproduces_the_csr_product(name, batch, tiles, width):
+def test_panel_layout_reproduces_the_csr_product(name, batch, tiles, width, pairs):
     graph = GRAPHS[name]()
     if width is not None and graph.n // width > 24:
         width = -(-graph.n // 24)          # keep the python emulation to <= 24 panels
     rng = np.random.default_rng(11)
     source = rng.random((graph.n, batch))
-    plan, result = emulate(graph, batch, tiles, width, source)
+    plan, result = emulate(graph, batch, tiles, width, source, pairs=pairs)
     from scipy.sparse import csr_matrix
 
     matrix = csr_matrix((graph.in_weight.astype(np.float64), graph.in_col, graph.in_rowptr),
@@ -176,10 +184,13 @@ def test_planner_rejects_bad_geometry():
     entries = native._c_i64()
     import ctypes
 
-    rc = lib.ns_plan_panels(rowptr.ctypes.data, col.ctypes.data, 2, 64, 1, 16, 12,
+    rc = lib.ns_plan_panels(rowptr.ctypes.data, col.ctypes.data, 2, 64, 1, 16, 12, 0,
                             ctypes.byref(plan), ctypes.byref(entries), *([None] * 7))
     assert rc != 0 and b"out of range" in lib.ns_last_error()
     col = np.array([0, 1], np.int32)
-    rc = lib.ns_plan_panels(rowptr.ctypes.data, col.ctypes.data, 2, 64, 1, 8, 12,
+    rc = lib.ns_plan_panels(rowptr.ctypes.data, col.ctypes.data, 2, 64, 1, 8, 12, 0,
                             ctypes.byref(plan), ctypes.byref(entries), *([None] * 7))
     assert rc != 0 and b"wavefronts" in lib.ns_last_error()
+    rc = lib.ns_plan_panels(rowptr.ctypes.data, col.ctypes.data, 2, 64, 1, 16, 12, 2,
+                            ctypes.byref(plan), ctypes.byref(entries), *([None] * 7))
+    assert rc != 0 and b"flags" in lib.ns_last_error()
