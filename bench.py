@@ -259,7 +259,13 @@ def measure_backward(topology, model, repeats: int = 10) -> dict:
     every parameter, the weights and the state requiring gradients, loss =
     sum of the new state): the native backward against autograd through the
     torch step that the reference runs for such ticks, each timed with HIP
-    events over ``repeats`` forward+backward passes."""
+    events over ``repeats`` forward+backward passes.  The weights do not
+    change between passes, so from the second backward on the native
+    transposed product streams a source-major copy of them (one gather per
+    weight version); ``native_changing_weights_ms`` times the native pass with
+    that copy off, as when an optimizer updates the weights every tick, and
+    ``native_bptt8_ms_per_tick`` eight recorded ticks and one backward through
+    them, per tick."""
     from neurosim_gpu import DendriticMatrixRuntime
 
     n = topology.n_neurons
@@ -271,15 +277,22 @@ def measure_backward(topology, model, repeats: int = 10) -> dict:
     dyn = DendriticDynamics(Dynamics(params[0], params[1]), *params[2:])
     out = {"workload": f"one fp32 tick + backward, N={n} M={topology.n_edges} B=1, gradients of "
                        "the weights, the six parameters and the state", "repeats": repeats}
-    for name, cls in (("native", NativeDendriticMatrixRuntime), ("torch_autograd", DendriticMatrixRuntime)):
+    runs = (("native", NativeDendriticMatrixRuntime, 1, True),
+            ("native_changing_weights", NativeDendriticMatrixRuntime, 1, False),
+            ("native_bptt8", NativeDendriticMatrixRuntime, 8, True),
+            ("torch_autograd", DendriticMatrixRuntime, 1, True))
+    for name, cls, ticks, copy in runs:
         state = torch.full((1, n), 0.2, device=weight.device)
         runtime = cls(trained, dyn, state)
+        if hasattr(runtime, "source_major_weights"):
+            runtime.source_major_weights.enabled = copy
 
         def once():
             runtime.state = state.clone().requires_grad_(True)
             runtime.dendritic_state = torch.zeros_like(state)
             runtime.adaptation_state = torch.zeros_like(state)
-            runtime.step(0.2, dendritic_drive=0.1)
+            for _ in range(ticks):
+                runtime.step(0.2, dendritic_drive=0.1)
             runtime.state.sum().backward()
 
         try:
@@ -297,7 +310,10 @@ def measure_backward(topology, model, repeats: int = 10) -> dict:
             once()
         end.record()
         torch.cuda.synchronize()
-        out[f"{name}_ms"] = round(start.elapsed_time(end) / repeats, 4)
+        if ticks == 1:
+            out[f"{name}_ms"] = round(start.elapsed_time(end) / repeats, 4)
+        else:
+            out[f"{name}_ms_per_tick"] = round(start.elapsed_time(end) / repeats / ticks, 4)
         weight.grad = None
         for p in params:
             p.grad = None

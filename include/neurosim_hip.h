@@ -258,6 +258,10 @@ typedef struct ns_step_grad_args {
   float* d_weight;             /* [M] in CSR order; NULL: not computed */
   float* d_params[6];          /* [N] each, per neuron; NULL: not computed */
   float* workspace;            /* ns_step_backward_workspace_floats(N, B) floats */
+  const float* out_weight;     /* optional [M]: the CSR weights in source-major order,
+                                  out_weight[e] == matrix.weight[out_weight_index[e]];
+                                  when set, the transposed product streams it instead of
+                                  gathering through out_weight_index (NULL: gather) */
 } ns_step_grad_args;
 
 /* Arguments of one weight encoding (fp8 e4m3 or NVFP4 CSR payload). */

@@ -32,6 +32,7 @@ namespace {
 
 constexpr int kGradThreads = 256;
 constexpr int kGradChunk = 8;   // columns per pass of the wavefront kernels
+constexpr int kGradUnroll = 4;  // edges per lane per round of the edge loops
 
 struct GradArgs {
   int64_t N, B;
@@ -99,7 +100,7 @@ __device__ __forceinline__ float wave_sum(float x) {
 // gs[b, c] += sum over out-edges e of source c of w[owi[e]] * gj[dst[e], b].
 __global__ __launch_bounds__(kGradThreads) void transposed_product_kernel(
     const int32_t* out_rowptr, const int32_t* dst, const int32_t* owi, const float* w,
-    const float* gj, int64_t N, int64_t B, OutPlane gs) {
+    const float* w_out, const float* gj, int64_t N, int64_t B, OutPlane gs) {
   const int64_t c = static_cast<int64_t>(blockIdx.x) * (kGradThreads / 64) + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (c >= N) return;
@@ -108,12 +109,26 @@ __global__ __launch_bounds__(kGradThreads) void transposed_product_kernel(
     float acc[kGradChunk];
 #pragma unroll
     for (int q = 0; q < kGradChunk; ++q) acc[q] = 0.0f;
-    for (int32_t e = e0 + lane; e < e1; e += 64) {
-      const float weight = w[owi[e]];
-      const int64_t t = dst[e];
+    // kGradUnroll edges per lane per round, every load of a round issued before
+    // the first multiply (an edge past the row's end rereads the row's last edge
+    // and adds nothing), so a round waits on memory once.
+    for (int32_t e = e0 + lane; e < e1; e += 64 * kGradUnroll) {
+      float weight[kGradUnroll];
+      int64_t t[kGradUnroll];
 #pragma unroll
-      for (int q = 0; q < kGradChunk; ++q)
-        if (b0 + q < B) acc[q] = __builtin_fmaf(weight, gj[t * B + b0 + q], acc[q]);
+      for (int u = 0; u < kGradUnroll; ++u) {
+        const int32_t at = min(e + 64 * u, e1 - 1);
+        // Source-major weights stream; otherwise each one is a gather into the CSR order.
+        weight[u] = w_out ? w_out[at] : w[owi[at]];
+        t[u] = dst[at];
+      }
+#pragma unroll
+      for (int u = 0; u < kGradUnroll; ++u) {
+        if (e + 64 * u >= e1) break;
+#pragma unroll
+        for (int q = 0; q < kGradChunk; ++q)
+          if (b0 + q < B) acc[q] = __builtin_fmaf(weight[u], gj[t[u] * B + b0 + q], acc[q]);
+      }
     }
 #pragma unroll
     for (int q = 0; q < kGradChunk; ++q) {
@@ -135,11 +150,23 @@ __global__ __launch_bounds__(kGradThreads) void weight_gradient_kernel(
   const int lane = threadIdx.x & 63;
   if (r >= N) return;
   const int32_t e0 = rowptr[r], e1 = rowptr[r + 1];
-  for (int32_t e = e0 + lane; e < e1; e += 64) {
-    const int64_t c = col[e];
-    float sum = 0.0f;
-    for (int64_t b = 0; b < B; ++b) sum = __builtin_fmaf(gj[r * B + b], s.get(b, c), sum);
-    gw[e] = sum;
+  // kGradUnroll edges per lane per round: the round's column indices load
+  // together, then their state gathers, then the stores.
+  for (int32_t e = e0 + lane; e < e1; e += 64 * kGradUnroll) {
+    int64_t c[kGradUnroll];
+#pragma unroll
+    for (int u = 0; u < kGradUnroll; ++u) c[u] = col[min(e + 64 * u, e1 - 1)];
+    float sum[kGradUnroll];
+#pragma unroll
+    for (int u = 0; u < kGradUnroll; ++u) sum[u] = 0.0f;
+    for (int64_t b = 0; b < B; ++b) {
+      const float g = gj[r * B + b];
+#pragma unroll
+      for (int u = 0; u < kGradUnroll; ++u) sum[u] = __builtin_fmaf(g, s.get(b, c[u]), sum[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kGradUnroll; ++u)
+      if (e + 64 * u < e1) gw[e + 64 * u] = sum[u];
   }
 }
 
@@ -214,8 +241,8 @@ extern "C" int ns_dendritic_step_backward(const ns_step_grad_args* args, void* s
   advance_backward_kernel<<<per_neuron, kGradThreads, 0, s>>>(G);
   if (a.matrix.n_edges > 0) {
     transposed_product_kernel<<<per_row, kGradThreads, 0, s>>>(
-        a.out_rowptr, a.dst, a.out_weight_index, static_cast<const float*>(a.matrix.weight), gj,
-        n, batch, out_plane(a.d_state));
+        a.out_rowptr, a.dst, a.out_weight_index, static_cast<const float*>(a.matrix.weight),
+        a.out_weight, gj, n, batch, out_plane(a.d_state));
     if (a.d_weight)
       weight_gradient_kernel<<<per_row, kGradThreads, 0, s>>>(
           a.matrix.rowptr, a.matrix.col, gj, plane(a.state, a.state.data), n, batch, a.d_weight);

@@ -125,7 +125,8 @@ class _StepGradArgs(ctypes.Structure):
                 ("grad_state", _Plane), ("grad_dendrite", _Plane), ("grad_adaptation", _Plane),
                 ("d_state", _OutPlane), ("d_dendrite", _OutPlane), ("d_adaptation", _OutPlane),
                 ("d_drive", _OutPlane), ("d_dendritic_drive", _OutPlane),
-                ("d_weight", _c_ptr), ("d_params", _c_ptr * 6), ("workspace", _c_ptr)]
+                ("d_weight", _c_ptr), ("d_params", _c_ptr * 6), ("workspace", _c_ptr),
+                ("out_weight", _c_ptr)]
 
 
 class _EncodeArgs(ctypes.Structure):
@@ -772,12 +773,14 @@ class NativeExtension:
                                 weight, input, input_scalar, dendritic_input, dendritic_scalar,
                                 out_rowptr, dst, weight_index, grad_state, grad_dendrite,
                                 grad_adaptation, *, need_drive=False, need_dendritic=False,
-                                need_weight=False, need_params=(False,) * 6):
+                                need_weight=False, need_params=(False,) * 6, out_weight=None):
         """Gradients of one float32 tick (ns_dendritic_step_backward).
 
         Returns (d_state, d_dendrite, d_adaptation, d_drive, d_dendritic_drive,
         d_weight, [d_param x 6]); entries not asked for are None.  Upstream
-        gradients may be None (zero).
+        gradients may be None (zero).  ``out_weight`` optionally gives the
+        weights in source-major order (``weight[weight_index]``), which the
+        transposed product then streams instead of gathering.
         """
         _check_state(state)
         batch, n = state.shape
@@ -800,6 +803,11 @@ class NativeExtension:
             raise RuntimeError("invalid source-major topology geometry")
         args.out_rowptr, args.dst = out_rowptr.data_ptr(), dst.data_ptr()
         args.out_weight_index = weight_index.data_ptr()
+        if out_weight is not None:
+            _check_float(out_weight, state, "source-major weights")
+            if out_weight.numel() != weight.numel() or not out_weight.is_contiguous():
+                raise RuntimeError("source-major weights must be a contiguous [M] vector")
+            args.out_weight = out_weight.data_ptr() if out_weight.numel() else None
         args.grad_state = _drive(grad_state, 0.0, state)
         args.grad_dendrite = _drive(grad_dendrite, 0.0, state)
         args.grad_adaptation = _drive(grad_adaptation, 0.0, state)

@@ -72,6 +72,37 @@ class _NativeCompartments:
                                        topology.in_weight.detach())
 
 
+class SourceMajorWeights:
+    """Source-major copy of the CSR weights for the backward's transposed product.
+
+    The transposed product walks out-edges; reading CSR-order weights there is
+    one random gather per edge.  Backpropagation through several ticks reuses
+    one weight version, so the copy (one gather) is built on the second
+    backward that sees a version and then streamed; a single backward keeps the
+    direct gather.  A version is (storage, in-place version counter, size), so
+    an optimizer step on the weights invalidates the copy.  ``enabled`` turns
+    the copy off.
+    """
+
+    def __init__(self) -> None:
+        self.enabled = True
+        self._key = None
+        self._seen = 0
+        self._values: torch.Tensor | None = None
+
+    def get(self, weight: torch.Tensor, out_weight_index: torch.Tensor) -> torch.Tensor | None:
+        if not self.enabled:
+            return None
+        key = (weight.data_ptr(), weight._version, weight.numel())
+        if key != self._key:
+            self._key, self._seen, self._values = key, 0, None
+        self._seen += 1
+        if self._seen >= 2 and self._values is None:
+            with torch.no_grad():
+                self._values = torch.index_select(weight.detach(), 0, out_weight_index)
+        return self._values
+
+
 class _NativeTick(torch.autograd.Function):
     """One float32 fused tick (ns_dendritic_step) whose backward is native too
     (ns_dendritic_step_backward): gradients of the states, tensor drives, the
@@ -80,7 +111,7 @@ class _NativeTick(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, info, state, dendrite, adaptation, weight, drive, dendritic_drive, *params):
-        extension, topology, us, vs, width, extra = info
+        extension, topology, us, vs, width, extra, _ = info
         outs = extension.dendritic_step(state, dendrite, adaptation, list(params),
                                         topology.in_rowptr, topology.in_col, weight,
                                         drive, us, dendritic_drive, vs, width, **extra)
@@ -94,7 +125,7 @@ class _NativeTick(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_state, grad_dendrite, grad_adaptation):
-        extension, topology, us, vs, _, _ = ctx.info
+        extension, topology, us, vs, _, _, source_major = ctx.info
         saved = list(ctx.saved_tensors)
         state, dendrite, adaptation, weight = saved[:4]
         params = saved[4:10]
@@ -108,7 +139,8 @@ class _NativeTick(torch.autograd.Function):
             drive, us, dendritic_drive, vs, topology.out_rowptr, topology.dst,
             topology.out_weight_index, grad_state, grad_dendrite, grad_adaptation,
             need_drive=bool(needs[5]), need_dendritic=bool(needs[6]), need_weight=bool(needs[4]),
-            need_params=tuple(bool(x) for x in needs[7:13]))
+            need_params=tuple(bool(x) for x in needs[7:13]),
+            out_weight=source_major.get(weight, topology.out_weight_index))
         return (None, d_state if needs[1] else None, d_dendrite if needs[2] else None,
                 d_adaptation if needs[3] else None, d_weight, d_drive, d_dendritic, *d_params)
 
@@ -192,6 +224,7 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
                                     tiles_per_panel=panel_tiles, max_panel_width=panel_width,
                                     pairs=panel_pairs)
                         if use_panels else None)
+        self.source_major_weights = SourceMajorWeights()
         self._bands = (BandLayout(topology, initial_state.device,
                                   band_width=band_width or BAND_WIDTH, block_rows=band_rows,
                                   block_steps=band_steps)
@@ -295,7 +328,8 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         weight = self.topology.in_weight
         # The row kernel reads in_weight itself on every tick, so weights an
         # optimizer updates in place are never served from a slot-order copy.
-        info = (self.extension, self.topology, us, vs, self.threads_per_row, {})
+        info = (self.extension, self.topology, us, vs, self.threads_per_row, {},
+                self.source_major_weights)
         self.state, self.dendritic_state, self.adaptation_state = _NativeTick.apply(
             info, self.state, self.dendritic_state, self.adaptation_state, weight, u, v,
             *self._parameters())

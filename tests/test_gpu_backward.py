@@ -10,7 +10,8 @@ the tolerance (1e-4 of the largest gradient of each tensor) covers only the
 native float32 arithmetic.  Covers one tick with every input requiring a
 gradient (states, [B,N] and [B,1] drives, the six parameters, the weights),
 eight-tick backpropagation through time, scalar drives, stride-0 parameters,
-and repeatability.
+repeatability, and the source-major weight copy the transposed product streams
+from the second backward of a weight version on.
 """
 
 from __future__ import annotations
@@ -63,12 +64,15 @@ def base(p):
     return p._base if p._base is not None else p
 
 
-def run(runtime_cls, g, inputs, dtype, device, ticks, *, scalar_drives, expanded, **kw):
+def run(runtime_cls, g, inputs, dtype, device, ticks, *, scalar_drives, expanded,
+        source_major=True, **kw):
     topo = topology(g, dtype, device)
     topo.in_weight.requires_grad_(True)
     mdl = model(inputs["params"], dtype, device, expanded)
     state0 = leaf(inputs["state"], dtype, device)
     rt = runtime_cls(topo, mdl, state0.detach(), **kw)
+    if hasattr(rt, "source_major_weights"):
+        rt.source_major_weights.enabled = source_major
     rt.state = state0
     rt.dendritic_state = leaf(inputs["dendrite"], dtype, device)
     rt.adaptation_state = leaf(inputs["adaptation"], dtype, device)
@@ -143,6 +147,24 @@ def test_backward_is_repeatable(gpu):
                     scalar_drives=False, expanded=False)
     for name in first:
         assert torch.equal(first[name], second[name]), name
+
+
+def test_source_major_weight_copy_changes_no_gradient(gpu):
+    """Backpropagation through 6 ticks: from the second backward on, the transposed
+    product streams a source-major copy of the weights instead of gathering them;
+    the gradients are bitwise those of the gather."""
+    print("case backward source-major weights", flush=True)
+    g = graph(3000, 90_000, 12)
+    inputs = inputs_for(g, 2, 21)
+    kw = dict(scalar_drives=False, expanded=False)
+    copied, rt = run(NativeDendriticMatrixRuntime, g, inputs, torch.float32, gpu, 6, **kw)
+    assert rt.source_major_weights._values is not None, "the copy was built"
+    assert rt.source_major_weights._seen == 6
+    gathered, rt2 = run(NativeDendriticMatrixRuntime, g, inputs, torch.float32, gpu, 6,
+                        source_major=False, **kw)
+    assert rt2.source_major_weights._values is None
+    for name in copied:
+        assert torch.equal(copied[name], gathered[name]), name
 
 
 def test_forward_of_a_recorded_tick_equals_the_inference_tick(gpu):
