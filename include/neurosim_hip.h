@@ -197,6 +197,8 @@ typedef struct ns_step_args {
   ns_out_plane out_state;      /* s_{t+1}; must not overlap any input */
   ns_out_plane out_dendrite;   /* d_{t+1} */
   ns_out_plane out_adaptation; /* a_{t+1} */
+  ns_out_plane out_current;    /* optional: j = W @ s_t as well (data NULL: not written);
+                                  a recorded tick keeps it for its backward */
 } ns_step_args;
 
 /* Arguments of one PELS event tick (advance + emit, then scatter). */
@@ -258,6 +260,9 @@ typedef struct ns_step_grad_args {
   float* d_weight;             /* [M] in CSR order; NULL: not computed */
   float* d_params[6];          /* [N] each, per neuron; NULL: not computed */
   float* workspace;            /* ns_step_backward_workspace_floats(N, B) floats */
+  const float* current;        /* optional [N*B]: j = W @ s of the forward, neuron-major
+                                  (j[n*B + b]), as ns_dendritic_step's out_current wrote
+                                  it; NULL: recomputed from the CSR */
   const float* out_weight;     /* optional [M]: the CSR weights in source-major order,
                                   out_weight[e] == matrix.weight[out_weight_index[e]];
                                   when set, the transposed product streams it instead of

@@ -52,6 +52,7 @@ struct BandArgs {
   const uint8_t* slot_scales;
   const float* gscale;
   OutPlane os, od, oa;
+  OutPlane oj;   // optional: j as well (data null: not written)
 };
 
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -211,6 +212,7 @@ __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) 
     A.os.put(b, n, x.soma);
     A.od.put(b, n, x.dendrite);
     A.oa.put(b, n, x.adaptation);
+    if (A.oj.data) A.oj.put(b, n, sums[i]);
   }
 }
 
@@ -287,7 +289,7 @@ int band_step(const ns_step_args& a, const ns_band_plan& pl, hipStream_t stream)
   A.wave_blocks = pl.wave_blocks; A.blocks = pl.blocks; A.rows = pl.rows; A.col = pl.col;
   A.weight = pl.weight; A.slot_scales = pl.slot_scales; A.gscale = a.matrix.global_scale;
   A.os = out_plane(a.out_state); A.od = out_plane(a.out_dendrite);
-  A.oa = out_plane(a.out_adaptation);
+  A.oa = out_plane(a.out_adaptation); A.oj = out_plane(a.out_current);
   static const hipError_t lds_ok = [] {
     hipError_t e = allow_band_lds<2>();
     if (e == hipSuccess) e = allow_band_lds<4>();

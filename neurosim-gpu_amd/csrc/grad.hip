@@ -200,27 +200,32 @@ extern "C" int ns_dendritic_step_backward(const ns_step_grad_args* args, void* s
   const Extent outs[5] = {extent(a.d_state, batch, n), extent(a.d_dendrite, batch, n),
                           extent(a.d_adaptation, batch, n), extent(a.d_drive, batch, n),
                           extent(a.d_dendritic_drive, batch, n)};
-  const Extent ins[8] = {extent(a.state, batch, n), extent(a.dendrite, batch, n),
+  const Extent ins[9] = {extent(a.state, batch, n), extent(a.dendrite, batch, n),
                          extent(a.adaptation, batch, n), extent(a.drive, batch, n),
                          extent(a.dendritic_drive, batch, n), extent(a.grad_state, batch, n),
-                         extent(a.grad_dendrite, batch, n), extent(a.grad_adaptation, batch, n)};
+                         extent(a.grad_dendrite, batch, n), extent(a.grad_adaptation, batch, n),
+                         extent_of(a.current, 1, 1, 1, batch * n)};
   const Extent work = extent_of(a.workspace, 1, 1, 1, 2 * batch * n);
+  if (overlaps(ins[8], work)) return fail("the forward's current must not overlap the workspace");
   for (int o = 0; o < 5; ++o) {
     if (overlaps(outs[o], work)) return fail("gradient planes must not overlap the workspace");
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < 9; ++i)
       if (overlaps(outs[o], ins[i])) return fail("gradient planes must not overlap inputs");
     for (int p = o + 1; p < 5; ++p)
       if (overlaps(outs[o], outs[p])) return fail("gradient planes must not overlap each other");
   }
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  float* j = a.workspace;
   float* gj = a.workspace + batch * n;
 
-  // j = W @ s, neuron-major.
-  ns_spmm_args prod{};
-  prod.n_neurons = n; prod.batch = batch; prod.source = a.state; prod.matrix = a.matrix;
-  prod.plan = a.plan; prod.out = ns_out_plane{j, 1, batch};
-  if (int rc = ns_csr_spmm(&prod, stream)) return rc;
+  // j = W @ s, neuron-major: the forward's, or recomputed into the workspace.
+  const float* j = a.current;
+  if (!j) {
+    ns_spmm_args prod{};
+    prod.n_neurons = n; prod.batch = batch; prod.source = a.state; prod.matrix = a.matrix;
+    prod.plan = a.plan; prod.out = ns_out_plane{a.workspace, 1, batch};
+    if (int rc = ns_csr_spmm(&prod, stream)) return rc;
+    j = a.workspace;
+  }
 
   GradArgs G{};
   G.N = n; G.B = batch;

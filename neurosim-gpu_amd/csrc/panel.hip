@@ -76,6 +76,7 @@ struct PanelArgs {
   float* sorted;     // [rows-table entries][BT]: row sums in row-table order
   float* partials;   // [n_panels][N][BT]: row sums by row (several panels)
   OutPlane os, od, oa;
+  OutPlane oj;       // optional: j as well (data null: not written)
   int32_t s_vec;   // s.sn == 1 (B == 1) or neuron-major B == 2, 16-byte aligned
 };
 
@@ -183,6 +184,7 @@ __device__ __forceinline__ void update(const PanelArgs& A, int64_t n, int64_t b,
   A.os.put(b, n, x.soma);
   A.od.put(b, n, x.dendrite);
   A.oa.put(b, n, x.adaptation);
+  if (A.oj.data) A.oj.put(b, n, j);
 }
 
 // A group descriptor held in scalar registers.
@@ -425,6 +427,7 @@ __global__ __launch_bounds__(kThreads) void panel_combine_kernel(PanelArgs A) {
     A.os.put(j, n, x.soma);
     A.od.put(j, n, x.dendrite);
     A.oa.put(j, n, x.adaptation);
+    if (A.oj.data) A.oj.put(j, n, sum[j]);
   }
 }
 
@@ -507,7 +510,7 @@ int panel_step(const ns_step_args& a, hipStream_t stream) {
   A.partials = pl.partials;
   A.sorted = pl.partials + int64_t{pl.n_panels} * a.n_neurons * a.batch;
   A.os = out_plane(a.out_state); A.od = out_plane(a.out_dendrite);
-  A.oa = out_plane(a.out_adaptation);
+  A.oa = out_plane(a.out_adaptation); A.oj = out_plane(a.out_current);
   const bool aligned = reinterpret_cast<uintptr_t>(a.state.data) % 16 == 0;
   A.s_vec = aligned && ((a.batch == 1 && a.state.stride_n == 1) ||
                         (a.batch == 2 && a.state.stride_b == 1 && a.state.stride_n == 2));

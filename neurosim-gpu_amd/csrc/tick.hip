@@ -62,6 +62,7 @@ struct TickArgs {
   const int32_t* bounds;
   int64_t n_blocks;
   OutPlane os, od, oa;
+  OutPlane oj;          // optional: j as well (data null: not written)
   int32_t quad_loads;   // col/weight pointers aligned for one-quad vector loads
   int32_t s_vec4;       // s is neuron-major with 16-byte aligned column groups
   int32_t spmm_only;    // write j to `os` instead of advancing
@@ -147,6 +148,7 @@ __device__ __forceinline__ void finish(const TickArgs& A, int64_t n, int64_t b, 
   A.os.put(b, n, x.soma);
   A.od.put(b, n, x.dendrite);
   A.oa.put(b, n, x.adaptation);
+  if (A.oj.data) A.oj.put(b, n, j);
 }
 
 // Rows of a block that does not fit the LDS path: the whole workgroup reduces
@@ -332,6 +334,7 @@ __global__ __launch_bounds__(kThreads) void tick_kernel(TickArgs A) {
         A.os.put(b0 + j, n, x.soma);
         A.od.put(b0 + j, n, x.dendrite);
         A.oa.put(b0 + j, n, x.adaptation);
+        if (A.oj.data) A.oj.put(b0 + j, n, acc);
       }
     }
   }
@@ -465,18 +468,19 @@ int check_step_planes(const ns_step_args& a) {
     return fail("state, dendrite and adaptation data are required");
   if (!a.out_state.data || !a.out_dendrite.data || !a.out_adaptation.data)
     return fail("three output planes are required");
-  const Extent outs[3] = {extent(a.out_state, a.batch, a.n_neurons),
+  const Extent outs[4] = {extent(a.out_state, a.batch, a.n_neurons),
                           extent(a.out_dendrite, a.batch, a.n_neurons),
-                          extent(a.out_adaptation, a.batch, a.n_neurons)};
+                          extent(a.out_adaptation, a.batch, a.n_neurons),
+                          extent(a.out_current, a.batch, a.n_neurons)};
   const Extent ins[5] = {extent(a.state, a.batch, a.n_neurons),
                          extent(a.dendrite, a.batch, a.n_neurons),
                          extent(a.adaptation, a.batch, a.n_neurons),
                          extent(a.drive, a.batch, a.n_neurons),
                          extent(a.dendritic_drive, a.batch, a.n_neurons)};
-  for (int o = 0; o < 3; ++o) {
+  for (int o = 0; o < 4; ++o) {
     for (int i = 0; i < 5; ++i)
       if (overlaps(outs[o], ins[i])) return fail("output planes must not overlap inputs");
-    for (int p = o + 1; p < 3; ++p)
+    for (int p = o + 1; p < 4; ++p)
       if (overlaps(outs[o], outs[p])) return fail("output planes must not overlap each other");
   }
   return NS_OK;
@@ -505,7 +509,7 @@ extern "C" int ns_dendritic_step(const ns_step_args* args, void* stream) {
   A.scales = a.matrix.block_scales; A.gscale = a.matrix.global_scale;
   A.bounds = a.plan.bounds; A.n_blocks = a.plan.n_blocks;
   A.os = out_plane(a.out_state); A.od = out_plane(a.out_dendrite);
-  A.oa = out_plane(a.out_adaptation);
+  A.oa = out_plane(a.out_adaptation); A.oj = out_plane(a.out_current);
   A.quad_loads = quad_aligned(a.matrix);
   A.s_vec4 = neuron_major_vec4(a.state, a.batch);
   A.spmm_only = 0;

@@ -94,7 +94,7 @@ class _StepArgs(ctypes.Structure):
                 ("params", _Vector * 6), ("matrix", _Csr), ("plan", _RowPlan),
                 ("panels", _c_ptr),
                 ("out_state", _OutPlane), ("out_dendrite", _OutPlane),
-                ("out_adaptation", _OutPlane)]
+                ("out_adaptation", _OutPlane), ("out_current", _OutPlane)]
 
 
 class _EventArgs(ctypes.Structure):
@@ -126,7 +126,7 @@ class _StepGradArgs(ctypes.Structure):
                 ("d_state", _OutPlane), ("d_dendrite", _OutPlane), ("d_adaptation", _OutPlane),
                 ("d_drive", _OutPlane), ("d_dendritic_drive", _OutPlane),
                 ("d_weight", _c_ptr), ("d_params", _c_ptr * 6), ("workspace", _c_ptr),
-                ("out_weight", _c_ptr)]
+                ("current", _c_ptr), ("out_weight", _c_ptr)]
 
 
 class _EncodeArgs(ctypes.Structure):
@@ -686,7 +686,8 @@ class NativeExtension:
     # -- ops ----------------------------------------------------------------
     def dendritic_step(self, state, dendrite, adaptation, params, rowptr, source, weight,
                        input, input_scalar, dendritic_input, dendritic_scalar, width,
-                       block_scales=None, global_scale=None, panels=None, bands=None):
+                       block_scales=None, global_scale=None, panels=None, bands=None,
+                       current_out=None):
         _check_state(state)
         args = _StepArgs()
         args.state = _plane(state, state, "state")
@@ -716,6 +717,11 @@ class NativeExtension:
             args.plan = self.plan_for(rowptr, batch)
         outs = new_planes(3, batch, n, state)
         args.out_state, args.out_dendrite, args.out_adaptation = (_out(o) for o in outs)
+        if current_out is not None:        # j = W @ s as well, for a recorded tick's backward
+            _check_float(current_out, state, "current")
+            if current_out.shape != state.shape:
+                raise RuntimeError("state/current shape mismatch")
+            args.out_current = _out(current_out)
         stream = torch.cuda.current_stream(state.device).cuda_stream
         if bands is not None:
             _raise_on(self.lib.ns_dendritic_step_bands(ctypes.byref(args), ctypes.byref(bands),
@@ -773,14 +779,17 @@ class NativeExtension:
                                 weight, input, input_scalar, dendritic_input, dendritic_scalar,
                                 out_rowptr, dst, weight_index, grad_state, grad_dendrite,
                                 grad_adaptation, *, need_drive=False, need_dendritic=False,
-                                need_weight=False, need_params=(False,) * 6, out_weight=None):
+                                need_weight=False, need_params=(False,) * 6, out_weight=None,
+                                current=None):
         """Gradients of one float32 tick (ns_dendritic_step_backward).
 
         Returns (d_state, d_dendrite, d_adaptation, d_drive, d_dendritic_drive,
         d_weight, [d_param x 6]); entries not asked for are None.  Upstream
         gradients may be None (zero).  ``out_weight`` optionally gives the
         weights in source-major order (``weight[weight_index]``), which the
-        transposed product then streams instead of gathering.
+        transposed product then streams instead of gathering.  ``current``
+        optionally gives the forward's j = W @ s as ``dendritic_step`` wrote it
+        (``current_out``, a neuron-major [B,N] plane), which spares recomputing it.
         """
         _check_state(state)
         batch, n = state.shape
@@ -808,6 +817,11 @@ class NativeExtension:
             if out_weight.numel() != weight.numel() or not out_weight.is_contiguous():
                 raise RuntimeError("source-major weights must be a contiguous [M] vector")
             args.out_weight = out_weight.data_ptr() if out_weight.numel() else None
+        if current is not None:
+            _check_float(current, state, "current")
+            if current.shape != state.shape or current.stride() != (1, batch):
+                raise RuntimeError("current must be a neuron-major [B,N] plane")
+            args.current = current.data_ptr()
         args.grad_state = _drive(grad_state, 0.0, state)
         args.grad_dendrite = _drive(grad_dendrite, 0.0, state)
         args.grad_adaptation = _drive(grad_adaptation, 0.0, state)

@@ -24,7 +24,8 @@ from __future__ import annotations
 import torch
 
 from .compartmental import DendriticDynamics, DendriticMatrixRuntime, DendriticPELSRuntime
-from .native import BAND_WIDTH, BandLayout, NativeExtension, PanelLayout, encode_weights, load_native_extension
+from .native import (BAND_WIDTH, BandLayout, NativeExtension, PanelLayout, encode_weights,
+                     load_native_extension, new_planes)
 from .topology import SparseTopology
 
 
@@ -112,9 +113,13 @@ class _NativeTick(torch.autograd.Function):
     @staticmethod
     def forward(ctx, info, state, dendrite, adaptation, weight, drive, dendritic_drive, *params):
         extension, topology, us, vs, width, extra, _ = info
+        # j = W @ s kept for the backward, which then needs no product of its own
+        current = new_planes(1, state.shape[0], state.shape[1], state)[0]
         outs = extension.dendritic_step(state, dendrite, adaptation, list(params),
                                         topology.in_rowptr, topology.in_col, weight,
-                                        drive, us, dendritic_drive, vs, width, **extra)
+                                        drive, us, dendritic_drive, vs, width, **extra,
+                                        current_out=current)
+        ctx.current = current
         ctx.info = info
         ctx.has_drive = (drive is not None, dendritic_drive is not None)
         saved = [state, dendrite, adaptation, weight, *params]
@@ -140,7 +145,8 @@ class _NativeTick(torch.autograd.Function):
             topology.out_weight_index, grad_state, grad_dendrite, grad_adaptation,
             need_drive=bool(needs[5]), need_dendritic=bool(needs[6]), need_weight=bool(needs[4]),
             need_params=tuple(bool(x) for x in needs[7:13]),
-            out_weight=source_major.get(weight, topology.out_weight_index))
+            out_weight=source_major.get(weight, topology.out_weight_index), current=ctx.current)
+        ctx.current = None
         return (None, d_state if needs[1] else None, d_dendrite if needs[2] else None,
                 d_adaptation if needs[3] else None, d_weight, d_drive, d_dendritic, *d_params)
 
