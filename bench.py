@@ -260,12 +260,13 @@ def measure_backward(topology, model, repeats: int = 10) -> dict:
     sum of the new state): the native backward against autograd through the
     torch step that the reference runs for such ticks, each timed with HIP
     events over ``repeats`` forward+backward passes.  The weights do not
-    change between passes, so from the second backward on the native
-    transposed product streams a source-major copy of them (one gather per
-    weight version); ``native_changing_weights_ms`` times the native pass with
-    that copy off, as when an optimizer updates the weights every tick, and
-    ``native_bptt8_ms_per_tick`` eight recorded ticks and one backward through
-    them, per tick."""
+    change between passes, so from the second pass on the native forward runs
+    on panels over a slot-order copy of them and the transposed product streams
+    a source-major copy (each built once per weight version).
+    ``native_changing_weights_ms`` marks the weights modified before every pass
+    (a new version, as after an optimizer step, values unchanged), so neither
+    copy is reused; ``native_bptt8_ms_per_tick`` times eight recorded ticks and
+    one backward through them, per tick."""
     from neurosim_gpu import DendriticMatrixRuntime
 
     n = topology.n_neurons
@@ -277,17 +278,17 @@ def measure_backward(topology, model, repeats: int = 10) -> dict:
     dyn = DendriticDynamics(Dynamics(params[0], params[1]), *params[2:])
     out = {"workload": f"one fp32 tick + backward, N={n} M={topology.n_edges} B=1, gradients of "
                        "the weights, the six parameters and the state", "repeats": repeats}
-    runs = (("native", NativeDendriticMatrixRuntime, 1, True),
-            ("native_changing_weights", NativeDendriticMatrixRuntime, 1, False),
-            ("native_bptt8", NativeDendriticMatrixRuntime, 8, True),
-            ("torch_autograd", DendriticMatrixRuntime, 1, True))
-    for name, cls, ticks, copy in runs:
+    runs = (("native", NativeDendriticMatrixRuntime, 1, False),
+            ("native_changing_weights", NativeDendriticMatrixRuntime, 1, True),
+            ("native_bptt8", NativeDendriticMatrixRuntime, 8, False),
+            ("torch_autograd", DendriticMatrixRuntime, 1, False))
+    for name, cls, ticks, new_version in runs:
         state = torch.full((1, n), 0.2, device=weight.device)
         runtime = cls(trained, dyn, state)
-        if hasattr(runtime, "source_major_weights"):
-            runtime.source_major_weights.enabled = copy
 
         def once():
+            if new_version:
+                torch.autograd.graph.increment_version(weight)
             runtime.state = state.clone().requires_grad_(True)
             runtime.dendritic_state = torch.zeros_like(state)
             runtime.adaptation_state = torch.zeros_like(state)

@@ -231,6 +231,7 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
                                     pairs=panel_pairs)
                         if use_panels else None)
         self.source_major_weights = SourceMajorWeights()
+        self._recorded_key, self._recorded_seen = None, 0
         self._bands = (BandLayout(topology, initial_state.device,
                                   band_width=band_width or BAND_WIDTH, block_rows=band_rows,
                                   block_steps=band_steps)
@@ -241,6 +242,30 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         self._packed_weight_version = -1
         self._panel_struct = None
         self._panel_struct_key = None
+
+    def _recorded_panel_plan(self, weight: torch.Tensor):
+        """Panel plan for a tick recorded for autograd, or None for the row kernel.
+
+        The row kernel reads ``weight`` (CSR order) itself, so a weight version
+        seen once (an optimizer step every tick) costs no slot-order copy.  From
+        the second recorded tick of one version on (backpropagation through
+        time, repeated evaluation) the panel kernel runs on a slot-order copy of
+        that version, built once.  A version is (storage, in-place version
+        counter), so an in-place update of the weights is never missed.
+        """
+        if self._panels is None:
+            return None
+        key = ("recorded", weight.data_ptr(), weight._version)
+        if key != self._recorded_key:
+            self._recorded_key, self._recorded_seen = key, 0
+        self._recorded_seen += 1
+        if self._recorded_seen < 2:
+            return None
+        if self._panel_struct_key != key:
+            slots, slot_scales = self._panels.slot_weights(key, weight.detach(), None)
+            self._panel_struct = self._panels.plan_struct(slots, slot_scales)
+            self._panel_struct_key = key
+        return self._panel_struct
 
     def _band_plan(self, weight: torch.Tensor, scales: tuple):
         """ctypes band plan for this tick's weights (rebuilt when the weights change)."""
@@ -332,9 +357,11 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         u, us = self._drive(drive)
         v, vs = self._drive(dendritic_drive)
         weight = self.topology.in_weight
-        # The row kernel reads in_weight itself on every tick, so weights an
-        # optimizer updates in place are never served from a slot-order copy.
-        info = (self.extension, self.topology, us, vs, self.threads_per_row, {},
+        extra = {}
+        plan = self._recorded_panel_plan(weight)
+        if plan is not None:
+            extra["panels"] = plan
+        info = (self.extension, self.topology, us, vs, self.threads_per_row, extra,
                 self.source_major_weights)
         self.state, self.dendritic_state, self.adaptation_state = _NativeTick.apply(
             info, self.state, self.dendritic_state, self.adaptation_state, weight, u, v,

@@ -167,6 +167,36 @@ def test_source_major_weight_copy_changes_no_gradient(gpu):
         assert torch.equal(copied[name], gathered[name]), name
 
 
+def test_recorded_ticks_move_to_panels_for_a_reused_weight_version(gpu):
+    """A recorded tick takes the row kernel the first time it sees a weight
+    version and the panel kernel from the second on; an in-place weight update
+    sends it back to the row kernel.  The states follow the inference ticks
+    (panels) to float32 summation-order differences."""
+    print("case backward recorded panel ticks", flush=True)
+    g = graph(4000, 100_000, 6)
+    topo = topology(g, torch.float32, gpu)
+    topo.in_weight.requires_grad_(True)
+    soma = Dynamics(torch.full((4000,), .72, device=gpu), torch.full((4000,), .8, device=gpu))
+    mdl = DendriticDynamics.from_time_constants(soma, dt=1., tau_dendrite=4., tau_adaptation=25.)
+    plain = NativeDendriticMatrixRuntime(topo, mdl, torch.zeros(1, 4000, device=gpu))
+    recorded = NativeDendriticMatrixRuntime(topo, mdl, torch.zeros(1, 4000, device=gpu))
+    assert recorded.kernel == "panels"
+    for tick in range(5):
+        with torch.no_grad():
+            plain.step(0.2, dendritic_drive=0.1)
+        recorded.step(0.2, dendritic_drive=0.1)
+        assert (recorded._panel_struct_key is not None) == (tick >= 1)
+    for name in ("state", "dendritic_state", "adaptation_state"):
+        err = float((getattr(recorded, name) - getattr(plain, name)).abs().max())
+        assert err <= 2e-6, (name, err)
+    recorded.state.sum().backward()
+    assert topo.in_weight.grad is not None and bool(torch.isfinite(topo.in_weight.grad).all())
+    with torch.no_grad():
+        topo.in_weight.mul_(0.5)                 # a new weight version: rows again, once
+    recorded.step(0.2, dendritic_drive=0.1)
+    assert recorded._recorded_seen == 1
+
+
 def test_forward_of_a_recorded_tick_equals_the_inference_tick(gpu):
     """Recording for autograd changes nothing in the forward values."""
     print("case backward forward values", flush=True)
