@@ -73,6 +73,15 @@ class _NativeCompartments:
                                        topology.in_weight.detach())
 
 
+def _weight_key(weight: torch.Tensor) -> tuple:
+    """Identity and in-place version of a weight tensor, for caches derived from
+    it.  A cache that stores this key also holds the tensor, so the identity
+    cannot pass to another tensor while the cache refers to it.  A tensor made
+    under torch.inference_mode has no version counter (PyTorch tracks none for
+    them); its key is its identity alone."""
+    return (id(weight), None if torch.is_inference(weight) else weight._version)
+
+
 class SourceMajorWeights:
     """Source-major copy of the CSR weights for the backward's transposed product.
 
@@ -80,23 +89,24 @@ class SourceMajorWeights:
     one random gather per edge.  Backpropagation through several ticks reuses
     one weight version, so the copy (one gather) is built on the second
     backward that sees a version and then streamed; a single backward keeps the
-    direct gather.  A version is (storage, in-place version counter, size), so
-    an optimizer step on the weights invalidates the copy.  ``enabled`` turns
-    the copy off.
+    direct gather.  A version is (tensor, in-place version counter), so an
+    optimizer step on the weights, in place or into a new tensor, invalidates
+    the copy.  ``enabled`` turns the copy off.
     """
 
     def __init__(self) -> None:
         self.enabled = True
         self._key = None
+        self._source: torch.Tensor | None = None
         self._seen = 0
         self._values: torch.Tensor | None = None
 
     def get(self, weight: torch.Tensor, out_weight_index: torch.Tensor) -> torch.Tensor | None:
         if not self.enabled:
             return None
-        key = (weight.data_ptr(), weight._version, weight.numel())
-        if key != self._key:
-            self._key, self._seen, self._values = key, 0, None
+        key = _weight_key(weight)
+        if key != self._key or self._source is not weight:
+            self._key, self._source, self._seen, self._values = key, weight, 0, None
         self._seen += 1
         if self._seen >= 2 and self._values is None:
             with torch.no_grad():
@@ -231,7 +241,7 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
                                     pairs=panel_pairs)
                         if use_panels else None)
         self.source_major_weights = SourceMajorWeights()
-        self._recorded_key, self._recorded_seen = None, 0
+        self._recorded_key, self._recorded_source, self._recorded_seen = None, None, 0
         self._bands = (BandLayout(topology, initial_state.device,
                                   band_width=band_width or BAND_WIDTH, block_rows=band_rows,
                                   block_steps=band_steps)
@@ -242,6 +252,7 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         self._packed_weight_version = -1
         self._panel_struct = None
         self._panel_struct_key = None
+        self._panel_struct_source = None
 
     def _recorded_panel_plan(self, weight: torch.Tensor):
         """Panel plan for a tick recorded for autograd, or None for the row kernel.
@@ -250,42 +261,42 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         seen once (an optimizer step every tick) costs no slot-order copy.  From
         the second recorded tick of one version on (backpropagation through
         time, repeated evaluation) the panel kernel runs on a slot-order copy of
-        that version, built once.  A version is (storage, in-place version
-        counter), so an in-place update of the weights is never missed.
+        that version, built once.  A version is (tensor, in-place version
+        counter), so an update of the weights is never missed.
         """
         if self._panels is None:
             return None
-        key = ("recorded", weight.data_ptr(), weight._version)
-        if key != self._recorded_key:
-            self._recorded_key, self._recorded_seen = key, 0
+        key = ("recorded",) + _weight_key(weight)
+        if key != self._recorded_key or self._recorded_source is not weight:
+            self._recorded_key, self._recorded_source, self._recorded_seen = key, weight, 0
         self._recorded_seen += 1
         if self._recorded_seen < 2:
             return None
+        return self._slot_plan(self._panels, key, weight.detach(), ())
+
+    def _slot_plan(self, layout, key: tuple, weight: torch.Tensor, scales: tuple):
+        """ctypes plan of ``layout`` over ``weight`` in slot order, rebuilt when
+        ``key`` changes.  The weight payload is held with the plan, so the
+        identity in the key stays its own."""
         if self._panel_struct_key != key:
-            slots, slot_scales = self._panels.slot_weights(key, weight.detach(), None)
-            self._panel_struct = self._panels.plan_struct(slots, slot_scales)
+            block = scales[0] if len(scales) == 2 else None
+            slots, slot_scales = layout.slot_weights(key, weight, block)
+            self._panel_struct = layout.plan_struct(slots, slot_scales)
             self._panel_struct_key = key
+            self._panel_struct_source = weight
         return self._panel_struct
 
     def _band_plan(self, weight: torch.Tensor, scales: tuple):
         """ctypes band plan for this tick's weights (rebuilt when the weights change)."""
-        key = (self.topology.weight_version, self.checkpoint_precision, weight.data_ptr())
-        if self._panel_struct_key != key:
-            block = scales[0] if len(scales) == 2 else None
-            slots, slot_scales = self._bands.slot_weights(key, weight, block)
-            self._panel_struct = self._bands.plan_struct(slots, slot_scales)
-            self._panel_struct_key = key
-        return self._panel_struct
+        key = (self.topology.weight_version, self.checkpoint_precision) + _weight_key(weight)
+        return self._slot_plan(self._bands, key, weight, scales)
 
     def _panel_plan(self, weight: torch.Tensor, scales: tuple):
-        """ctypes panel plan for this tick's weights (rebuilt when the weights change)."""
-        key = (self.topology.weight_version, self.checkpoint_precision, weight.data_ptr())
-        if self._panel_struct_key != key:
-            block = scales[0] if len(scales) == 2 else None
-            slots, slot_scales = self._panels.slot_weights(key, weight, block)
-            self._panel_struct = self._panels.plan_struct(slots, slot_scales)
-            self._panel_struct_key = key
-        return self._panel_struct
+        """ctypes panel plan for this tick's weights (rebuilt when the weights
+        change: a new topology weight version, or the payload replaced or
+        modified in place)."""
+        key = (self.topology.weight_version, self.checkpoint_precision) + _weight_key(weight)
+        return self._slot_plan(self._panels, key, weight, scales)
 
     @property
     def checkpoint_precision(self) -> str:

@@ -137,6 +137,25 @@ def test_nvfp4_pair_layout_is_the_default_and_matches_per_slot_scales(gpu, batch
     assert errors(runs[None], oracle) <= 1e-5
 
 
+def test_panel_fp32_follows_in_place_edits_of_in_weight(gpu):
+    """The reference's fp32 tick reads in_weight on every tick, so an in-place edit
+    of in_weight (no topology weight version bump) takes effect at once; the
+    panel path's slot-order copy is keyed on the tensor's version counter."""
+    case = make_case(3000, 60_000, 4, gpu)
+    native = NativeDendriticMatrixRuntime(case.topology, case.model, torch.zeros(1, 3000, device=gpu),
+                                          kernel="panels", panel_width=512, panel_tiles=4)
+    oracle = ort.MatrixOracle(case.graph, case.params, torch.zeros(1, 3000))
+    for tick in range(8):
+        if tick == 4:
+            with torch.no_grad():
+                case.topology.in_weight.mul_(0.5)
+            oracle.matrix = ort.csr_matrix(case.graph, torch.float32,
+                                           case.topology.in_weight.cpu().numpy())
+        native.step(0.2, dendritic_drive=0.1)
+        oracle.step(0.2, 0.1)
+    assert errors(native, oracle) <= 1e-5
+
+
 def test_panel_weight_refresh_after_mutation(gpu):
     case = make_case(3000, 60_000, 4, gpu)
     native = NativeDendriticMatrixRuntime(case.topology, case.model, torch.zeros(1, 3000, device=gpu),
