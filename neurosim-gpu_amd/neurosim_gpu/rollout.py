@@ -19,8 +19,10 @@ class MatrixRollout:
     """``ticks`` fused ticks of a NativeDendriticMatrixRuntime per ``run()``.
 
     Drives are fixed for the rollout (numbers or tensors broadcastable to
-    [B, N]).  The runtime's current states seed the rollout; ``write_back()``
-    hands the rolled-out states back to the runtime.
+    [B, N]), and so are the weights: the captured ticks read the weight payload
+    (or its slot-order copy) of construction time, so build a new rollout after
+    changing the weights.  The runtime's current states seed the rollout;
+    ``write_back()`` hands the rolled-out states back to the runtime.
     """
 
     def __init__(self, runtime, ticks: int, *, drive=0.0, dendritic_drive=0.0,
