@@ -271,3 +271,15 @@ def test_backward_validation_messages(lib):
     assert rc == 0
     rc, message = call()
     assert rc != 0 and "state, dendrite and adaptation" in message
+    # complete host-memory arguments: the forward's current must not overlap the workspace
+    buf = np.zeros(16 * 10, np.float32)
+    base = buf.ctypes.data
+    plane = lambda k: native._Plane(base + 40 * k, 1, 1, 0.0)          # noqa: E731
+    out = lambda k: native._OutPlane(base + 40 * k, 1, 1)               # noqa: E731
+    index = np.zeros(11, np.int32)
+    rc, message = call(state=plane(0), dendrite=plane(1), adaptation=plane(2),
+                       d_state=out(3), d_dendrite=out(4), d_adaptation=out(5),
+                       out_rowptr=index.ctypes.data, dst=index.ctypes.data,
+                       out_weight_index=index.ctypes.data, workspace=base + 40 * 6,
+                       current=base + 40 * 7)
+    assert rc != 0 and "current must not overlap the workspace" in message
