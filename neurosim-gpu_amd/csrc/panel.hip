@@ -10,8 +10,12 @@
 //    destination rows.  It stages the panel's slice of s in LDS, plus one zero
 //    that padding slots point at;
 //  * the tile's rows are grouped by segment length; a group gives each row
-//    2^lg lanes, and lane j of a row accumulates the row's edges j, j+2^lg, ...
-//    in one float32 FMA chain, so the inner loop has no row boundaries;
+//    2^lg lanes, and lane j of a row accumulates items j, j+2^lg, ... of the
+//    row's segment in one float32 FMA chain, so the inner loop has no row
+//    boundaries.  The items are the segment's edges in CSR order or, in the
+//    pair layout (NS_PANEL_PAIRS), grouped by 16-edge weight block with each
+//    block's run padded to even length, so that two neighbouring lanes of a
+//    row hold edges of one NVFP4 block and share one scale byte;
 //  * each wavefront owns a run of consecutive groups (balanced by the planner)
 //    whose slots are one contiguous stream of 64-lane steps (16-bit
 //    panel-local source index plus the weight in its encoding).  The stream
@@ -26,8 +30,8 @@
 //    panel's partial sums by row and a second kernel adds them in panel
 //    order and applies the update.
 //
-// Results are bitwise repeatable and identical across weight encodings that
-// decode to the same float32 values.
+// Results are bitwise repeatable and, on one layout, identical across weight
+// encodings that decode to the same float32 values.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
