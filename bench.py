@@ -340,24 +340,27 @@ def measure_batched(device) -> dict:
 
 
 def measure_pels(device, theta: float = 0.02) -> dict:
-    """N=50000, M~1M, B=1: ms/tick of the two-kernel event tick in graphs of 64
+    """N=50000, M~1M, B=1: ms/tick of the one-launch event tick in graphs of 64
     ticks, for three activity regimes: drive .2/.1 switched on at a zero state,
     both inputs withdrawn after 512 driven ticks, and quiescence after 4096
     withdrawn ticks.  Each regime's activity (emitting sources and pushed
-    edges per tick) is counted on an eager run of the same 64 ticks."""
+    edges per tick) is counted on an eager run of the same 64 ticks.  The
+    driven regime is also timed on the two-launch tick (advance, then scatter)."""
     n, candidates, chunk = 50_000, 1_000_000, 64
     topology_cpu = random_topology(n, candidates, device="cpu", seed=0)
     topology = topology_to(topology_cpu, device)
     _, model = standard_model(n, device)
     runtime = NativeDendriticPELSRuntime(topology, model, torch.zeros(1, n, device=device),
                                          theta=theta)
+    two_launch = NativeDendriticPELSRuntime(topology, model, torch.zeros(1, n, device=device),
+                                            theta=theta, one_launch=False)
     out_degree = (topology.out_rowptr[1:] - topology.out_rowptr[:-1]).to(torch.int64)
     fields = ("state", "dendritic_state", "adaptation_state", "emitted_state",
               "persistent_current")
     result = {"workload": f"PELS event tick, N={n} M={topology_cpu.n_edges} B=1, theta {theta}",
               "ticks_per_graph": chunk}
 
-    def phase(drive: float, dendritic: float) -> dict:
+    def phase(drive: float, dendritic: float, runtime=runtime) -> dict:
         with torch.inference_mode():
             saved = [getattr(runtime, f).clone() for f in fields]
             sources = edges = 0
@@ -377,15 +380,16 @@ def measure_pels(device, theta: float = 0.02) -> dict:
             for f, value in zip(fields, saved):
                 setattr(runtime, f, value.clone())
             # The graph's first tick reads these input tensors again on every replay;
-            # only the persistent current is updated in place, so it is reset each time.
-            current = runtime.persistent_current
+            # only the persistent current (with the pending buffer of the one-launch
+            # tick) is updated in place, so it is reset each time: reading the
+            # attribute folds the outstanding buffer, then the copy overwrites.
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
                 for _ in range(chunk):
                     runtime.step(drive, dendritic_drive=dendritic)
             timings = []
             for _ in range(8):
-                current.copy_(saved[-1])
+                runtime.persistent_current.copy_(saved[-1])
                 start = torch.cuda.Event(enable_timing=True)
                 end = torch.cuda.Event(enable_timing=True)
                 start.record()
@@ -403,6 +407,8 @@ def measure_pels(device, theta: float = 0.02) -> dict:
                 "achieved_GBps": round(alg / ms / 1e6, 1)}
 
     result["driven_onset"] = phase(0.2, 0.1)
+    result["driven_onset_two_launch"] = phase(0.2, 0.1, two_launch)
+    del two_launch
     with torch.inference_mode():
         for _ in range(512):
             runtime.step(0.2, dendritic_drive=0.1)

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 6
+#define NS_ABI_VERSION 7
 
 /* Return codes. */
 #define NS_OK 0
@@ -221,7 +221,20 @@ typedef struct ns_event_args {
   const float* weight;         /* [M] destination-major float32 weights */
   int64_t n_edges;
   ns_out_plane out_state, out_dendrite, out_adaptation, out_emitted;
-  float* delta;                /* workspace float32[B*N], overwritten */
+  float* delta;                /* workspace float32[B*N], overwritten (two-launch tick) */
+  /* Optional, both or neither: the one-launch tick.  Each is float32[B*N],
+     entry n*B + b.  The true persistent current is then `current` plus the
+     pending contributions: on entry the tick reads j = current + pending_in,
+     stores j into `current` and zeroes pending_in; the emitters' out-edges are
+     added into pending_out, which must be zero on entry.  The caller swaps the
+     two buffers between ticks, or adds pending_out into `current` and zeroes
+     it.  `delta` is not used. */
+  float* pending_in;
+  float* pending_out;
+  /* Optional: the weights in source-major order, out_weight[e] ==
+     weight[weight_index[e]], so the scatter streams them instead of gathering
+     through weight_index (NULL: gather). */
+  const float* out_weight;
 } ns_event_args;
 
 /* Arguments of a plain CSR product J = W @ S (no neuron update). */
@@ -388,7 +401,9 @@ int ns_dendritic_step_bands(const ns_step_args* args, const ns_band_plan* plan, 
  * dendritic_event (reference: csrc/bindings.cpp:8-12,143;
  * csrc/compartmental.cu:238-273), except that the caller supplies the four
  * output planes and the delta workspace.  The emitted output follows the
- * reference runtime (runtime.py:241-242): emitted + delta. */
+ * reference runtime (runtime.py:241-242): emitted + delta.  With pending_in
+ * and pending_out set, the tick is one launch and its scatter goes to
+ * pending_out instead of `current` (see ns_event_args). */
 int ns_dendritic_event(const ns_event_args* args, void* stream);
 
 /* CSR product J = W @ S with the tick's decoding and summation order.

@@ -11,9 +11,18 @@
 //
 // Work decomposition (this library's own): kernel 1 walks (neuron, column)
 // pairs in neuron-major order, one lane each.  Kernel 2 gives each wavefront
-// 64 consecutive pairs: a ballot over their deltas finds the emitters, and
-// four 16-lane groups walk four emitters' source-major out-edge lists at a
-// time.  Inactive stretches cost one coalesced load and one ballot.
+// 64 consecutive pairs and spreads their emitters' source-major out-edges
+// over its lanes (see scatter_chunk).  Inactive stretches cost a few
+// coalesced loads and a prefix sum.
+//
+// One-launch tick (pending buffers given): the scatter cannot add into the
+// current that other wavefronts of the same launch still have to read, so it
+// adds into a zeroed pending buffer instead, and the next tick folds that
+// buffer into the current as it reads it (j = current + pending).  A
+// wavefront advances its 64 pairs and scatters their deltas straight from
+// registers; the launch boundary orders one tick's scatter before the next
+// tick's reads.  Two buffers alternate, so the buffer a tick scatters into is
+// never the one it reads and zeroes.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -36,9 +45,10 @@ struct EventArgs {
   const int32_t* dst;
   const int32_t* weight_index;
   const float* weight;
+  const float* out_weight;
+  float* pending_in;
+  float* pending_out;
 };
-
-constexpr int kScatterGroup = 16;  // lanes walking one emitter's out-edges
 
 __global__ __launch_bounds__(kThreads) void event_advance_kernel(EventArgs A) {
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
@@ -65,35 +75,114 @@ __global__ __launch_bounds__(kThreads) void event_advance_kernel(EventArgs A) {
   }
 }
 
+// Edges per lane per round of the scatter, loaded before any is added.
+constexpr int kScatterUnroll = 2;
+
+// Adds W[:, n] * delta for the emitters among one wavefront's 64 pairs into
+// target[b*tb + dst*tn].  Pair chunk*64 + lane holds `mine` and its neuron's
+// source-major out-edge range [start, end).  The emitters' out-edges are
+// numbered wave-wide by an inclusive prefix sum over their degrees; lane l
+// takes edges l, l + 64, ... and finds each one's emitter by a binary search
+// over the prefix sums.  Every lane has work whatever the degrees, and an
+// edge's loads (target index, weight) do not wait on each other.
+__device__ __forceinline__ void scatter_chunk(const EventArgs& A, int64_t chunk, int lane,
+                                              float mine, int64_t start, int64_t end,
+                                              float* target, int64_t tb, int64_t tn) {
+  const int64_t count = mine != 0.0f ? end - start : 0;
+  int64_t incl = count;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int64_t up = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += up;
+  }
+  const int64_t first = incl - count;  // number of this pair's first edge
+  const int64_t total = __shfl(incl, 63, 64);
+  const int64_t pair = chunk * 64 + lane;
+  const int column = static_cast<int>(pair - (pair / A.B) * A.B);
+  for (int64_t base = 0; base < total; base += 64 * kScatterUnroll) {
+    int64_t edge[kScatterUnroll];
+    float scale[kScatterUnroll];
+    int col[kScatterUnroll];
+    bool live[kScatterUnroll];
+#pragma unroll
+    for (int r = 0; r < kScatterUnroll; ++r) {
+      const int64_t k = base + r * 64 + lane;
+      // owner: the lowest lane whose inclusive sum exceeds k (all lanes search)
+      int o = 0;
+#pragma unroll
+      for (int step = 32; step > 0; step >>= 1)
+        if (__shfl(incl, o + step - 1, 64) <= k) o += step;
+      // Every lane takes part in each shuffle: a lane left out of one supplies
+      // zero to the lanes that read from it.
+      const int64_t owner_start = __shfl(start, o, 64);
+      const int64_t owner_first = __shfl(first, o, 64);
+      scale[r] = __shfl(mine, o, 64);
+      col[r] = __shfl(column, o, 64);
+      live[r] = k < total;
+      // a lane past the last edge reads edge 0 (total > 0, so it exists) and adds nothing
+      edge[r] = live[r] ? owner_start + (k - owner_first) : 0;
+    }
+    int32_t to[kScatterUnroll];
+    float w[kScatterUnroll];
+#pragma unroll
+    for (int r = 0; r < kScatterUnroll; ++r) {
+      to[r] = A.dst[edge[r]];
+      w[r] = A.out_weight ? A.out_weight[edge[r]] : A.weight[A.weight_index[edge[r]]];
+    }
+#pragma unroll
+    for (int r = 0; r < kScatterUnroll; ++r)
+      if (live[r])
+        unsafeAtomicAdd(target + col[r] * tb + static_cast<int64_t>(to[r]) * tn,
+                        scale[r] * w[r]);
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void event_scatter_kernel(EventArgs A) {
   const int lane = threadIdx.x & 63;
   const int64_t chunk = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) >> 6;
   const int64_t i = chunk * 64 + lane;
-  const float mine = i < A.count ? A.delta[i] : 0.0f;
-  uint64_t pending = __ballot(mine != 0.0f);
-  const int group = lane / kScatterGroup;
-  const int glane = lane & (kScatterGroup - 1);
-  while (pending) {
-    // The g-th lowest pending bit goes to group g (the same sequence on every lane).
-    int pick = -1;
-#pragma unroll
-    for (int g = 0; g < 64 / kScatterGroup; ++g) {
-      const int bit = pending ? __builtin_ctzll(pending) : -1;
-      if (bit >= 0) pending &= pending - 1;
-      if (g == group) pick = bit;
-    }
-    const float dl = __shfl(mine, pick < 0 ? 0 : pick, 64);
-    if (pick >= 0) {
-      const int64_t entry = chunk * 64 + pick;
-      const int64_t n = entry / A.B;
-      const int64_t b = entry - n * A.B;
-      const int64_t start = A.out_rowptr[n], end = A.out_rowptr[n + 1];
-      float* target = A.current + b * A.csb;
-      for (int64_t e = start + glane; e < end; e += kScatterGroup)
-        unsafeAtomicAdd(target + static_cast<int64_t>(A.dst[e]) * A.csn,
-                        dl * A.weight[A.weight_index[e]]);
-    }
+  float mine = 0.0f;
+  int64_t start = 0, end = 0;
+  if (i < A.count) {
+    const int64_t n = i / A.B;
+    mine = A.delta[i];
+    start = A.out_rowptr[n];
+    end = A.out_rowptr[n + 1];
   }
+  scatter_chunk(A, chunk, lane, mine, start, end, A.current, A.csb, A.csn);
+}
+
+// The one-launch tick: one lane per pair, one wavefront per 64 pairs.
+__global__ __launch_bounds__(kThreads) void event_tick_kernel(EventArgs A) {
+  const int lane = threadIdx.x & 63;
+  const int64_t chunk = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) >> 6;
+  const int64_t i = chunk * 64 + lane;
+  float dl = 0.0f;
+  int64_t start = 0, end = 0;
+  if (i < A.count) {
+    const int64_t n = i / A.B;
+    const int64_t b = i - n * A.B;
+    start = A.out_rowptr[n];
+    end = A.out_rowptr[n + 1];
+    float* at = A.current + b * A.csb + n * A.csn;
+    const float j = *at + A.pending_in[i];
+    *at = j;
+    A.pending_in[i] = 0.0f;
+    const NextState x = advance_one(A.p, n, j, A.s.get(b, n), A.d.get(b, n), A.a.get(b, n),
+                                    A.u.get(b, n), A.v.get(b, n));
+    const float previous = A.emitted.get(b, n);
+    {
+#pragma clang fp contract(off)
+      const float residual = x.soma - previous;
+      const bool active = fabsf(residual) >= A.theta.get(n);
+      dl = active ? residual : 0.0f;
+      A.oe.put(b, n, previous + dl);
+    }
+    A.os.put(b, n, x.soma);
+    A.od.put(b, n, x.dendrite);
+    A.oa.put(b, n, x.adaptation);
+  }
+  scatter_chunk(A, chunk, lane, dl, start, end, A.pending_out, 1, A.B);
 }
 
 }  // namespace ns
@@ -122,20 +211,37 @@ extern "C" int ns_dendritic_event(const ns_event_args* args, void* stream) {
   if (!a.out_state.data || !a.out_dendrite.data || !a.out_adaptation.data ||
       !a.out_emitted.data)
     return fail("four output planes are required");
-  if (!a.delta) return fail("a delta workspace is required");
+  const bool fused = a.pending_in || a.pending_out;
+  if (fused && !(a.pending_in && a.pending_out))
+    return fail("pending_in and pending_out go together");
+  if (!fused && !a.delta) return fail("a delta workspace is required");
   const int64_t B = a.batch, N = a.n_neurons;
-  const Extent outs[5] = {extent(a.out_state, B, N), extent(a.out_dendrite, B, N),
-                          extent(a.out_adaptation, B, N), extent(a.out_emitted, B, N),
-                          extent_of(a.delta, N, 1, B, N)};
-  const Extent ins[7] = {extent(a.state, B, N), extent(a.dendrite, B, N),
+  // Written memory: the four planes, then the delta workspace or the two
+  // pending buffers (entry n*B + b).
+  Extent outs[6] = {extent(a.out_state, B, N), extent(a.out_dendrite, B, N),
+                    extent(a.out_adaptation, B, N), extent(a.out_emitted, B, N)};
+  int n_outs = 5;
+  if (fused) {
+    outs[4] = extent_of(a.pending_in, 1, B, B, N);
+    outs[5] = extent_of(a.pending_out, 1, B, B, N);
+    n_outs = 6;
+  } else {
+    outs[4] = extent_of(a.delta, N, 1, B, N);
+  }
+  const Extent ins[8] = {extent(a.state, B, N), extent(a.dendrite, B, N),
                          extent(a.adaptation, B, N), extent(a.drive, B, N),
                          extent(a.dendritic_drive, B, N), extent(a.emitted, B, N),
-                         extent_of(a.current, a.current_stride_b, a.current_stride_n, B, N)};
-  for (int o = 0; o < 5; ++o) {
-    for (int i = 0; i < 7; ++i)
-      if (overlaps(outs[o], ins[i])) return fail("output planes must not overlap inputs");
-    for (int p = o + 1; p < 5; ++p)
-      if (overlaps(outs[o], outs[p])) return fail("output planes must not overlap each other");
+                         extent_of(a.current, a.current_stride_b, a.current_stride_n, B, N),
+                         extent_of(a.out_weight, 0, 1, 1, a.n_edges)};
+  for (int o = 0; o < n_outs; ++o) {
+    for (int i = 0; i < 8; ++i)
+      if (overlaps(outs[o], ins[i]))
+        return fail(o < 4 ? "output planes must not overlap inputs"
+                          : "event workspaces must not overlap inputs or the current");
+    for (int p = o + 1; p < n_outs; ++p)
+      if (overlaps(outs[o], outs[p]))
+        return fail(p < 4 ? "output planes must not overlap each other"
+                          : "event workspaces must not overlap outputs or each other");
   }
   if ((B * N + kThreads - 1) / kThreads > 0x7FFFFFFF)
     return fail("B*N is too large for one scatter launch");
@@ -154,8 +260,16 @@ extern "C" int ns_dendritic_event(const ns_event_args* args, void* stream) {
   A.delta = a.delta;
   A.out_rowptr = a.out_rowptr; A.dst = a.dst; A.weight_index = a.weight_index;
   A.weight = a.weight;
+  A.out_weight = a.out_weight;
+  A.pending_in = a.pending_in; A.pending_out = a.pending_out;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (fused) {
+    const int64_t blocks = (A.count + kThreads - 1) / kThreads;
+    event_tick_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, s>>>(A);
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? NS_OK : fail_launch("event tick", err);
+  }
   const int64_t advance_blocks = std::min<int64_t>((A.count + kThreads - 1) / kThreads, 65536);
   event_advance_kernel<<<dim3(static_cast<unsigned>(advance_blocks)), dim3(kThreads), 0, s>>>(A);
   hipError_t err = hipGetLastError();

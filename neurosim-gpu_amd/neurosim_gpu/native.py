@@ -35,7 +35,7 @@ import numpy as np
 import torch
 
 _LIB_NAME = "libneurosim_hip.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 WEIGHT_F32, WEIGHT_F16, WEIGHT_E4M3, WEIGHT_NVFP4 = 0, 1, 2, 3
 _PLAN_CACHE = 64   # row plans kept per extension (one per live topology and batch width)
@@ -108,7 +108,8 @@ class _EventArgs(ctypes.Structure):
                 ("weight", _c_ptr), ("n_edges", _c_i64),
                 ("out_state", _OutPlane), ("out_dendrite", _OutPlane),
                 ("out_adaptation", _OutPlane), ("out_emitted", _OutPlane),
-                ("delta", _c_ptr)]
+                ("delta", _c_ptr), ("pending_in", _c_ptr), ("pending_out", _c_ptr),
+                ("out_weight", _c_ptr)]
 
 
 class _SpmmArgs(ctypes.Structure):
@@ -732,7 +733,18 @@ class NativeExtension:
 
     def dendritic_event(self, state, dendrite, adaptation, params, current, emitted, theta,
                         rowptr, dst, weight_index, weight, input, input_scalar,
-                        dendritic_input, dendritic_scalar, delta=None):
+                        dendritic_input, dendritic_scalar, delta=None, pending=None,
+                        out_weight=None):
+        """One PELS tick (ns_dendritic_event); returns the four new planes.
+
+        Without ``pending`` the tick is two launches and ``current`` is updated
+        in place.  ``pending=(pending_in, pending_out)``, two float32 buffers of
+        B*N entries (n*B + b), makes it one launch: ``current`` receives
+        current + pending_in, pending_in is zeroed, and this tick's W @ delta
+        is added into pending_out (zero on entry), so the persistent current
+        afterwards is current + pending_out.  ``out_weight`` optionally gives
+        the weights in source-major order (``weight[weight_index]``), which the
+        scatter then streams instead of gathering."""
         _check_state(state)
         args = _EventArgs()
         args.state = _plane(state, state, "state")
@@ -766,11 +778,26 @@ class NativeExtension:
         outs = new_planes(4, batch, n, state)
         (args.out_state, args.out_dendrite, args.out_adaptation,
          args.out_emitted) = (_out(o) for o in outs)
-        if delta is None:
+        if out_weight is not None:
+            if (out_weight.dtype != torch.float32 or not out_weight.is_contiguous()
+                    or out_weight.numel() != weight.numel()
+                    or out_weight.device != state.device):
+                raise RuntimeError("out_weight must be M contiguous float32 on the state's device")
+            args.out_weight = out_weight.data_ptr()
+        if pending is not None:
+            pending_in, pending_out = pending
+            for buffer in (pending_in, pending_out):
+                if (buffer.numel() < batch * n or buffer.dtype != torch.float32
+                        or not buffer.is_contiguous() or buffer.device != state.device):
+                    raise RuntimeError("pending buffers must hold B*N float32 on the state's device")
+            args.pending_in, args.pending_out = pending_in.data_ptr(), pending_out.data_ptr()
+        elif delta is None:
             delta = torch.empty(batch * n, dtype=torch.float32, device=state.device)
-        elif delta.numel() < batch * n or delta.dtype != torch.float32 or not delta.is_contiguous():
-            raise RuntimeError("delta workspace must hold B*N float32")
-        args.delta = delta.data_ptr()
+        if delta is not None:
+            if (delta.numel() < batch * n or delta.dtype != torch.float32
+                    or not delta.is_contiguous()):
+                raise RuntimeError("delta workspace must hold B*N float32")
+            args.delta = delta.data_ptr()
         stream = torch.cuda.current_stream(state.device).cuda_stream
         _raise_on(self.lib.ns_dendritic_event(ctypes.byref(args), stream), self.lib)
         return outs

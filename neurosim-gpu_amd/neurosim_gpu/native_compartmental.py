@@ -51,9 +51,11 @@ class _NativeCompartments:
         values = [self.state, self.dendritic_state, self.adaptation_state,
                   self.topology.weight, self.topology.in_weight, *self._parameters(),
                   drive, dendritic_drive]
-        if hasattr(self, "persistent_current"):
-            values += [self.persistent_current, self.emitted_state]
+        values += self._event_tensors()
         return any(isinstance(v, torch.Tensor) and v.requires_grad for v in values)
+
+    def _event_tensors(self) -> list[torch.Tensor]:
+        return []
 
     def _drive(self, value) -> tuple[torch.Tensor | None, float]:
         """(broadcast [B,N] view, 0.0) for tensors, (None, value) for numbers."""
@@ -382,12 +384,27 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
 
 
 class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
-    """Two HIP launches per tick: advance/emission, then out-edge scatter.
+    """The PELS event tick on the device, by default in one HIP launch.
 
-    The scan covers all B*N (neuron, column) pairs on the device; only pairs
-    with a nonzero delta walk their out-edges.  Float32 atomics make the
-    scatter's summation order, and therefore the last bits of the current,
-    run-dependent.  Statistics and autograd requests use the reference step.
+    The scan covers all B*N (neuron, column) pairs; only pairs with a nonzero
+    delta walk their out-edges.  In the one-launch tick a wavefront advances
+    its pairs and scatters their deltas itself.  Its scatter cannot add into
+    the current that other wavefronts of the launch still read, so it adds
+    into one of two pending buffers, and the next tick folds that buffer into
+    the current as it reads it (j = current + pending, the same float32 sum
+    either way).  Reading ``persistent_current`` folds the outstanding buffer
+    first, so the attribute always holds W @ emitted as in the reference;
+    assigning it discards the outstanding buffer.  The scatter streams a
+    source-major copy of the weights (M floats, rebuilt when the weights
+    change; ``source_major_weights = False`` gathers through
+    ``out_weight_index`` instead).  Ticks captured in a HIP
+    graph use fixed buffers: replays of an even number of ticks chain as they
+    are, after an odd number read ``persistent_current`` (which folds) before
+    the next replay.  ``one_launch=False`` runs
+    the two-launch tick (advance, then scatter into the current).  Float32
+    atomics make the scatter's summation order, and therefore the last bits
+    of the current, run-dependent.  Statistics and autograd requests use the
+    reference step.
     """
 
     @property
@@ -396,13 +413,58 @@ class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
 
     def __init__(self, topology: SparseTopology, dynamics: DendriticDynamics,
                  initial_state: torch.Tensor, *, theta: float | torch.Tensor,
-                 extension=None) -> None:
+                 extension=None, one_launch: bool = True) -> None:
         _require_gpu_float32(initial_state)
+        self._pending = None
         self.extension = extension if extension is not None else load_native_extension()
         super().__init__(topology, dynamics, initial_state, theta=theta, propagation="event")
         self._init_native(initial_state, self.extension)
         batch, n = initial_state.shape
-        self._delta = torch.empty(batch * n, dtype=torch.float32, device=initial_state.device)
+        self.source_major_weights = True
+        self._out_weight = self._out_weight_key = self._out_weight_source = None
+        if one_launch and isinstance(self.extension, NativeExtension):
+            self._pending = torch.zeros(2, batch * n, dtype=torch.float32,
+                                        device=initial_state.device)
+            self._parity = 0
+        else:
+            self._delta = torch.empty(batch * n, dtype=torch.float32, device=initial_state.device)
+
+    @property
+    def persistent_current(self) -> torch.Tensor:
+        pending = self._pending
+        if pending is not None and not self._current.requires_grad:
+            # Between ticks at most one buffer is nonzero, so adding both adds it
+            # exactly.  No host flag tracks which: replays of captured ticks
+            # change the buffers without the host seeing them.
+            batch, n = self._current.shape
+            with torch.inference_mode():
+                self._current.add_(pending.sum(0).view(n, batch).t())
+                pending.zero_()
+        return self._current
+
+    @persistent_current.setter
+    def persistent_current(self, value: torch.Tensor) -> None:
+        if self._pending is not None:
+            with torch.inference_mode():
+                self._pending.zero_()
+        self._current = value
+
+    def _event_tensors(self) -> list[torch.Tensor]:
+        return [self._current, self.emitted_state]
+
+    def _source_major(self) -> torch.Tensor | None:
+        """in_weight[out_weight_index], rebuilt when the weights change (a new
+        tensor, an in-place edit, or a new topology weight version)."""
+        if not self.source_major_weights or not isinstance(self.extension, NativeExtension):
+            return None
+        topology = self.topology
+        key = (_weight_key(topology.in_weight), topology.weight_version)
+        if key != self._out_weight_key or self._out_weight_source is not topology.in_weight:
+            with torch.no_grad():
+                self._out_weight = torch.index_select(topology.in_weight.detach(), 0,
+                                                      topology.out_weight_index)
+            self._out_weight_key, self._out_weight_source = key, topology.in_weight
+        return self._out_weight
 
     def _initial_current(self) -> torch.Tensor:
         if torch.is_grad_enabled() and (self.emitted_state.requires_grad
@@ -428,14 +490,24 @@ class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
         u, us = self._drive(drive)
         v, vs = self._drive(dendritic_drive)
         self._refresh_current()
-        extra = {"delta": self._delta} if isinstance(self.extension, NativeExtension) else {}
-        # The current is updated in place only after the advance kernel has read it.
+        if self._pending is not None:
+            # pending[parity] holds the last tick's scatter (or zeros); the other is zero.
+            extra = {"pending": (self._pending[self._parity], self._pending[1 - self._parity])}
+        elif isinstance(self.extension, NativeExtension):
+            extra = {"delta": self._delta}
+        else:
+            extra = {}
+        out_weight = self._source_major()
+        if out_weight is not None:
+            extra["out_weight"] = out_weight
         self.state, self.dendritic_state, self.adaptation_state, self.emitted_state = (
             self.extension.dendritic_event(
                 self.state, self.dendritic_state, self.adaptation_state, self._parameters(),
-                self.persistent_current, self.emitted_state, self.theta,
+                self._current, self.emitted_state, self.theta,
                 self.topology.out_rowptr, self.topology.dst, self.topology.out_weight_index,
                 self.topology.in_weight, u, us, v, vs, **extra))
+        if self._pending is not None:
+            self._parity ^= 1
         self._tick += 1
         self.last_backend = "native"
         return self.state

@@ -283,3 +283,60 @@ def test_backward_validation_messages(lib):
                        out_weight_index=index.ctypes.data, workspace=base + 40 * 6,
                        current=base + 40 * 7)
     assert rc != 0 and "current must not overlap the workspace" in message
+
+
+def fake_event_args(n=8, batch=2):
+    """Valid-looking host buffers for ns_dendritic_event; used only for calls
+    that fail validation, so nothing is launched."""
+    keep = [np.zeros(batch * n, np.float32) for _ in range(12)]
+    params = [np.ones(n, np.float32) for _ in range(7)]
+    rowptr = np.zeros(n + 1, np.int32)
+    args = native._EventArgs()
+    args.n_neurons, args.batch = n, batch
+    args.state, args.dendrite, args.adaptation, args.emitted = (
+        native._Plane(k.ctypes.data, n, 1, 0.0) for k in keep[:4])
+    args.drive = native._Plane(None, 0, 0, 0.2)
+    args.dendritic_drive = native._Plane(None, 0, 0, 0.1)
+    for i in range(6):
+        args.params[i] = native._Vector(params[i].ctypes.data, 1)
+    args.theta = native._Vector(params[6].ctypes.data, 1)
+    args.current, args.current_stride_b, args.current_stride_n = keep[4].ctypes.data, n, 1
+    args.out_rowptr, args.n_edges = rowptr.ctypes.data, 0
+    args.out_state, args.out_dendrite, args.out_adaptation, args.out_emitted = (
+        native._OutPlane(k.ctypes.data, n, 1) for k in keep[5:9])
+    args.delta = keep[9].ctypes.data
+    return args, (keep, params, rowptr)
+
+
+def test_event_validation_messages(lib):
+    """ns_dendritic_event's rejections, for the two-launch and the one-launch
+    (pending buffers) tick, all before any launch."""
+    def call(args):
+        rc = lib.ns_dendritic_event(ctypes.byref(args), None)
+        return rc, lib.ns_last_error().decode()
+
+    args, keep = fake_event_args()
+    args.delta = None
+    assert "delta workspace" in call(args)[1]
+    args, keep = fake_event_args()
+    args.pending_in = keep[0][10].ctypes.data
+    assert "go together" in call(args)[1]
+    args, keep = fake_event_args()
+    args.out_dendrite = native._OutPlane(args.state.data, 8, 1)
+    assert "output planes must not overlap inputs" in call(args)[1]
+    args, keep = fake_event_args()
+    args.delta = args.current
+    assert "workspaces must not overlap inputs" in call(args)[1]
+    for pending_in, pending_out, message in (
+            (4, 10, "workspaces must not overlap inputs"),          # the current
+            (10, 5, "must not overlap outputs"),                    # out_state
+            (10, 10, "must not overlap outputs or each other")):
+        args, keep = fake_event_args()
+        buffers = keep[0]
+        args.delta = None
+        args.pending_in = buffers[pending_in].ctypes.data
+        args.pending_out = buffers[pending_out].ctypes.data
+        rc, text = call(args)
+        assert rc != 0 and message in text, text
+    args, keep = fake_event_args(batch=0)
+    assert call(args) == (0, "")

@@ -24,11 +24,13 @@ def state_error(native, oracle) -> float:
     return max(max_err(getattr(native, f), getattr(oracle, f)) for f in FIELDS)
 
 
-def test_theta_zero_long_rollout_matches_matrix(gpu):
+@pytest.mark.parametrize("one_launch", [True, False])
+def test_theta_zero_long_rollout_matches_matrix(gpu, one_launch):
     """Reference test_native_compartmental.py:99-110 (N=1024, B=2, 16000 edges, 500 ticks)."""
     case = make_case(1024, 16000, 83, gpu, kind="reference")
     state = torch.full((2, 1024), 0.2)
-    native = NativeDendriticPELSRuntime(case.topology, case.model, state.to(gpu), theta=0)
+    native = NativeDendriticPELSRuntime(case.topology, case.model, state.to(gpu), theta=0,
+                                        one_launch=one_launch)
     matrix = ort.MatrixOracle(case.graph, case.params, state)
     for t in range(500):
         value = 0.2 if t % 70 < 35 else 0.05
@@ -39,13 +41,15 @@ def test_theta_zero_long_rollout_matches_matrix(gpu):
     assert max_err(native.persistent_current, current) <= 1e-5
 
 
-def test_nonzero_theta_emission_and_weight_mutation(gpu):
+@pytest.mark.parametrize("one_launch", [True, False])
+def test_nonzero_theta_emission_and_weight_mutation(gpu, one_launch):
     """Reference test_native_compartmental.py:142-164 (theta .02, weights x0.7 at tick 25)."""
     from oracle import topology as otop
 
     case = make_case(97, 600, 83, gpu, kind="reference")
     state = torch.full((3, 97), 0.2)
-    native = NativeDendriticPELSRuntime(case.topology, case.model, state.to(gpu), theta=0.02)
+    native = NativeDendriticPELSRuntime(case.topology, case.model, state.to(gpu), theta=0.02,
+                                        one_launch=one_launch)
     oracle = ort.PelsOracle(case.graph, case.params, state, theta=0.02)
     for t in range(50):
         if t == 25:
@@ -119,3 +123,70 @@ def test_cfg4_event_path_warmup_then_withdrawn(gpu, theta):
     assert worst_current <= bar
     assert max_err(native.emitted_state, oracle.emitted_state) <= bar
     assert mismatches <= 1e-3 * max(checked, 1)
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_one_launch_pending_reads_and_assignments(gpu, batch):
+    """Reads of the persistent current fold the outstanding pending buffer; an
+    assignment replaces the current and discards it.  Either way the run goes on
+    matching the oracle and the two-launch tick (which gathers its weights
+    through out_weight_index instead of streaming the source-major copy)."""
+    case = make_case(2000, 40_000, 7, gpu)
+    matrix = ort.csr_matrix(case.graph)
+    state = torch.full((batch, 2000), 0.1)
+    native = NativeDendriticPELSRuntime(case.topology, case.model, state.to(gpu), theta=0.01)
+    two = NativeDendriticPELSRuntime(case.topology, case.model, state.to(gpu), theta=0.01,
+                                     one_launch=False)
+    two.source_major_weights = False            # the scatter gathers through out_weight_index
+    oracle = ort.PelsOracle(case.graph, case.params, state, theta=0.01)
+    for tick in range(60):
+        drive = 0.3 if tick < 40 else 0.0
+        for runtime in (native, two):
+            runtime.step(drive, dendritic_drive=0.1)
+        oracle.step(drive, 0.1)
+        exact = ort.propagate(matrix, native.emitted_state.cpu())
+        if tick % 7 == 3:
+            assert max_err(native.persistent_current, exact) <= 1e-5
+        if tick % 11 == 5:
+            # the exact current, assigned while a scatter is outstanding
+            native.persistent_current = exact.to(gpu)
+        if tick % 11 == 6:
+            assert max_err(native.persistent_current, exact) <= 1e-5
+    assert state_error(native, oracle) <= 1e-3
+    assert state_error(native, two) <= 1e-3
+    assert max_err(native.persistent_current, oracle.persistent_current) <= 1e-3
+
+
+def test_one_launch_graph_replay_matches_eager(gpu):
+    """Ticks captured in a HIP graph (an odd count, so the pending buffers swap
+    roles between replays) against eager ticks, theta 0."""
+    case = make_case(3000, 60_000, 8, gpu)
+    state = torch.full((2, 3000), 0.1, device=gpu)
+    eager = NativeDendriticPELSRuntime(case.topology, case.model, state.clone(), theta=0.0)
+    rolled = NativeDendriticPELSRuntime(case.topology, case.model, state.clone(), theta=0.0)
+    for runtime in (eager, rolled):
+        for _ in range(3):
+            runtime.step(0.2, dendritic_drive=0.1)
+    fields = ("state", "dendritic_state", "adaptation_state", "emitted_state")
+    start = [getattr(rolled, f) for f in fields]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(5):
+            rolled.step(0.2, dendritic_drive=0.1)
+    end = [getattr(rolled, f) for f in fields]
+    for replay in range(3):
+        if replay:
+            # the next replay starts from this replay's end; the graph's pending
+            # buffers swap roles, which the captured ticks cannot do, so the
+            # outstanding buffer is folded into the current first
+            for first, last in zip(start, end):
+                first.copy_(last)
+            rolled.persistent_current
+            assert not rolled._pending.any()
+        graph.replay()
+        for _ in range(5):
+            eager.step(0.2, dendritic_drive=0.1)
+        torch.cuda.synchronize()
+        for name, value in zip(fields, end):
+            assert max_err(value, getattr(eager, name)) <= 1e-5, (replay, name)
+        assert max_err(rolled.persistent_current, eager.persistent_current) <= 1e-5, replay
