@@ -50,28 +50,34 @@ struct EventArgs {
   float* pending_out;
 };
 
+// Advances pair (n, b) on current j, stores the three states and the
+// emitted state, and returns the pair's delta.
+__device__ __forceinline__ float advance_pair(const EventArgs& A, int64_t n, int64_t b,
+                                              float j) {
+  const NextState x = advance_one(A.p, n, j, A.s.get(b, n), A.d.get(b, n), A.a.get(b, n),
+                                  A.u.get(b, n), A.v.get(b, n));
+  const float previous = A.emitted.get(b, n);
+  float dl;
+  {
+#pragma clang fp contract(off)
+    const float residual = x.soma - previous;
+    const bool active = fabsf(residual) >= A.theta.get(n);
+    dl = active ? residual : 0.0f;
+    A.oe.put(b, n, previous + dl);
+  }
+  A.os.put(b, n, x.soma);
+  A.od.put(b, n, x.dendrite);
+  A.oa.put(b, n, x.adaptation);
+  return dl;
+}
+
 __global__ __launch_bounds__(kThreads) void event_advance_kernel(EventArgs A) {
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < A.count;
        i += stride) {
     const int64_t n = i / A.B;
     const int64_t b = i - n * A.B;
-    const float j = A.current[b * A.csb + n * A.csn];
-    const NextState x = advance_one(A.p, n, j, A.s.get(b, n), A.d.get(b, n), A.a.get(b, n),
-                                    A.u.get(b, n), A.v.get(b, n));
-    const float previous = A.emitted.get(b, n);
-    float dl;
-    {
-#pragma clang fp contract(off)
-      const float residual = x.soma - previous;
-      const bool active = fabsf(residual) >= A.theta.get(n);
-      dl = active ? residual : 0.0f;
-      A.oe.put(b, n, previous + dl);
-    }
-    A.os.put(b, n, x.soma);
-    A.od.put(b, n, x.dendrite);
-    A.oa.put(b, n, x.adaptation);
-    A.delta[i] = dl;
+    A.delta[i] = advance_pair(A, n, b, A.current[b * A.csb + n * A.csn]);
   }
 }
 
@@ -168,19 +174,7 @@ __global__ __launch_bounds__(kThreads) void event_tick_kernel(EventArgs A) {
     const float j = *at + A.pending_in[i];
     *at = j;
     A.pending_in[i] = 0.0f;
-    const NextState x = advance_one(A.p, n, j, A.s.get(b, n), A.d.get(b, n), A.a.get(b, n),
-                                    A.u.get(b, n), A.v.get(b, n));
-    const float previous = A.emitted.get(b, n);
-    {
-#pragma clang fp contract(off)
-      const float residual = x.soma - previous;
-      const bool active = fabsf(residual) >= A.theta.get(n);
-      dl = active ? residual : 0.0f;
-      A.oe.put(b, n, previous + dl);
-    }
-    A.os.put(b, n, x.soma);
-    A.od.put(b, n, x.dendrite);
-    A.oa.put(b, n, x.adaptation);
+    dl = advance_pair(A, n, b, j);
   }
   scatter_chunk(A, chunk, lane, dl, start, end, A.pending_out, 1, A.B);
 }
