@@ -190,3 +190,43 @@ def test_one_launch_graph_replay_matches_eager(gpu):
         for name, value in zip(fields, end):
             assert max_err(value, getattr(eager, name)) <= 1e-5, (replay, name)
         assert max_err(rolled.persistent_current, eager.persistent_current) <= 1e-5, replay
+
+
+@pytest.mark.parametrize("one_launch", [True, False])
+@pytest.mark.parametrize("theta", [0.0, 0.01])
+def test_hub_sources_scatter_many_rounds(gpu, one_launch, theta):
+    """Sources with thousands of out-edges next to ordinary ones, B=3: one
+    wavefront's emitters then span dozens of 64-edge rounds, and an edge's
+    emitter is found among neighbours of very different degree."""
+    from oracle import topology as otop
+    from neurosim_gpu import SparseTopology, topology_to
+    from cases import model_to, standard_model
+
+    print(f"case pels hubs theta={theta} one_launch={one_launch}", flush=True)
+    n = 3000
+    rng = np.random.default_rng(21)
+    hubs = [(5, 2900), (6, 1500), (64, 2999), (2999, 2000)]
+    src = [rng.integers(0, n, 20 * n)]
+    dst = [rng.integers(0, n, 20 * n)]
+    for source, degree in hubs:
+        src.append(np.full(degree, source))
+        dst.append(rng.permutation(n)[:degree])
+    src, dst = np.concatenate(src), np.concatenate(dst)
+    weight = (rng.standard_normal(src.size) * 0.02).astype(np.float32)
+    graph = otop.build(n, src, dst, weight)
+    topology = topology_to(SparseTopology.from_edges(n, torch.from_numpy(src), torch.from_numpy(dst),
+                                                     torch.from_numpy(weight)), gpu)
+    model, params = standard_model(n)
+    state = torch.full((3, n), 0.1)
+    native = NativeDendriticPELSRuntime(topology, model_to(model, gpu), state.to(gpu), theta=theta,
+                                        one_launch=one_launch)
+    oracle = ort.PelsOracle(graph, params, state, theta=theta)
+    matrix = ort.csr_matrix(graph)
+    for tick in range(40):
+        drive = 0.3 if tick < 25 else 0.05
+        native.step(drive, dendritic_drive=0.1)
+        oracle.step(drive, 0.1)
+    exact = ort.propagate(matrix, native.emitted_state.cpu())
+    bar = 1e-5 if theta == 0 else 1e-3
+    assert max_err(native.persistent_current, exact) <= 1e-5
+    assert state_error(native, oracle) <= bar
