@@ -3,11 +3,13 @@
 API of the reference's native_compartmental module
 (src/neurosim_gpu/native_compartmental.py:13-177):
 
-* NativeDendriticMatrixRuntime -- one fused kernel per tick: CSR gather-product
-  over the B columns plus the three-state update, with fp32 / fp16 / fp8 e4m3 /
-  nvfp4 weights decoded in-kernel and accumulated in float32.
-* NativeDendriticPELSRuntime -- two kernels per tick: advance + emission
-  threshold, then the emitters' out-edge scatter into the persistent current.
+* NativeDendriticMatrixRuntime -- the fused tick: CSR gather-product over the
+  B columns plus the three-state update, with fp32 / fp16 / fp8 e4m3 / nvfp4
+  weights decoded in-kernel and accumulated in float32 (one launch on row
+  blocks or bands; on column panels, a panel launch and a combine launch).
+* NativeDendriticPELSRuntime -- advance + emission threshold, then the
+  emitters' out-edge scatter into the persistent current: one launch per tick
+  (through pending buffers), or the reference's two (``one_launch=False``).
 
 Matrix ticks that need autograd (any tensor with requires_grad under grad
 mode) run the same native forward with a native backward
