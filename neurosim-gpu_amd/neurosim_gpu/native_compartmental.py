@@ -87,32 +87,39 @@ def _weight_key(weight: torch.Tensor) -> tuple:
 
 
 class SourceMajorWeights:
-    """Source-major copy of the CSR weights for the backward's transposed product.
+    """Source-major copy of the CSR weights (``weight[out_weight_index]``) for
+    kernels that walk out-edges: the backward's transposed product and the PELS
+    scatter.
 
-    The transposed product walks out-edges; reading CSR-order weights there is
-    one random gather per edge.  Backpropagation through several ticks reuses
-    one weight version, so the copy (one gather) is built on the second
-    backward that sees a version and then streamed; a single backward keeps the
-    direct gather.  A version is (tensor, in-place version counter), so an
-    optimizer step on the weights, in place or into a new tensor, invalidates
-    the copy.  ``enabled`` turns the copy off.
+    Reading CSR-order weights along out-edges is one random gather per edge.
+    The copy costs one such gather and is then streamed, so it is built on the
+    ``build_after``-th request for one weight version: the second for the
+    backward (backpropagation through several ticks reuses a version; a single
+    backward keeps the direct gather), the first for PELS ticks.  A version is
+    (tensor, in-place version counter, optional caller key), so an optimizer
+    step on the weights, in place or into a new tensor, invalidates the copy.
+    ``enabled`` turns the copy off.
     """
 
-    def __init__(self) -> None:
+    def __init__(self, build_after: int = 2) -> None:
         self.enabled = True
+        self.build_after = build_after
         self._key = None
         self._source: torch.Tensor | None = None
         self._seen = 0
         self._values: torch.Tensor | None = None
 
-    def get(self, weight: torch.Tensor, out_weight_index: torch.Tensor) -> torch.Tensor | None:
+    def get(self, weight: torch.Tensor, out_weight_index: torch.Tensor,
+            version=None) -> torch.Tensor | None:
+        """The copy for ``weight``, or None while it is not (yet) built.
+        ``version`` adds to the key (e.g. a topology weight version)."""
         if not self.enabled:
             return None
-        key = _weight_key(weight)
+        key = (_weight_key(weight), version)
         if key != self._key or self._source is not weight:
             self._key, self._source, self._seen, self._values = key, weight, 0, None
         self._seen += 1
-        if self._seen >= 2 and self._values is None:
+        if self._seen >= self.build_after and self._values is None:
             with torch.no_grad():
                 self._values = torch.index_select(weight.detach(), 0, out_weight_index)
         return self._values
@@ -398,7 +405,7 @@ class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
     first, so the attribute always holds W @ emitted as in the reference;
     assigning it discards the outstanding buffer.  The scatter streams a
     source-major copy of the weights (M floats, rebuilt when the weights
-    change; ``source_major_weights = False`` gathers through
+    change; ``source_major_weights.enabled = False`` gathers through
     ``out_weight_index`` instead).  Ticks captured in a HIP
     graph use fixed buffers: replays of an even number of ticks chain as they
     are, after an odd number read ``persistent_current`` (which folds) before
@@ -422,8 +429,7 @@ class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
         super().__init__(topology, dynamics, initial_state, theta=theta, propagation="event")
         self._init_native(initial_state, self.extension)
         batch, n = initial_state.shape
-        self.source_major_weights = True
-        self._out_weight = self._out_weight_key = self._out_weight_source = None
+        self.source_major_weights = SourceMajorWeights(build_after=1)
         if one_launch and isinstance(self.extension, NativeExtension):
             self._pending = torch.zeros(2, batch * n, dtype=torch.float32,
                                         device=initial_state.device)
@@ -457,16 +463,11 @@ class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
     def _source_major(self) -> torch.Tensor | None:
         """in_weight[out_weight_index], rebuilt when the weights change (a new
         tensor, an in-place edit, or a new topology weight version)."""
-        if not self.source_major_weights or not isinstance(self.extension, NativeExtension):
+        if not isinstance(self.extension, NativeExtension):
             return None
         topology = self.topology
-        key = (_weight_key(topology.in_weight), topology.weight_version)
-        if key != self._out_weight_key or self._out_weight_source is not topology.in_weight:
-            with torch.no_grad():
-                self._out_weight = torch.index_select(topology.in_weight.detach(), 0,
-                                                      topology.out_weight_index)
-            self._out_weight_key, self._out_weight_source = key, topology.in_weight
-        return self._out_weight
+        return self.source_major_weights.get(topology.in_weight, topology.out_weight_index,
+                                             topology.weight_version)
 
     def _initial_current(self) -> torch.Tensor:
         if torch.is_grad_enabled() and (self.emitted_state.requires_grad

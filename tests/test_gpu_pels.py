@@ -137,7 +137,7 @@ def test_one_launch_pending_reads_and_assignments(gpu, batch):
     native = NativeDendriticPELSRuntime(case.topology, case.model, state.to(gpu), theta=0.01)
     two = NativeDendriticPELSRuntime(case.topology, case.model, state.to(gpu), theta=0.01,
                                      one_launch=False)
-    two.source_major_weights = False            # the scatter gathers through out_weight_index
+    two.source_major_weights.enabled = False    # the scatter gathers through out_weight_index
     oracle = ort.PelsOracle(case.graph, case.params, state, theta=0.01)
     for tick in range(60):
         drive = 0.3 if tick < 40 else 0.0
