@@ -4,6 +4,10 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <atomic>
+#include <functional>
+#include <system_error>
+#include <thread>
 #include <cstdio>
 #include <vector>
 
@@ -347,6 +351,26 @@ extern "C" int ns_plan_panels(const int32_t* rowptr, const int32_t* col, int64_t
 namespace {
 
 // The band layout of one graph, in host vectors (built twice: size query, then fill).
+// Host threads a planner may use (the hosts this runs on give a process
+// about 16 cores).
+constexpr unsigned kPlanThreads = 16;
+
+// Runs `work` on min(kPlanThreads, hardware threads, items) threads, this one
+// included; `work` takes its items from a shared counter.  Without threads
+// (creation fails) it runs on this thread alone.
+template <typename Work>
+void run_on_threads(Work& work, int64_t items) {
+  const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+  const int64_t n = std::min<int64_t>({int64_t{kPlanThreads}, int64_t{hw}, std::max<int64_t>(items, 1)});
+  std::vector<std::thread> pool;
+  try {
+    for (int64_t t = 1; t < n; ++t) pool.emplace_back(std::ref(work));
+  } catch (const std::system_error&) {
+  }
+  work();
+  for (std::thread& t : pool) t.join();
+}
+
 struct BandLayout {
   int64_t n_groups = 0, n_slots = 0;
   std::vector<int32_t> wave_blocks, blocks, perm;
@@ -471,41 +495,68 @@ extern "C" int ns_plan_bands(const int32_t* rowptr, const int32_t* col, int64_t 
   const bool fill = wave_blocks || blocks || rows || perm || col_out;
   if (fill && !(wave_blocks && blocks && rows && perm && col_out))
     return fail("all output arrays are required together");
-  BandLayout layout;
-  for (int64_t q = 0; q < n_row_blocks; ++q) {
-    const int64_t r0 = q * block_rows, r1 = std::min<int64_t>(n_rows, r0 + block_rows);
-    append_band_block(layout, rowptr, col, r0, r1, band_width, static_cast<int32_t>(n_bands),
-                      block_steps, fill);
-    if (layout.n_slots >= (int64_t{1} << 37) || layout.blocks.size() / 4 >= (size_t{1} << 31))
-      return fail("band layout needs too many slots");
+  // Row blocks are laid out independently, on up to kPlanThreads threads,
+  // then concatenated in order with their slot, group and block numbers
+  // shifted: the result does not depend on the thread count.
+  std::vector<BandLayout> parts(static_cast<size_t>(n_row_blocks));
+  std::atomic<int64_t> next{0};
+  auto work = [&] {
+    for (int64_t q = next.fetch_add(1); q < n_row_blocks; q = next.fetch_add(1)) {
+      const int64_t r0 = q * block_rows, r1 = std::min<int64_t>(n_rows, r0 + block_rows);
+      append_band_block(parts[q], rowptr, col, r0, r1, band_width, static_cast<int32_t>(n_bands),
+                        block_steps, fill);
+    }
+  };
+  run_on_threads(work, n_row_blocks);
+  int64_t n_slots = 0, n_groups = 0, n_blocks64 = 0;
+  for (const BandLayout& part : parts) {
+    n_slots += part.n_slots;
+    n_groups += part.n_groups;
+    n_blocks64 += static_cast<int64_t>(part.blocks.size() / 4);
   }
-  layout.wave_blocks.push_back(static_cast<int32_t>(layout.blocks.size() / 4));
-  const int32_t n_blocks = static_cast<int32_t>(layout.blocks.size() / 4);
-  // Sentinel group (no rows) and block record, then the tail padding: the
-  // kernel loads one block ahead and a whole register block of slots.
-  const int32_t sentinel[4] = {0, 0, 0, static_cast<int32_t>(layout.n_groups++)};
-  layout.blocks.insert(layout.blocks.end(), sentinel, sentinel + 4);
-  layout.n_slots += int64_t{kBandMaxBlockSteps} * 64;
+  if (n_slots + int64_t{kBandMaxBlockSteps} * 64 >= (int64_t{1} << 37) ||
+      n_blocks64 + 1 >= (int64_t{1} << 31) || n_groups + 1 >= (int64_t{1} << 31))
+    return fail("band layout needs too many slots");
+  const int32_t n_blocks = static_cast<int32_t>(n_blocks64);
+  // The sentinel group (no rows) and block record follow the row blocks, then
+  // the tail padding: the kernel loads one block ahead and a whole register
+  // block of slots.
+  const int32_t sentinel_group = static_cast<int32_t>(n_groups++);
+  n_slots += int64_t{kBandMaxBlockSteps} * 64;
   if (fill) {
-    layout.rows.insert(layout.rows.end(), 64, uint16_t{0xFFFF});
-    layout.perm.insert(layout.perm.end(), kBandMaxBlockSteps * 64, -1);
-    layout.col.insert(layout.col.end(), kBandMaxBlockSteps * 64, uint16_t{0xFFFF});
+    int64_t slot0 = 0, group0 = 0, block0 = 0;
+    int32_t* wb = wave_blocks;
+    for (const BandLayout& part : parts) {
+      for (int32_t w : part.wave_blocks) *wb++ = static_cast<int32_t>(w + block0);
+      for (size_t b = 0; b < part.blocks.size(); b += 4) {
+        int32_t* rec = blocks + 4 * block0 + b;
+        rec[0] = static_cast<int32_t>(part.blocks[b] + slot0 / 64);
+        rec[1] = part.blocks[b + 1];
+        rec[2] = part.blocks[b + 2];
+        rec[3] = static_cast<int32_t>(part.blocks[b + 3] + group0);
+      }
+      std::copy(part.rows.begin(), part.rows.end(), rows + 64 * group0);
+      std::copy(part.perm.begin(), part.perm.end(), perm + slot0);
+      std::copy(part.col.begin(), part.col.end(), col_out + slot0);
+      slot0 += part.n_slots;
+      group0 += part.n_groups;
+      block0 += static_cast<int64_t>(part.blocks.size() / 4);
+    }
+    *wb = n_blocks;
+    const int32_t sentinel[4] = {0, 0, 0, sentinel_group};
+    std::copy(sentinel, sentinel + 4, blocks + 4 * block0);
+    std::fill(rows + 64 * group0, rows + 64 * (group0 + 1), uint16_t{0xFFFF});
+    std::fill(perm + slot0, perm + slot0 + kBandMaxBlockSteps * 64, -1);
+    std::fill(col_out + slot0, col_out + slot0 + kBandMaxBlockSteps * 64, uint16_t{0xFFFF});
   }
   plan->band_width = band_width;
   plan->n_bands = static_cast<int32_t>(n_bands);
   plan->block_rows = block_rows;
   plan->n_row_blocks = static_cast<int32_t>(n_row_blocks);
   plan->n_blocks = n_blocks;
-  plan->n_groups = static_cast<int32_t>(layout.n_groups);
+  plan->n_groups = static_cast<int32_t>(n_groups);
   plan->block_steps = block_steps;
   plan->reserved = 0;
-  plan->n_slots = layout.n_slots;
-  if (fill) {
-    std::copy(layout.wave_blocks.begin(), layout.wave_blocks.end(), wave_blocks);
-    std::copy(layout.blocks.begin(), layout.blocks.end(), blocks);
-    std::copy(layout.rows.begin(), layout.rows.end(), rows);
-    std::copy(layout.perm.begin(), layout.perm.end(), perm);
-    std::copy(layout.col.begin(), layout.col.end(), col_out);
-  }
+  plan->n_slots = n_slots;
   return NS_OK;
 }
