@@ -75,6 +75,26 @@ namespace {
 // XCDs of the target (gfx950): the panel planner orders tiles for them.
 constexpr int64_t kXcds = 8;
 
+// Host threads a planner may use (the hosts this runs on give a process
+// about 16 cores).
+constexpr unsigned kPlanThreads = 16;
+
+// Runs `work` on min(kPlanThreads, hardware threads, items) threads, this one
+// included; `work` takes its items from a shared counter.  Without threads
+// (creation fails) it runs on this thread alone.
+template <typename Work>
+void run_on_threads(Work& work, int64_t items) {
+  const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+  const int64_t n = std::min<int64_t>({int64_t{kPlanThreads}, int64_t{hw}, std::max<int64_t>(items, 1)});
+  std::vector<std::thread> pool;
+  try {
+    for (int64_t t = 1; t < n; ++t) pool.emplace_back(std::ref(work));
+  } catch (const std::system_error&) {
+  }
+  work();
+  for (std::thread& t : pool) t.join();
+}
+
 // The sliced layout of one graph, in host vectors (built twice: size query, then fill).
 struct PanelLayout {
   int32_t panel_width = 0, n_panels = 0;
@@ -285,9 +305,44 @@ int build_panels(const int32_t* rowptr, const int32_t* col, int64_t n, int32_t m
   int64_t next = 0;
   for (int64_t x = 0; x < kXcds; ++x)
     for (int64_t k = x; k < nt; k += kXcds) slot_tile[k] = next++;
-  for (int64_t k = 0; k < nt; ++k) {
-    const Cut& c = cuts[slot_tile[k]];
-    append_tile(out, col, it, P, width, c.p, c.r0, c.r1, waves, lane_target, min_lg);
+  // Tiles are laid out independently, on up to kPlanThreads threads, then
+  // concatenated in emitted order with their slot, group and row numbers (and
+  // group-end bits) shifted: the result does not depend on the thread count.
+  std::vector<PanelLayout> parts(static_cast<size_t>(nt));
+  std::atomic<int64_t> next_tile{0};
+  auto work = [&] {
+    for (int64_t k = next_tile.fetch_add(1); k < nt; k = next_tile.fetch_add(1)) {
+      const Cut& c = cuts[slot_tile[k]];
+      append_tile(parts[k], col, it, P, width, c.p, c.r0, c.r1, waves, lane_target, min_lg);
+    }
+  };
+  run_on_threads(work, nt);
+  for (PanelLayout& part : parts) {
+    const int64_t slot0 = static_cast<int64_t>(out.perm.size());
+    const int64_t group0 = static_cast<int64_t>(out.groups.size() / 4);
+    const int64_t row0 = static_cast<int64_t>(out.rows.size());
+    if (slot0 + static_cast<int64_t>(part.perm.size()) >= (int64_t{1} << 31))
+      return fail("panel layout needs 2^31 or more slots");
+    const int32_t rec[4] = {part.tiles[0], part.tiles[1], part.tiles[2],
+                            static_cast<int32_t>(part.tiles[3] + row0)};
+    out.tiles.insert(out.tiles.end(), rec, rec + 4);
+    for (int32_t w : part.wave_groups) out.wave_groups.push_back(static_cast<int32_t>(w + group0));
+    for (size_t g = 0; g < part.groups.size(); g += 4) {
+      const int32_t rec_g[4] = {static_cast<int32_t>(part.groups[g] + slot0), part.groups[g + 1],
+                                part.groups[g + 2], static_cast<int32_t>(part.groups[g + 3] + row0)};
+      out.groups.insert(out.groups.end(), rec_g, rec_g + 4);
+    }
+    out.rows.insert(out.rows.end(), part.rows.begin(), part.rows.end());
+    out.perm.insert(out.perm.end(), part.perm.begin(), part.perm.end());
+    out.col.insert(out.col.end(), part.col.begin(), part.col.end());
+    for (size_t wd = 0; wd < part.last_steps.size(); ++wd)
+      for (uint32_t bits = part.last_steps[wd]; bits; bits &= bits - 1) {
+        const int64_t step = slot0 / 64 + static_cast<int64_t>(wd) * 32 + __builtin_ctz(bits);
+        if (static_cast<int64_t>(out.last_steps.size()) <= step / 32)
+          out.last_steps.resize(step / 32 + 1, 0u);
+        out.last_steps[step / 32] |= 1u << (step % 32);
+      }
+    part = PanelLayout();   // release the part's memory as it is copied
   }
   out.wave_groups.push_back(static_cast<int32_t>(out.groups.size() / 4));
   // Trailing padding: prefetches run up to two blocks of steps past a stream's end.
@@ -351,26 +406,6 @@ extern "C" int ns_plan_panels(const int32_t* rowptr, const int32_t* col, int64_t
 namespace {
 
 // The band layout of one graph, in host vectors (built twice: size query, then fill).
-// Host threads a planner may use (the hosts this runs on give a process
-// about 16 cores).
-constexpr unsigned kPlanThreads = 16;
-
-// Runs `work` on min(kPlanThreads, hardware threads, items) threads, this one
-// included; `work` takes its items from a shared counter.  Without threads
-// (creation fails) it runs on this thread alone.
-template <typename Work>
-void run_on_threads(Work& work, int64_t items) {
-  const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
-  const int64_t n = std::min<int64_t>({int64_t{kPlanThreads}, int64_t{hw}, std::max<int64_t>(items, 1)});
-  std::vector<std::thread> pool;
-  try {
-    for (int64_t t = 1; t < n; ++t) pool.emplace_back(std::ref(work));
-  } catch (const std::system_error&) {
-  }
-  work();
-  for (std::thread& t : pool) t.join();
-}
-
 struct BandLayout {
   int64_t n_groups = 0, n_slots = 0;
   std::vector<int32_t> wave_blocks, blocks, perm;
