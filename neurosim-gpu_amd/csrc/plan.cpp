@@ -79,6 +79,9 @@ constexpr int64_t kXcds = 8;
 // about 16 cores).
 constexpr unsigned kPlanThreads = 16;
 
+// Rows per work item of the planners' row-parallel passes.
+constexpr int64_t kPlanRowChunk = 4096;
+
 // Runs `work` on min(kPlanThreads, hardware threads, items) threads, this one
 // included; `work` takes its items from a shared counter.  Without threads
 // (creation fails) it runs on this thread alone.
@@ -216,20 +219,34 @@ int build_panels(const int32_t* rowptr, const int32_t* col, int64_t n, int32_t m
   out.n_panels = static_cast<int32_t>((n + width - 1) / width);
   const int32_t P = out.n_panels;
 
+  // Rows are independent below: chunks of kPlanRowChunk rows go to up to
+  // kPlanThreads threads, and each row writes only its own ranges.
+  const int64_t n_chunks = (n + kPlanRowChunk - 1) / kPlanRowChunk;
+  auto for_rows = [&](auto&& body) {
+    std::atomic<int64_t> next_chunk{0};
+    auto work = [&] {
+      for (int64_t q = next_chunk.fetch_add(1); q < n_chunks; q = next_chunk.fetch_add(1))
+        for (int64_t r = q * kPlanRowChunk; r < std::min(n, (q + 1) * kPlanRowChunk); ++r) body(r);
+    };
+    run_on_threads(work, n_chunks);
+  };
+
   // Each row's edges grouped by panel (stable counting sort).
-  std::vector<int32_t> order(m), bucket(n * (P + 1), 0), fill(P);
-  for (int64_t r = 0; r < n; ++r) {
+  std::vector<int32_t> order(m), bucket(n * (P + 1), 0);
+  std::atomic<int64_t> bad_col{-1};
+  for_rows([&](int64_t r) {
     int32_t* b = &bucket[r * (P + 1)];
     for (int64_t e = rowptr[r]; e < rowptr[r + 1]; ++e) {
       const int64_t c = col[e];
-      if (c < 0 || c >= n) return fail("CSR column %lld out of range", (long long)c);
+      if (c < 0 || c >= n) { bad_col.store(c); return; }
       ++b[c / width + 1];
     }
     for (int32_t p = 0; p < P; ++p) b[p + 1] += b[p];
-    for (int32_t p = 0; p < P; ++p) fill[p] = b[p];
+    std::vector<int32_t> fill(b, b + P);
     for (int64_t e = rowptr[r]; e < rowptr[r + 1]; ++e)
       order[rowptr[r] + fill[col[e] / width]++] = static_cast<int32_t>(e);
-  }
+  });
+  if (bad_col.load() != -1) return fail("CSR column %lld out of range", (long long)bad_col.load());
 
   // Items.  Plain layouts: the edges as grouped above.  Pair layouts: within
   // each (row, panel) segment the edges grouped by 16-edge weight block (stable,
@@ -243,26 +260,45 @@ int build_panels(const int32_t* rowptr, const int32_t* col, int64_t n, int32_t m
     it.bucket = std::move(bucket);
     for (int64_t r = 0; r <= n; ++r) it.base[r] = rowptr[r];
   } else {
+    // Per row: its segments regrouped by weight block into `regrouped` (in
+    // place of `order`) with the padded length of each segment in it.bucket;
+    // then the rows' item ranges by a prefix sum, and the items written.
     it.bucket.assign(n * (P + 1), 0);
-    it.items.reserve(m + m / 8 + 16);
-    std::vector<int32_t> seg;
-    for (int64_t r = 0; r < n; ++r) {
-      it.base[r] = static_cast<int64_t>(it.items.size());
+    std::vector<int32_t> regrouped(m);
+    for_rows([&](int64_t r) {
       const int32_t* b = &bucket[r * (P + 1)];
       int32_t* ib = &it.bucket[r * (P + 1)];
+      int32_t* seg = &regrouped[rowptr[r]];
+      std::copy(order.begin() + rowptr[r], order.begin() + rowptr[r + 1], seg);
+      int32_t padded = 0;
       for (int32_t p = 0; p < P; ++p) {
-        seg.assign(order.begin() + rowptr[r] + b[p], order.begin() + rowptr[r] + b[p + 1]);
-        std::stable_sort(seg.begin(), seg.end(), [](int32_t x, int32_t y) { return (x >> 4) < (y >> 4); });
-        for (size_t i = 0; i < seg.size();) {
-          size_t j = i;
-          while (j < seg.size() && (seg[j] >> 4) == (seg[i] >> 4)) it.items.push_back(seg[j++]);
-          if ((j - i) % 2) it.items.push_back(-1);
+        std::stable_sort(seg + b[p], seg + b[p + 1],
+                         [](int32_t x, int32_t y) { return (x >> 4) < (y >> 4); });
+        for (int32_t i = b[p]; i < b[p + 1];) {
+          int32_t j = i;
+          while (j < b[p + 1] && (seg[j] >> 4) == (seg[i] >> 4)) ++j;
+          padded += (j - i) + ((j - i) % 2);
           i = j;
         }
-        ib[p + 1] = static_cast<int32_t>(static_cast<int64_t>(it.items.size()) - it.base[r]);
+        ib[p + 1] = padded;
       }
-    }
-    it.base[n] = static_cast<int64_t>(it.items.size());
+    });
+    it.base[0] = 0;
+    for (int64_t r = 0; r < n; ++r) it.base[r + 1] = it.base[r] + it.bucket[r * (P + 1) + P];
+    it.items.assign(static_cast<size_t>(it.base[n]), -1);
+    for_rows([&](int64_t r) {
+      const int32_t* b = &bucket[r * (P + 1)];
+      const int32_t* seg = &regrouped[rowptr[r]];
+      int32_t* out_items = &it.items[it.base[r]];
+      int32_t k = 0;
+      for (int32_t p = 0; p < P; ++p)
+        for (int32_t i = b[p]; i < b[p + 1];) {
+          int32_t j = i;
+          while (j < b[p + 1] && (seg[j] >> 4) == (seg[i] >> 4)) out_items[k++] = seg[j++];
+          if ((j - i) % 2) out_items[k++] = -1;
+          i = j;
+        }
+    });
   }
   const int32_t min_lg = pairs ? 1 : 0;
 
