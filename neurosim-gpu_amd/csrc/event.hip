@@ -202,6 +202,19 @@ extern "C" int ns_dendritic_event(const ns_event_args* args, void* stream) {
   if (!a.state.data || !a.dendrite.data || !a.adaptation.data || !a.emitted.data)
     return fail("state, dendrite, adaptation and emitted data are required");
   if (!a.current) return fail("persistent current is required");
+  {
+    // The current is updated in place, one element per (b, n): no two pairs
+    // may share an element (a zero stride, or strides that interleave).
+    const int64_t B = a.batch, N = a.n_neurons;
+    const int64_t sb = a.current_stride_b < 0 ? -a.current_stride_b : a.current_stride_b;
+    const int64_t sn = a.current_stride_n < 0 ? -a.current_stride_n : a.current_stride_n;
+    const bool distinct = B == 1 ? (N == 1 || sn > 0)
+                          : N == 1 ? sb > 0
+                                   : (sn > 0 && sb >= N * sn) || (sb > 0 && sn >= B * sb);
+    if (!distinct)
+      return fail("the persistent current must not overlap itself (strides %lld, %lld)",
+                  (long long)a.current_stride_b, (long long)a.current_stride_n);
+  }
   if (!a.out_state.data || !a.out_dendrite.data || !a.out_adaptation.data ||
       !a.out_emitted.data)
     return fail("four output planes are required");

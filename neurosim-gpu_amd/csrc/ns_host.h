@@ -10,20 +10,9 @@
 #include <cstdio>
 
 #include "ns_common.h"
+#include "ns_error.h"
 
 namespace ns {
-
-char* error_buffer();
-
-inline void clear_error() { error_buffer()[0] = '\0'; }
-
-__attribute__((format(printf, 1, 2))) inline int fail(const char* fmt, ...) {
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(error_buffer(), 512, fmt, ap);
-  va_end(ap);
-  return NS_ERR_INVALID;
-}
 
 inline int fail_launch(const char* what, hipError_t err) {
   snprintf(error_buffer(), 512, "%s launch failed: %s", what, hipGetErrorString(err));

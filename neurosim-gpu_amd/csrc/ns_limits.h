@@ -1,0 +1,21 @@
+// Launch geometry shared by the kernels and the host-side planners (plain
+// C++: the planners compile without the HIP headers).
+#pragma once
+
+namespace ns {
+
+constexpr int kThreads = 256;   // 4 wavefronts of 64 lanes
+constexpr int kMaxRows = 256;   // rows per row block (one lane per row at most density)
+
+// Column-panel kernel (batch widths 1 and 2): 16 wavefronts per workgroup
+// stream their own runs of 64-lane steps; a slot stream ends with
+// kPanelTailSlots padding slots so prefetches may run past a stream's end.
+constexpr int kPanelWaves = 16;
+constexpr int kPanelThreads = kPanelWaves * 64;
+constexpr int kPanelMaxPrefetch = 16;                  // steps per register block, at most
+constexpr int kPanelTailSlots = 2 * kPanelMaxPrefetch * 64;
+constexpr int kBandWaves = 4;                           // wavefronts per band workgroup
+constexpr int kBandMaxBlockRows = 2496;                 // 16 float row sums each in LDS (156 KB)
+constexpr int kBandMaxBlockSteps = 8;                   // steps per register block, at most
+
+}  // namespace ns

@@ -492,12 +492,19 @@ int panel_step(const ns_step_args& a, hipStream_t stream) {
   if (reinterpret_cast<uintptr_t>(pl.col) % 2 || reinterpret_cast<uintptr_t>(pl.weight) % need)
     return fail("panel arrays are misaligned");
   {
-    const Extent part = extent_of(pl.partials, 1, 1, 1, 2 * int64_t{pl.n_panels} * a.n_neurons * a.batch);
-    const Extent outs[3] = {extent(a.out_state, a.batch, a.n_neurons),
-                            extent(a.out_dendrite, a.batch, a.n_neurons),
-                            extent(a.out_adaptation, a.batch, a.n_neurons)};
-    for (const Extent& o : outs)
-      if (overlaps(part, o)) return fail("the partials workspace overlaps an output");
+    // Tiles write partial sums while other workgroups still read the state and
+    // drives, so the workspace may overlap no operand at all.
+    const int64_t B = a.batch, N = a.n_neurons;
+    const Extent part = extent_of(pl.partials, 1, 1, 1, 2 * int64_t{pl.n_panels} * N * B);
+    const Extent others[9] = {extent(a.out_state, B, N), extent(a.out_dendrite, B, N),
+                              extent(a.out_adaptation, B, N), extent(a.out_current, B, N),
+                              extent(a.state, B, N), extent(a.dendrite, B, N),
+                              extent(a.adaptation, B, N), extent(a.drive, B, N),
+                              extent(a.dendritic_drive, B, N)};
+    for (int i = 0; i < 9; ++i)
+      if (overlaps(part, others[i]))
+        return fail(i < 4 ? "the partials workspace overlaps an output"
+                          : "the partials workspace overlaps an input");
   }
 
   PanelArgs A{};

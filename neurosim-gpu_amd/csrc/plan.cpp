@@ -9,9 +9,11 @@
 #include <system_error>
 #include <thread>
 #include <cstdio>
+#include <cstdlib>
 #include <vector>
 
-#include "ns_host.h"
+#include "ns_error.h"
+#include "ns_limits.h"
 
 namespace ns {
 
@@ -82,13 +84,26 @@ constexpr unsigned kPlanThreads = 16;
 // Rows per work item of the planners' row-parallel passes.
 constexpr int64_t kPlanRowChunk = 4096;
 
-// Runs `work` on min(kPlanThreads, hardware threads, items) threads, this one
-// included; `work` takes its items from a shared counter.  Without threads
-// (creation fails) it runs on this thread alone.
+// Host threads the planners use: min(kPlanThreads, hardware threads), or the
+// positive value of NEUROSIM_PLAN_THREADS (capped at kPlanThreads).  Layouts do
+// not depend on it; the variable exists so that a one-thread build of a plan
+// can be compared with a threaded one.
+int64_t plan_threads() {
+  const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+  int64_t n = std::min<int64_t>(kPlanThreads, hw);
+  if (const char* env = std::getenv("NEUROSIM_PLAN_THREADS")) {
+    const long v = std::strtol(env, nullptr, 10);
+    if (v > 0) n = std::min<int64_t>(kPlanThreads, v);
+  }
+  return n;
+}
+
+// Runs `work` on min(plan_threads(), items) threads, this one included;
+// `work` takes its items from a shared counter.  Without threads (creation
+// fails) it runs on this thread alone.
 template <typename Work>
 void run_on_threads(Work& work, int64_t items) {
-  const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
-  const int64_t n = std::min<int64_t>({int64_t{kPlanThreads}, int64_t{hw}, std::max<int64_t>(items, 1)});
+  const int64_t n = std::min<int64_t>(plan_threads(), std::max<int64_t>(items, 1));
   std::vector<std::thread> pool;
   try {
     for (int64_t t = 1; t < n; ++t) pool.emplace_back(std::ref(work));
@@ -136,7 +151,7 @@ void append_tile(PanelLayout& out, const int32_t* col, const Items& it, int32_t 
   const int64_t nr = r1 - r0;
   const std::vector<int32_t>& bucket = it.bucket;
   auto seg_len = [&](int64_t r) -> int64_t {
-    const int32_t* b = &bucket[r * (P + 1)];
+    const int32_t* b = bucket.data() + r * (P + 1);
     return b[p + 1] - b[p];
   };
   std::vector<int32_t> sorted(nr);
@@ -221,6 +236,9 @@ int build_panels(const int32_t* rowptr, const int32_t* col, int64_t n, int32_t m
 
   // Rows are independent below: chunks of kPlanRowChunk rows go to up to
   // kPlanThreads threads, and each row writes only its own ranges.
+  // Each row's edges grouped by panel (stable counting sort).
+  // Columns are checked first, on all rows: the passes below index by them.
+  // The first offending edge (lowest index) is reported, whatever the threads.
   const int64_t n_chunks = (n + kPlanRowChunk - 1) / kPlanRowChunk;
   auto for_rows = [&](auto&& body) {
     std::atomic<int64_t> next_chunk{0};
@@ -230,23 +248,29 @@ int build_panels(const int32_t* rowptr, const int32_t* col, int64_t n, int32_t m
     };
     run_on_threads(work, n_chunks);
   };
-
-  // Each row's edges grouped by panel (stable counting sort).
-  std::vector<int32_t> order(m), bucket(n * (P + 1), 0);
-  std::atomic<int64_t> bad_col{-1};
+  constexpr int64_t kNoEdge = INT64_MAX;
+  std::atomic<int64_t> bad_edge{kNoEdge};
   for_rows([&](int64_t r) {
-    int32_t* b = &bucket[r * (P + 1)];
-    for (int64_t e = rowptr[r]; e < rowptr[r + 1]; ++e) {
-      const int64_t c = col[e];
-      if (c < 0 || c >= n) { bad_col.store(c); return; }
-      ++b[c / width + 1];
-    }
+    for (int64_t e = rowptr[r]; e < rowptr[r + 1]; ++e)
+      if (col[e] < 0 || col[e] >= n) {
+        int64_t seen = bad_edge.load();
+        while (e < seen && !bad_edge.compare_exchange_weak(seen, e)) {
+        }
+        return;
+      }
+  });
+  if (const int64_t e = bad_edge.load(); e != kNoEdge)
+    return fail("CSR column %lld out of range (edge %lld)", (long long)col[e], (long long)e);
+
+  std::vector<int32_t> order(m), bucket(n * (P + 1), 0);
+  for_rows([&](int64_t r) {
+    int32_t* b = bucket.data() + r * (P + 1);
+    for (int64_t e = rowptr[r]; e < rowptr[r + 1]; ++e) ++b[col[e] / width + 1];
     for (int32_t p = 0; p < P; ++p) b[p + 1] += b[p];
     std::vector<int32_t> fill(b, b + P);
     for (int64_t e = rowptr[r]; e < rowptr[r + 1]; ++e)
       order[rowptr[r] + fill[col[e] / width]++] = static_cast<int32_t>(e);
   });
-  if (bad_col.load() != -1) return fail("CSR column %lld out of range", (long long)bad_col.load());
 
   // Items.  Plain layouts: the edges as grouped above.  Pair layouts: within
   // each (row, panel) segment the edges grouped by 16-edge weight block (stable,
@@ -266,9 +290,9 @@ int build_panels(const int32_t* rowptr, const int32_t* col, int64_t n, int32_t m
     it.bucket.assign(n * (P + 1), 0);
     std::vector<int32_t> regrouped(m);
     for_rows([&](int64_t r) {
-      const int32_t* b = &bucket[r * (P + 1)];
-      int32_t* ib = &it.bucket[r * (P + 1)];
-      int32_t* seg = &regrouped[rowptr[r]];
+      const int32_t* b = bucket.data() + r * (P + 1);
+      int32_t* ib = it.bucket.data() + r * (P + 1);
+      int32_t* seg = regrouped.data() + rowptr[r];
       std::copy(order.begin() + rowptr[r], order.begin() + rowptr[r + 1], seg);
       int32_t padded = 0;
       for (int32_t p = 0; p < P; ++p) {
@@ -287,9 +311,9 @@ int build_panels(const int32_t* rowptr, const int32_t* col, int64_t n, int32_t m
     for (int64_t r = 0; r < n; ++r) it.base[r + 1] = it.base[r] + it.bucket[r * (P + 1) + P];
     it.items.assign(static_cast<size_t>(it.base[n]), -1);
     for_rows([&](int64_t r) {
-      const int32_t* b = &bucket[r * (P + 1)];
-      const int32_t* seg = &regrouped[rowptr[r]];
-      int32_t* out_items = &it.items[it.base[r]];
+      const int32_t* b = bucket.data() + r * (P + 1);
+      const int32_t* seg = regrouped.data() + rowptr[r];
+      int32_t* out_items = it.items.data() + it.base[r];
       int32_t k = 0;
       for (int32_t p = 0; p < P; ++p)
         for (int32_t i = b[p]; i < b[p + 1];) {
@@ -478,7 +502,7 @@ void append_band_block(BandLayout& out, const int32_t* rowptr, const int32_t* co
     int64_t total = 0;
     for (int64_t i = 0; i < nw; ++i) {
       const int64_t r = r0 + rows_w[i];
-      int32_t* st = &start[i * (n_bands + 1)];
+      int32_t* st = start.data() + i * (n_bands + 1);
       for (int64_t e = rowptr[r]; e < rowptr[r + 1]; ++e) ++st[col[e] / band_width + 1];
       for (int32_t k = 0; k < n_bands; ++k) st[k + 1] += st[k];
       total += rowptr[r + 1] - rowptr[r];
@@ -491,7 +515,7 @@ void append_band_block(BandLayout& out, const int32_t* rowptr, const int32_t* co
       std::vector<int32_t> at(n_bands);
       for (int64_t i = 0; i < nw; ++i) {
         const int64_t r = r0 + rows_w[i];
-        const int32_t* st = &start[i * (n_bands + 1)];
+        const int32_t* st = start.data() + i * (n_bands + 1);
         for (int32_t k = 0; k < n_bands; ++k) at[k] = st[k];
         for (int64_t e = rowptr[r]; e < rowptr[r + 1]; ++e)
           order[row_base[i] + at[col[e] / band_width]++] = static_cast<int32_t>(e);
@@ -500,7 +524,7 @@ void append_band_block(BandLayout& out, const int32_t* rowptr, const int32_t* co
     std::vector<int32_t> cand;
     for (int32_t k = 0; k < n_bands; ++k) {
       auto seg_len = [&](int32_t i) -> int32_t {
-        const int32_t* st = &start[static_cast<int64_t>(i) * (n_bands + 1)];
+        const int32_t* st = start.data() + static_cast<int64_t>(i) * (n_bands + 1);
         return st[k + 1] - st[k];
       };
       cand.clear();

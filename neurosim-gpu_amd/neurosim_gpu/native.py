@@ -548,6 +548,10 @@ class PanelLayout(_SlotLayout):
         plan.weight = slot_weight.data_ptr()
         plan.slot_scales = slot_scales.data_ptr() if slot_scales is not None else None
         plan.partials = self.partials.data_ptr()
+        # The struct holds raw pointers: it keeps what they point at alive, so a
+        # launch captured with it (a rollout's graph) stays valid after the
+        # layout has moved on to other weights.
+        plan._tensors = (self, slot_weight, slot_scales)
         return plan
 
 
@@ -608,6 +612,7 @@ class BandLayout(_SlotLayout):
         plan.rows, plan.col = self.rows.data_ptr(), self.col.data_ptr()
         plan.weight = slot_weight.data_ptr()
         plan.slot_scales = slot_scales.data_ptr() if slot_scales is not None else None
+        plan._tensors = (self, slot_weight, slot_scales)   # kept alive with the pointers
         return plan
 
 
@@ -888,12 +893,19 @@ class NativeExtension:
         return out
 
 
-class TickLauncher:
-    """A prepared fused tick: fixed weights, plan, parameters and drives.
+def drive_plane(value: torch.Tensor, state_like: torch.Tensor) -> _Plane:
+    """The plane of a [B,N]-broadcastable float32 drive tensor (validated)."""
+    view = value.expand_as(state_like)
+    return _plane(view, state_like, "drive")
 
-    Only the input/output state planes change between launches, so a
-    multi-tick loop does no validation or allocation per tick and can be
-    captured into one HIP graph.  Keeps every tensor it points at alive.
+
+class TickLauncher:
+    """A prepared fused tick: fixed weights, plan and parameters.
+
+    Only the state planes (and, if given per call, the drive planes) change
+    between launches, so a multi-tick loop does no validation or allocation per
+    tick and can be captured into one HIP graph.  Keeps every tensor it points
+    at alive; drive planes passed per call must be kept alive by the caller.
     """
 
     def __init__(self, extension: "NativeExtension", state_like: torch.Tensor, params, rowptr,
@@ -913,6 +925,8 @@ class TickLauncher:
         args.drive = _drive(drive_t, 0.0 if drive_t is not None else float(drive), state_like)
         args.dendritic_drive = _drive(ddrive_t, 0.0 if ddrive_t is not None
                                       else float(dendritic_drive), state_like)
+        self.fixed_drives = (_Plane.from_buffer_copy(args.drive),
+                             _Plane.from_buffer_copy(args.dendritic_drive))
         batch, n = state_like.shape
         args.n_neurons, args.batch = n, batch
         bounds = None
@@ -931,9 +945,16 @@ class TickLauncher:
         self._keep = (list(params), rowptr, col, weight, drive_t, ddrive_t, block_scales,
                       global_scale, bounds, panels, bands)
 
-    def __call__(self, source: tuple, target: tuple, stream: int | None = None) -> None:
-        """One tick from planes (s, d, a) into planes (s', d', a') (all [B,N] views)."""
+    def __call__(self, source: tuple, target: tuple, stream: int | None = None,
+                 drives: tuple | None = None) -> None:
+        """One tick from planes (s, d, a) into planes (s', d', a') (all [B,N] views).
+        ``drives`` optionally replaces the two drive planes for this launch:
+        (somatic, dendritic) ``_Plane`` structs (see ``drive_plane``), None for
+        the one fixed at construction."""
         args = self.args
+        somatic, dendritic = drives if drives is not None else (None, None)
+        args.drive = somatic if somatic is not None else self.fixed_drives[0]
+        args.dendritic_drive = dendritic if dendritic is not None else self.fixed_drives[1]
         args.state = _Plane(source[0].data_ptr(), source[0].stride(0), source[0].stride(1), 0.0)
         args.dendrite = _Plane(source[1].data_ptr(), source[1].stride(0), source[1].stride(1), 0.0)
         args.adaptation = _Plane(source[2].data_ptr(), source[2].stride(0), source[2].stride(1),

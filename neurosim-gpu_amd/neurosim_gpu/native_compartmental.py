@@ -493,6 +493,12 @@ class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
         u, us = self._drive(drive)
         v, vs = self._drive(dendritic_drive)
         self._refresh_current()
+        # The tick updates the current in place, one element per (column,
+        # neuron): an assigned view (expanded, strided) is replaced by a dense
+        # copy first, as in the reference (native_compartmental.py:164).  The
+        # pending buffers are separate, so nothing outstanding is lost.
+        if not self._current.is_contiguous():
+            self._current = self._current.contiguous()
         if self._pending is not None:
             # pending[parity] holds the last tick's scatter (or zeros); the other is zero.
             extra = {"pending": (self._pending[self._parity], self._pending[1 - self._parity])}

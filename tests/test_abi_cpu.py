@@ -338,5 +338,42 @@ def test_event_validation_messages(lib):
         args.pending_out = buffers[pending_out].ctypes.data
         rc, text = call(args)
         assert rc != 0 and message in text, text
+    for strides in ((0, 1), (1, 1), (4, 1), (1, 0)):         # zero or interleaved strides
+        args, keep = fake_event_args()
+        args.current_stride_b, args.current_stride_n = strides
+        rc, text = call(args)
+        assert rc != 0 and "must not overlap itself" in text, (strides, text)
     args, keep = fake_event_args(batch=0)
     assert call(args) == (0, "")
+
+
+def fake_panel_plan(n, batch):
+    """A structurally valid one-panel plan over host arrays (validation only)."""
+    tables = [np.zeros(4, np.int32), np.zeros(17, np.int32), np.zeros(4, np.int32),
+              np.zeros(1, np.uint16), np.zeros(4, np.uint32), np.zeros(2048, np.uint16),
+              np.zeros(2048, np.float32), np.zeros(2 * n * batch, np.float32)]
+    plan = native._PanelPlan()
+    plan.panel_width, plan.n_panels, plan.n_tiles, plan.n_groups = max(4, -(-n // 4) * 4), 1, 1, 0
+    plan.waves, plan.flags, plan.n_slots, plan.n_step_words = 16, 0, 2048, 4
+    (plan.tiles, plan.wave_groups, plan.groups, plan.rows, plan.last_steps, plan.col,
+     plan.weight, plan.partials) = (t.ctypes.data for t in tables)
+    return plan, tables
+
+
+def test_panel_workspace_must_not_overlap_any_operand(lib):
+    """Tiles write the partials workspace while other workgroups still read the
+    state and drives: an overlap with any input or output is rejected."""
+    n, batch = 8, 1
+    for field in ("state", "dendrite", "adaptation", "drive", "dendritic_drive",
+                  "out_state", "out_current"):
+        args, keep = fake_step_args(n=n, batch=batch)
+        plan, tables = fake_panel_plan(n, batch)
+        args.panels = ctypes.addressof(plan)
+        workspace = tables[-1].ctypes.data
+        if field.startswith("out_"):
+            setattr(args, field, native._OutPlane(workspace, n, 1))
+        else:
+            setattr(args, field, native._Plane(workspace, n, 1, 0.0))
+        rc, text = call(lib, args)
+        kind = "output" if field.startswith("out_") else "input"
+        assert rc != 0 and f"partials workspace overlaps an {kind}" in text, (field, text)

@@ -193,3 +193,19 @@ def test_band_planner_rejects_bad_arguments():
     bad_col[3] = 100
     assert "out of range" in rc(c=bad_col)[1]
     assert "N must be" in rc(n=0)[1]
+    bad_col[3] = -1
+    assert "out of range" in rc(c=bad_col)[1]
+
+
+def test_band_plan_does_not_depend_on_thread_count(monkeypatch):
+    """Row blocks are laid out on up to 16 host threads and concatenated in order."""
+    rowptr, col = random_csr(40_000, 400_000, 9, ((5, 3000),))
+    plans = []
+    for threads in ("1", "16"):
+        monkeypatch.setenv("NEUROSIM_PLAN_THREADS", threads)
+        plans.append(plan_bands_host(torch.from_numpy(rowptr), torch.from_numpy(col), 4096, 300, 4))
+    one, many = plans
+    for field in ("n_bands", "n_row_blocks", "n_blocks", "n_groups", "n_slots"):
+        assert getattr(one[0], field) == getattr(many[0], field)
+    for x, y in zip(one[1:], many[1:]):
+        assert np.array_equal(x, y)

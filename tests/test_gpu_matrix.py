@@ -17,7 +17,7 @@ from cases import column_drive, make_case, max_err, model_to, standard_model
 from oracle import precision as op
 from oracle import runtime as ort
 from oracle import topology as otop
-from neurosim_gpu import (NativeDendriticMatrixRuntime, NativeDendriticPELSRuntime,
+from neurosim_gpu import (MatrixRollout, NativeDendriticMatrixRuntime, NativeDendriticPELSRuntime,
                           SparseTopology, encode_sparse_weights, load_native_extension,
                           random_topology, topology_to)
 
@@ -231,15 +231,22 @@ def test_cfg2_batched_fp32_1000_ticks(gpu):
     native = NativeDendriticMatrixRuntime(case.topology, case.model, torch.zeros(8, 50_000, device=gpu))
     oracle = ort.MatrixOracle(case.graph, case.params, torch.zeros(8, 50_000))
     drive_gpu = drive.to(gpu)
-    worst = 0.0
+    # The timed path as well: 100-tick graph replays, checked at every chunk end.
+    rolled = NativeDendriticMatrixRuntime(case.topology, case.model,
+                                          torch.zeros(8, 50_000, device=gpu))
+    rollout = MatrixRollout(rolled, 100, drive=drive_gpu, dendritic_drive=0.1)
+    worst = worst_rollout = 0.0
     for tick in range(1000):
         native.step(drive_gpu, dendritic_drive=0.1)
         oracle.step(drive, 0.1)
         if tick % 10 == 9:
             worst = max(worst, errors(native, oracle))
+        if tick % 100 == 99:
+            rollout.run()
+            worst_rollout = max(worst_rollout, errors(rollout, oracle))
     worst = max(worst, errors(native, oracle))
-    print(f"cfg2 max abs error over 1000 ticks: {worst:.3e}")
-    assert worst <= 1e-5
+    print(f"cfg2 max abs error over 1000 ticks: eager {worst:.3e}, graph chunks {worst_rollout:.3e}")
+    assert worst <= 1e-5 and worst_rollout <= 1e-5
 
 
 @pytest.mark.parametrize("fmt", ["fp8", "nvfp4"])
@@ -286,15 +293,23 @@ def test_cfg3_large_1000_ticks(gpu, large_case, fmt):
                                           torch.zeros(1, 166_000, device=gpu), **kwargs)
     in_weight = op.quantize_dequantize(case.graph.in_weight, fmt)
     oracle = ort.MatrixOracle(case.graph, case.params, torch.zeros(1, 166_000), in_weight=in_weight)
-    worst = 0.0
+    # The path bench.py times: 100-tick graph replays, checked at every chunk end.
+    rolled = NativeDendriticMatrixRuntime(case.topology, case.model,
+                                          torch.zeros(1, 166_000, device=gpu), **kwargs)
+    rollout = MatrixRollout(rolled, 100, drive=0.2, dendritic_drive=0.1)
+    worst = worst_rollout = 0.0
     with torch.inference_mode():
         for tick in range(1000):
             native.step(0.2, dendritic_drive=0.1)
             oracle.step(0.2, 0.1)
             if tick % 50 == 49:
                 worst = max(worst, errors(native, oracle))
-    print(f"cfg3 {fmt} max abs error over 1000 ticks: {worst:.3e}")
-    assert worst <= 1e-5
+            if tick % 100 == 99:
+                rollout.run()
+                worst_rollout = max(worst_rollout, errors(rollout, oracle))
+    print(f"cfg3 {fmt} max abs error over 1000 ticks: eager {worst:.3e}, "
+          f"graph chunks {worst_rollout:.3e}")
+    assert worst <= 1e-5 and worst_rollout <= 1e-5
 
 
 def test_cfg5_scaleout_fp8_10_ticks(gpu):
@@ -322,11 +337,15 @@ def test_cfg5_scaleout_fp8_10_ticks(gpu):
     oracle = ort.MatrixOracle(graph, params, torch.zeros(batch, n),
                               in_weight=op.quantize_dequantize(graph.in_weight, "fp8"))
     drive = column_drive(batch)
+    # The timed path as well: one 10-tick graph replay from the same zero state.
+    rollout = MatrixRollout(native, 10, drive=drive.to(gpu), dendritic_drive=0.1)
     worst = 0.0
     with torch.inference_mode():
         for _ in range(10):
             native.step(drive.to(gpu), dendritic_drive=0.1)
             oracle.step(drive, 0.1)
             worst = max(worst, errors(native, oracle))
-    print(f"cfg5 fp8 max abs error over 10 ticks: {worst:.3e}")
-    assert worst <= 1e-5
+        rollout.run()
+        worst_rollout = errors(rollout, oracle)
+    print(f"cfg5 fp8 max abs error over 10 ticks: eager {worst:.3e}, graph {worst_rollout:.3e}")
+    assert worst <= 1e-5 and worst_rollout <= 1e-5

@@ -194,3 +194,45 @@ def test_planner_rejects_bad_geometry():
     rc = lib.ns_plan_panels(rowptr.ctypes.data, col.ctypes.data, 2, 64, 1, 16, 12, 2,
                             ctypes.byref(plan), ctypes.byref(entries), *([None] * 7))
     assert rc != 0 and b"flags" in lib.ns_last_error()
+
+
+@pytest.mark.parametrize("flags", [0, 1])
+@pytest.mark.parametrize("rowptr,col,bad", [
+    ([0, 1, 2], [0, -1], -1),                                  # -1: no longer a 'no error' value
+    ([0, 1, 2], [-7, 1], -7),
+    ([0] + list(range(5, 5 * 13, 5)), [4, 4, 4, 8, -1] * 12, -1),   # 12 rows, several panels
+])
+def test_planner_rejects_negative_and_large_columns(flags, rowptr, col, bad):
+    import ctypes
+
+    from neurosim_gpu import native
+
+    lib = native.load_library()
+    rowptr = np.asarray(rowptr, np.int32)
+    n = rowptr.size - 1
+    col = np.asarray(col, np.int32)
+    plan = native._PanelPlan()
+    entries = native._c_i64()
+    rc = lib.ns_plan_panels(rowptr.ctypes.data, col.ctypes.data, n, 4, 1, 16, 12, flags,
+                            ctypes.byref(plan), ctypes.byref(entries), *([None] * 7))
+    message = lib.ns_last_error()
+    assert rc != 0 and b"out of range" in message
+    first = int(np.flatnonzero((col < 0) | (col >= n))[0])
+    assert f"column {bad} out of range (edge {first})".encode() in message
+
+
+@pytest.mark.parametrize("pairs", [False, True])
+def test_panel_plan_does_not_depend_on_thread_count(monkeypatch, pairs):
+    """Rows are laid out in chunks of 4096 on up to 16 host threads; a graph of
+    many chunks must give the same plan as a one-thread build."""
+    graph = hub_graph(70_000, 5)
+    plans = []
+    for threads in ("1", "16"):
+        monkeypatch.setenv("NEUROSIM_PLAN_THREADS", threads)
+        plans.append(plan_panels_host(torch.from_numpy(graph.in_rowptr),
+                                      torch.from_numpy(graph.in_col), 1, 37, 4000, pairs=pairs))
+    one, many = plans
+    for field in ("panel_width", "n_panels", "n_tiles", "n_groups", "n_slots", "n_step_words"):
+        assert getattr(one[0], field) == getattr(many[0], field)
+    for x, y in zip(one[1:], many[1:]):
+        assert np.array_equal(x, y)
