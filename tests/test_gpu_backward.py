@@ -1,13 +1,14 @@
 """Native float32 backward of the matrix tick (ns_dendritic_step_backward)
-against autograd through the PyTorch reference step.
+against the oracle's gradients.
 
 The reference's native runtime records no graph of its own: whenever a
 gradient is needed it runs its torch step (native_compartmental.py:104-108),
 and autograd differentiates torch.sparse.mm and the update ops.  Here the
-same gradients come from HIP kernels.  The reference for the comparison is
-that torch step run by autograd in float64 on the CPU on the same inputs, so
-the tolerance (1e-4 of the largest gradient of each tensor) covers only the
-native float32 arithmetic.  Covers one tick with every input requiring a
+same gradients come from HIP kernels.  The expected values come from
+oracle/grad.py: float64 autograd through the oracle's update on the dense
+weight matrix, pinned by finite differences (tests/test_oracle_grad.py), on
+the same float32 inputs, so the tolerance (1e-4 of the largest gradient of
+each tensor) covers only the native float32 arithmetic.  Covers one tick with every input requiring a
 gradient (states, [B,N] and [B,1] drives, the six parameters, the weights),
 eight-tick backpropagation through time, scalar drives, stride-0 parameters,
 repeatability, and the source-major weight copy the transposed product streams
@@ -20,9 +21,10 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import grad as og
 from oracle import topology as otop
-from neurosim_gpu import (DendriticDynamics, DendriticMatrixRuntime, Dynamics,
-                          NativeDendriticMatrixRuntime, SparseTopology)
+from neurosim_gpu import (DendriticDynamics, Dynamics, NativeDendriticMatrixRuntime,
+                          SparseTopology)
 
 pytestmark = pytest.mark.gpu
 
@@ -112,6 +114,33 @@ def inputs_for(g, batch, seed):
     }
 
 
+def oracle_gradients(g, inputs, ticks, *, scalar_drives, expanded) -> dict:
+    """The oracle's gradients on the inputs as the native run sees them
+    (rounded to float32), keyed like ``run``'s."""
+    f32 = lambda v: np.asarray(v, np.float32).astype(np.float64)  # noqa: E731
+    n = g.n
+    params = {}
+    for name, key in zip(og.PARAM_NAMES, ("alpha", "gain", "rho_d", "rho_a", "coupling", "strength")):
+        value = f32(inputs["params"][key])
+        params[name] = np.full(n, value[0]) if expanded and key in ("coupling", "strength") else value
+    x = og.TickInputs(state=f32(inputs["state"]), dendrite=f32(inputs["dendrite"]),
+                      adaptation=f32(inputs["adaptation"]),
+                      drive=0.2 if scalar_drives else f32(inputs["drive"]),
+                      dendritic=0.1 if scalar_drives else f32(inputs["dendritic"]),
+                      params=params, probe={k: f32(inputs["probe"][k]) for k in ("s", "d", "a")})
+    got = og.tick_gradients(g, x, ticks)
+    out = {"weight": got["weight"], "state": got["state"], "dendrite": got["dendrite"],
+           "adaptation": got["adaptation"]}
+    if not scalar_drives:
+        out["drive"], out["dendritic"] = got["drive"], got["dendritic"]
+    for name in og.PARAM_NAMES:
+        value = got[name]
+        if expanded and name in ("coupling", "strength"):
+            value = value.sum()                  # the gradient of the 0-d base
+        out[name] = value
+    return {k: torch.from_numpy(np.asarray(v, np.float64)) for k, v in out.items()}
+
+
 def compare(native: dict, reference: dict, rtol: float = 1e-4) -> None:
     assert native.keys() == reference.keys()
     for name, want in reference.items():
@@ -125,7 +154,7 @@ def compare(native: dict, reference: dict, rtol: float = 1e-4) -> None:
 
 @pytest.mark.parametrize("ticks,batch,scalar_drives,expanded", [
     (1, 3, False, False), (1, 1, True, True), (8, 2, False, True), (8, 4, True, False)])
-def test_gradients_match_autograd_of_the_torch_step(gpu, ticks, batch, scalar_drives, expanded):
+def test_gradients_match_the_oracle(gpu, ticks, batch, scalar_drives, expanded):
     print(f"case backward ticks={ticks} batch={batch} scalar_drives={scalar_drives} "
           f"expanded={expanded}", flush=True)
     g = graph(600, 12_000, 9)
@@ -133,8 +162,7 @@ def test_gradients_match_autograd_of_the_torch_step(gpu, ticks, batch, scalar_dr
     kw = dict(scalar_drives=scalar_drives, expanded=expanded)
     native, rt = run(NativeDendriticMatrixRuntime, g, inputs, torch.float32, gpu, ticks, **kw)
     assert rt.last_backend == "native-autograd"
-    reference, _ = run(DendriticMatrixRuntime, g, inputs, torch.float64, "cpu", ticks, **kw)
-    compare(native, reference)
+    compare(native, oracle_gradients(g, inputs, ticks, **kw))
 
 
 def test_backward_is_repeatable(gpu):
