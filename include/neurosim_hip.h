@@ -436,6 +436,19 @@ int64_t ns_encode_workspace_bytes(void);
  * allocation, no host synchronisation; parity is defined for finite weights. */
 int ns_encode_weights(const ns_encode_args* args, void* stream);
 
+/* No counterpart in the reference: ns_encode_weights for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid allocation).  Same arguments and bit-identical
+ * results, except that `args->workspace` must be NULL: the amax partials go to
+ * a library-owned device array of 4 KiB (1024 partials, enough for every
+ * n_edges the encoder accepts, [0, 2^40)), one per GPU, held until the process
+ * ends.  Its address is looked up on the first call on each device, with that
+ * device current; `stream` must belong to the current device.  Nothing in the
+ * array needs clearing (each call rewrites every partial it reads), but calls
+ * that overlap on one GPU (on different streams) race on it.  Allocates
+ * nothing, launches two kernels on `stream`, no host synchronisation. */
+int ns_encode_weights_no_alloc(const ns_encode_args* args, void* stream);
+
 /* Bytes of workspace ns_build_topology needs for N neurons and Mc candidates
  * (-1 on invalid sizes, with ns_last_error set). */
 int64_t ns_topology_workspace_bytes(int64_t n_neurons, int64_t n_candidates);

@@ -20,6 +20,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "ns_common.h"
 #include "ns_host.h"
@@ -192,6 +193,40 @@ __global__ __launch_bounds__(kEncodeThreads) void encode_nvfp4_kernel(
   }
 }
 
+// The partials of ns_encode_weights_no_alloc: a library-owned device array,
+// one per GPU (each device holds its own copy at its own address), alive until
+// the process ends.  Host code never passes `scratch` itself to a kernel (on
+// the host the name is a stand-in, not a device address): it looks up each
+// device's address once and passes that.
+static __device__ __align__(256) uint32_t scratch[kEncodePartials];
+
+constexpr int kMaxDevices = 64;
+
+// The device address of `scratch` on the current device, looked up on the
+// first call on that device (with it current) and kept; null with the error
+// set on failure.
+uint32_t* scratch_on_current_device() {
+  static std::mutex mu;
+  static uint32_t* address[kMaxDevices] = {};
+  int device = -1;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) {
+    fail("no usable current HIP device (device %d)", device);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!address[device]) {
+    void* ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !ptr) {
+      fail("could not find the encoder's scratch array on device %d: %s", device,
+           hipGetErrorString(err));
+      return nullptr;
+    }
+    address[device] = static_cast<uint32_t*>(ptr);
+  }
+  return address[device];
+}
+
 int partial_blocks(int64_t m) {
   const int64_t quads = (m + 3) / 4;
   return static_cast<int>(std::min<int64_t>(kEncodePartials,
@@ -204,14 +239,14 @@ using namespace ns;
 
 extern "C" int64_t ns_encode_workspace_bytes(void) { return 4 * int64_t{kEncodePartials}; }
 
-extern "C" int ns_encode_weights(const ns_encode_args* args, void* stream) {
-  clear_error();
-  if (!args) return fail("arguments are required");
-  const ns_encode_args& a = *args;
+namespace {
+
+// Every argument but the workspace.
+int check_args(const ns_encode_args& a) {
   if (a.n_edges < 0 || a.n_edges >= (int64_t{1} << 40)) return fail("n_edges must be in [0, 2^40)");
   if (a.format != NS_WEIGHT_E4M3 && a.format != NS_WEIGHT_NVFP4)
     return fail("weight encoding needs format E4M3 or NVFP4, not %d", a.format);
-  if (!a.global_scale || !a.workspace) return fail("global_scale and workspace are required");
+  if (!a.global_scale) return fail("global_scale is required");
   if (a.n_edges > 0 && (!a.weight || !a.codes)) return fail("weight and codes are required");
   if (a.format == NS_WEIGHT_NVFP4 && a.n_edges > 0 && !a.block_scales)
     return fail("NVFP4 encoding requires block_scales");
@@ -221,22 +256,65 @@ extern "C" int ns_encode_weights(const ns_encode_args* args, void* stream) {
     return fail("E4M3 codes must be 4-byte aligned");
   if (a.format == NS_WEIGHT_NVFP4 && reinterpret_cast<uintptr_t>(a.codes) % 8)
     return fail("NVFP4 codes must be 8-byte aligned");
-  if (reinterpret_cast<uintptr_t>(a.workspace) % 4) return fail("workspace must be 4-byte aligned");
+  return NS_OK;
+}
+
+// Launches the two kernels of checked arguments with the amax partials in
+// `partials` (room for kEncodePartials entries).
+int encode(const ns_encode_args& a, uint32_t* partials, void* stream) {
   const hipStream_t s = static_cast<hipStream_t>(stream);
+  // Every partial the encoder reads is written by the first launch: nothing
+  // in `partials` needs to be cleared beforehand.
   const int parts = partial_blocks(a.n_edges);
-  amax_partials_kernel<<<dim3(parts), dim3(kEncodeThreads), 0, s>>>(a.weight, a.n_edges, a.workspace);
+  amax_partials_kernel<<<dim3(parts), dim3(kEncodeThreads), 0, s>>>(a.weight, a.n_edges, partials);
   if (hipGetLastError() != hipSuccess) return fail("amax launch failed");
   if (a.format == NS_WEIGHT_E4M3) {
     const int64_t quads = a.n_edges / 4;
     const int grid = static_cast<int>(std::min<int64_t>(2048, std::max<int64_t>(1, (quads + kEncodeThreads - 1) / kEncodeThreads)));
     encode_e4m3_kernel<<<dim3(grid), dim3(kEncodeThreads), 0, s>>>(
-        a.weight, a.n_edges, a.workspace, parts, a.codes, a.global_scale);
+        a.weight, a.n_edges, partials, parts, a.codes, a.global_scale);
   } else {
     const int64_t blocks = (a.n_edges + 15) / 16;
     const int grid = static_cast<int>(std::min<int64_t>(2048, std::max<int64_t>(1, (blocks + kEncodeThreads - 1) / kEncodeThreads)));
     encode_nvfp4_kernel<<<dim3(grid), dim3(kEncodeThreads), 0, s>>>(
-        a.weight, a.n_edges, a.workspace, parts, a.codes, a.block_scales, a.global_scale);
+        a.weight, a.n_edges, partials, parts, a.codes, a.block_scales, a.global_scale);
   }
   if (hipGetLastError() != hipSuccess) return fail("encode launch failed");
   return NS_OK;
+}
+
+}  // namespace
+
+extern "C" int ns_encode_weights(const ns_encode_args* args, void* stream) {
+  clear_error();
+  if (!args) return fail("arguments are required");
+  const ns_encode_args& a = *args;
+  if (!a.global_scale || !a.workspace) return fail("global_scale and workspace are required");
+  if (int rc = check_args(a)) return rc;
+  if (reinterpret_cast<uintptr_t>(a.workspace) % 4) return fail("workspace must be 4-byte aligned");
+  return encode(a, a.workspace, stream);
+}
+
+extern "C" int ns_encode_weights_no_alloc(const ns_encode_args* args, void* stream) {
+  clear_error();
+  if (!args) return fail("arguments are required");
+  const ns_encode_args& a = *args;
+  if (int rc = check_args(a)) return rc;
+  if (a.workspace) return fail("the no-allocation encoder takes no workspace (pass NULL)");
+  // The partials of any M in range fit the scratch array: at most
+  // kEncodePartials workgroups write them (partial_blocks).
+  if (partial_blocks(a.n_edges) > kEncodePartials)
+    return fail("%lld edges need more than the %d partials of the scratch array",
+                (long long)a.n_edges, kEncodePartials);
+  if (stream) {
+    int current = -1, owner = -1;
+    if (hipGetDevice(&current) != hipSuccess ||
+        hipStreamGetDevice(static_cast<hipStream_t>(stream), &owner) != hipSuccess)
+      return fail("could not query the current device or the stream's device");
+    if (current != owner)
+      return fail("the stream belongs to device %d but device %d is current", owner, current);
+  }
+  uint32_t* partials = scratch_on_current_device();
+  if (!partials) return NS_ERR_INVALID;
+  return encode(a, partials, stream);
 }

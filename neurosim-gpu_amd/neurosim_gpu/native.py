@@ -191,6 +191,7 @@ def load_library() -> ctypes.CDLL:
     lib.ns_topology_workspace_bytes.argtypes = [_c_i64, _c_i64]
     for name, kind in (("ns_dendritic_step", _StepArgs), ("ns_dendritic_event", _EventArgs),
                        ("ns_csr_spmm", _SpmmArgs), ("ns_encode_weights", _EncodeArgs),
+                       ("ns_encode_weights_no_alloc", _EncodeArgs),
                        ("ns_build_topology", _TopologyArgs),
                        ("ns_dendritic_step_backward", _StepGradArgs)):
         fn = getattr(lib, name)

@@ -33,6 +33,7 @@ def test_every_declared_symbol_is_exported(lib):
                           "ns_plan_row_blocks", "ns_dendritic_step", "ns_dendritic_event",
                           "ns_csr_spmm", "ns_plan_panels", "ns_panel_geometry",
                           "ns_encode_workspace_bytes", "ns_encode_weights",
+                          "ns_encode_weights_no_alloc",
                           "ns_topology_workspace_bytes", "ns_build_topology",
                           "ns_step_backward_workspace_floats", "ns_dendritic_step_backward",
                           "ns_plan_bands", "ns_band_max_block_rows", "ns_dendritic_step_bands"}
@@ -216,6 +217,26 @@ def test_encoder_validation_messages(lib):
     assert rc != 0 and "4-byte aligned" in message
     rc, message = call(n_edges=-1)
     assert rc != 0 and "n_edges" in message
+    rc, message = call(workspace=None)
+    assert rc != 0 and "workspace" in message
+
+    def no_alloc(**fields):
+        base = dict(weight=None, n_edges=0, format=native.WEIGHT_E4M3, reserved=0, codes=None,
+                    block_scales=None, global_scale=16, workspace=None)
+        base.update(fields)
+        args = native._EncodeArgs(**base)
+        rc = lib.ns_encode_weights_no_alloc(ctypes.byref(args), None)
+        return rc, lib.ns_last_error().decode()
+
+    # The same argument checks, before the device is touched, plus: no workspace.
+    rc, message = no_alloc(workspace=16)
+    assert rc != 0 and "takes no workspace" in message
+    rc, message = no_alloc(format=native.WEIGHT_F32)
+    assert rc != 0 and "E4M3 or NVFP4" in message
+    rc, message = no_alloc(n_edges=1 << 40)
+    assert rc != 0 and "n_edges" in message
+    rc, message = no_alloc(n_edges=10, weight=16, codes=16, format=native.WEIGHT_NVFP4)
+    assert rc != 0 and "block_scales" in message
 
 
 def test_topology_builder_validation(lib):
