@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 7
+#define NS_ABI_VERSION 8
 
 /* Return codes. */
 #define NS_OK 0
@@ -91,8 +91,9 @@ typedef struct ns_row_plan {
 
 /* Column-panel layout of a CSR matrix for batch widths 1 and 2, built by
  * ns_plan_panels.  Columns are cut into `n_panels` panels of `panel_width`
- * neurons (a panel's slice of the state fits in one workgroup's LDS).  A tile
- * is one workgroup's work: one panel and a range of destination rows.  The
+ * neurons (a panel's slice of the state fits in one workgroup's LDS).  Rows
+ * are cut into `n_ranges` ranges shared by every panel.  A tile is one
+ * workgroup's work: one panel and one row range.  The
  * tile's rows are sorted by the length of their segment in the panel and cut
  * into groups; a group gives each of its rows 2^lg lanes of a 64-lane
  * wavefront (64 >> lg rows), lane j of a row taking the row's edges j, j+2^lg,
@@ -109,18 +110,26 @@ typedef struct ns_row_plan {
  * low nibble) and the pair's e4m3 block-scale code in the high byte. */
 #define NS_PANEL_PAIRS 1
 
+/* Panel plan flag (set by the caller, not the planner): finish the tick with a
+ * second launch that adds each row's panel sums and applies the update,
+ * instead of letting the last tile of each row range do it in the same launch.
+ * The results are bitwise the same. */
+#define NS_PANEL_COMBINE_LAUNCH 2
+
 typedef struct ns_panel_plan {
   int32_t panel_width;
   int32_t n_panels;
   int32_t n_tiles;
   int32_t n_groups;
   int32_t waves;               /* wavefronts per workgroup the plan was built for */
-  int32_t flags;               /* NS_PANEL_* layout flags the plan was built with */
-  int32_t reserved[2];
+  int32_t flags;               /* NS_PANEL_* flags */
+  int32_t n_ranges;            /* row ranges; each panel has one tile per range */
+  int32_t reserved;
   int64_t n_slots;             /* edge slots including padding and the tail padding */
   int64_t n_step_words;        /* uint32 words of `last_steps` */
   const int32_t* tiles;        /* [n_tiles][4]: panel, first row, end row, first entry of
                                   the tile's rows in `rows` */
+  const int32_t* tile_ranges;  /* [n_tiles]: row range of each tile */
   const int32_t* wave_groups;  /* [n_tiles*waves + 1]: wave w of tile t owns groups
                                   wave_groups[t*waves+w] .. wave_groups[t*waves+w+1]-1 */
   const int32_t* groups;       /* [n_groups][4]: first slot, steps, lg | rows << 8,
@@ -137,7 +146,15 @@ typedef struct ns_panel_plan {
   float* partials;             /* workspace float[2][n_panels*N*batch]: the second half
                                   holds row sums in row-table order, the first half the
                                   per-panel row sums by row (several panels), added in
-                                  panel order by a second kernel */
+                                  panel order once every panel's tile of the row range
+                                  has stored them */
+  uint32_t* range_counters;    /* workspace uint32[n_ranges] (several panels, unless
+                                  NS_PANEL_COMBINE_LAUNCH): zero before the first launch;
+                                  each tile adds one to its range's counter after storing
+                                  its sums, and the tile that brings it to n_panels
+                                  finishes the range's rows and sets it back to zero, so
+                                  every launch leaves the counters zero.  Launches sharing
+                                  a plan's workspace must be ordered on one stream. */
 } ns_panel_plan;
 
 /* Source-band layout of a CSR matrix for wide batches (batch a multiple of
@@ -338,17 +355,18 @@ int ns_plan_row_blocks(const int32_t* rowptr_host, int64_t n_rows, int32_t block
 
 /* Host-side panel planner for a host copy of (rowptr, col).  Panel width is
  * the largest that fits `max_panel_width` neurons, equalised over panels and
- * rounded to a multiple of 4.  Each panel's rows are cut into about
- * `tiles_per_panel` tiles of equal cost (segment edges + 1 per row, at most
- * 65536 rows each).  A row whose segment has L edges gets the smallest
+ * rounded to a multiple of 4.  Rows are cut into about `tiles_per_panel`
+ * ranges of equal cost over all panels (items + 1 per row and panel, at most
+ * 65536 rows each); each panel has one tile per range.  A row whose segment has L edges gets the smallest
  * power-of-two lane count that leaves each lane at most `lane_target` edges
  * (at most 64; at least 2 with NS_PANEL_PAIRS in `flags`, where a segment's
  * length counts its padding items).  Groups go to the `waves` wavefronts of their tile (which
  * must be the kernel's wavefronts per workgroup) longest first onto the
  * least-loaded one.  Call once with all output pointers NULL to get the sizes
  * in *plan (n_panels, panel_width, n_tiles, n_groups, n_slots, waves,
- * n_step_words) and *n_row_entries, then again with arrays of those sizes:
- * tiles int32[4*n_tiles], wave_groups int32[n_tiles*waves+1], groups
+ * n_step_words, n_ranges) and *n_row_entries, then again with arrays of those
+ * sizes: tiles int32[4*n_tiles], tile_ranges int32[n_tiles], wave_groups
+ * int32[n_tiles*waves+1], groups
  * int32[4*n_groups], rows uint16[n_row_entries], last_steps
  * uint32[n_step_words], perm int32[n_slots] (-1 for padding), col
  * uint16[n_slots].  Pointer fields of *plan are not touched. */
@@ -356,8 +374,8 @@ int ns_plan_panels(const int32_t* rowptr_host, const int32_t* col_host, int64_t 
                    int32_t max_panel_width, int32_t tiles_per_panel, int32_t waves,
                    int32_t lane_target, int32_t flags, ns_panel_plan* plan,
                    int64_t* n_row_entries,
-                   int32_t* tiles, int32_t* wave_groups, int32_t* groups, uint16_t* rows,
-                   uint32_t* last_steps, int32_t* perm, uint16_t* col);
+                   int32_t* tiles, int32_t* tile_ranges, int32_t* wave_groups, int32_t* groups,
+                   uint16_t* rows, uint32_t* last_steps, int32_t* perm, uint16_t* col);
 
 /* Panel geometry the tick kernels use for batch width `batch` (1 or 2):
  * largest panel width and the wavefronts per workgroup (NULL outputs are

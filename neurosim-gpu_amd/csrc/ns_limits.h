@@ -5,6 +5,8 @@
 namespace ns {
 
 constexpr int kThreads = 256;   // 4 wavefronts of 64 lanes
+// XCDs of the target (gfx950); workgroups are dealt to them round-robin by id.
+constexpr int kXcds = 8;
 constexpr int kMaxRows = 256;   // rows per row block (one lane per row at most density)
 
 // Column-panel kernel (batch widths 1 and 2): 16 wavefronts per workgroup

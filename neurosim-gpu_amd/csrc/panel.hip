@@ -27,8 +27,17 @@
 //    per row stores the sum at the group's row-table entries);
 //  * after its stream each wavefront maps its row-table entries back to rows:
 //    with one panel it updates those rows, with several it stores the
-//    panel's partial sums by row and a second kernel adds them in panel
-//    order and applies the update.
+//    panel's partial sums by row;
+//  * rows are cut into ranges shared by all panels, so the tiles of one range
+//    (one per panel) together hold every panel's sums of the range's rows.
+//    Each tile counts itself in on its range's counter once its sums are
+//    stored, and the tile that completes the count adds the range's sums in
+//    panel order and applies the update: one launch per tick.  The sums are
+//    written through to, and read back from, the device-coherent level
+//    (agent-scope atomic stores and loads), and a tile's stores have completed
+//    before it counts itself in, so they need no cache write-back.  A second
+//    kernel that does the same adds after the tick kernel
+//    (NS_PANEL_COMBINE_LAUNCH) gives bitwise the same results.
 //
 // Results are bitwise repeatable and, on one layout, identical across weight
 // encodings that decode to the same float32 values.
@@ -53,6 +62,9 @@ constexpr int panel_capacity_neurons() {
 // high byte.  A kernel template format of its own, next to the NS_WEIGHT_* ones.
 constexpr int kNvfp4Pairs = 4;
 
+// Wave priority follows each wave's remaining stream.
+constexpr bool kPacedWaves = true;
+
 // Steps per register block: enough 64-lane loads in flight per wavefront to
 // cover HBM latency with 16 wavefronts per compute unit, within 128 VGPRs.
 template <int BT, int FMT>
@@ -69,6 +81,8 @@ struct PanelArgs {
   Params p;
   int32_t width, n_panels;
   const int32_t* tiles;
+  const int32_t* tile_ranges;
+  uint32_t* counters;  // [n_ranges]; null: a second kernel combines the panels
   const int32_t* wave_groups;
   const int32_t* groups;
   const uint16_t* rows;
@@ -182,6 +196,21 @@ __device__ __forceinline__ float decode_slot(const Slot& x, int lane, float gsca
   }
 }
 
+// The kernel's arguments read again from the kernel argument segment.  The
+// opaque pointer makes the compiler load the fields a caller uses where it
+// uses them, instead of keeping them in scalar registers since kernel entry.
+__device__ __forceinline__ PanelArgs fresh_args() {
+  static_assert(sizeof(PanelArgs) % 4 == 0, "kernel arguments are copied in 32-bit words");
+  typedef const __attribute__((address_space(4))) uint32_t* kernarg_ptr;
+  kernarg_ptr p = (kernarg_ptr)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(p));
+  PanelArgs out;
+  uint32_t* words = reinterpret_cast<uint32_t*>(&out);
+#pragma unroll
+  for (unsigned i = 0; i < sizeof(PanelArgs) / 4; ++i) words[i] = p[i];
+  return out;
+}
+
 __device__ __forceinline__ void update(const PanelArgs& A, int64_t n, int64_t b, float j) {
   const NextState x = advance_one(A.p, n, j, A.s.get(b, n), A.d.get(b, n), A.a.get(b, n),
                                   A.u.get(b, n), A.v.get(b, n));
@@ -209,6 +238,113 @@ __device__ __forceinline__ uint32_t boundary_bits(const PanelArgs& A, int64_t k0
   return static_cast<uint32_t>(both >> (k0 & 31)) & ((1u << D) - 1u);
 }
 
+// Panel sums loaded per round before they are added.
+constexpr int kCombineBatch = 8;
+
+// Rows per thread per round of the finish below: a range of up to
+// kPanelThreads * finish_rows rows with at most kCombineBatch panels finishes
+// in one round.
+template <int BT>
+constexpr int finish_rows() {
+  return BT == 1 ? 4 : 2;
+}
+
+// One launch per tick with several panels: called by every tile after its
+// wavefronts have stored the panel's sums of rows [r0, r1) (agent-scope atomic
+// stores).  The tile counts itself in on its range's counter; the tile that
+// completes the count (all n_panels tiles of the range have stored their
+// sums) sets the counter back to zero for the next launch, then adds each
+// row's sums in panel order and applies the update.  Each round issues every
+// load of its rows (parameters, states, drives, the first kCombineBatch
+// panels' sums) before the first add, so it waits on memory once.
+template <int BT>
+__device__ __forceinline__ void finish_range(const PanelArgs& A, int64_t r0, int64_t r1) {
+  __shared__ int last;
+  // Each lane's sums have reached the device-coherent level before the
+  // barrier, so before the count below.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t* const counter = A.counters + A.tile_ranges[blockIdx.x];
+    const uint32_t before = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+    const bool done = before == static_cast<uint32_t>(A.n_panels - 1);
+    if (done) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = done;
+  }
+  __syncthreads();
+  if (!last) return;
+  constexpr int R = finish_rows<BT>();
+  const int64_t plane = A.N * BT;
+  auto partial = [&](int p, int64_t n, int j) {
+    return __hip_atomic_load(A.partials + p * plane + n * BT + j, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+  };
+  for (int64_t n0 = r0 + threadIdx.x; n0 < r1; n0 += kPanelThreads * R) {
+    NeuronParams prm[R];
+    float s[R][BT], d[R][BT], a[R][BT], u[R][BT], v[R][BT];
+    float part[R][kCombineBatch][BT];
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      // Rows past the range and panels past the last reread the last ones
+      // (not used), so that no load waits behind a branch.
+      const int64_t n = min(n0 + k * kPanelThreads, r1 - 1);
+      prm[k] = load_params(A.p, n);
+#pragma unroll
+      for (int j = 0; j < BT; ++j) {
+        s[k][j] = A.s.get(j, n); d[k][j] = A.d.get(j, n); a[k][j] = A.a.get(j, n);
+        u[k][j] = A.u.get(j, n); v[k][j] = A.v.get(j, n);
+      }
+#pragma unroll
+      for (int q = 0; q < kCombineBatch; ++q)
+#pragma unroll
+        for (int j = 0; j < BT; ++j) part[k][q][j] = partial(min(q, A.n_panels - 1), n, j);
+    }
+    float sum[R][BT];
+#pragma unroll
+    for (int k = 0; k < R; ++k)
+#pragma unroll
+      for (int j = 0; j < BT; ++j) {
+        sum[k][j] = 0.0f;
+#pragma unroll
+        for (int q = 0; q < kCombineBatch; ++q)
+          if (q < A.n_panels) sum[k][j] += part[k][q][j];
+      }
+    for (int p0 = kCombineBatch; p0 < A.n_panels; p0 += kCombineBatch) {
+#pragma unroll
+      for (int k = 0; k < R; ++k) {
+        const int64_t n = min(n0 + k * kPanelThreads, r1 - 1);
+#pragma unroll
+        for (int q = 0; q < kCombineBatch; ++q)
+#pragma unroll
+          for (int j = 0; j < BT; ++j) part[k][q][j] = partial(min(p0 + q, A.n_panels - 1), n, j);
+      }
+#pragma unroll
+      for (int k = 0; k < R; ++k)
+#pragma unroll
+        for (int q = 0; q < kCombineBatch; ++q)
+#pragma unroll
+          for (int j = 0; j < BT; ++j)
+            if (p0 + q < A.n_panels) sum[k][j] += part[k][q][j];
+    }
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      const int64_t n = n0 + k * kPanelThreads;
+      if (n < r1) {
+#pragma unroll
+        for (int j = 0; j < BT; ++j) {
+          const NextState x = advance_loaded(prm[k], sum[k][j], s[k][j], d[k][j], a[k][j],
+                                             u[k][j], v[k][j]);
+          A.os.put(j, n, x.soma);
+          A.od.put(j, n, x.dendrite);
+          A.oa.put(j, n, x.adaptation);
+          if (A.oj.data) A.oj.put(j, n, sum[k][j]);
+        }
+      }
+    }
+  }
+}
+
 template <int BT, int FMT>
 __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) {
   constexpr int D = block_steps<BT, FMT>();
@@ -231,7 +367,9 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
 
   // A contiguous slice of s is staged with direct global -> LDS loads, issued
   // first since they need only the panel: wavefront chunk ch covers float4s
-  // [64ch, 64ch + 64) (each lane's 16 bytes land at its own offset).
+  // [64ch, 64ch + 64) (each lane's 16 bytes land at its own offset).  (Staging
+  // through registers, in the same order or with each workgroup of an XCD
+  // starting at its own place in the slice, measured no faster.)
   const v4f* src = reinterpret_cast<const v4f*>(A.s.data + base * BT);
   const int n4 = len * BT / 4;
   if (A.s_vec) {
@@ -339,60 +477,106 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
       if (g + 1 < g_end) next = load_group(A, g + 1);
     }
   };
+  // The waves of a compute unit take turns by age, so with equal streams the
+  // oldest would finish well before the youngest and leave the tile's last
+  // stretch to a few waves.  A wave's priority instead follows the share of
+  // its stream still ahead of it, which keeps the waves abreast.
+  auto pace = [&](int b) {
+    if constexpr (kPacedWaves) {
+      const int ahead = 4 * (total - b * D);
+      if (ahead > 3 * total) __builtin_amdgcn_s_setprio(3);
+      else if (ahead > 2 * total) __builtin_amdgcn_s_setprio(2);
+      else if (ahead > total) __builtin_amdgcn_s_setprio(1);
+      else __builtin_amdgcn_s_setprio(0);
+    }
+  };
   for (int b = 0; b * D < total; b += 2) {
+    pace(b);
     block(buf_a, buf_b, b);
     if ((b + 1) * D >= total) break;
+    pace(b + 1);
     block(buf_b, buf_a, b + 1);
   }
+  if constexpr (kPacedWaves) __builtin_amdgcn_s_setprio(0);
 
-  // Map this wavefront's row-table entries (one contiguous range: its groups'
-  // rows in order) back to rows as soon as its own stream is done: with one
-  // panel update the rows here, with several store this panel's partial sums
-  // by row.  The entries were stored by this wavefront's lanes; the fence
-  // orders those stores before the loads below.
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
-  if (wg[0] < g_end) {
-    const_i32_ptr head = (const_i32_ptr)(A.groups + 4 * static_cast<int64_t>(wg[0]));
-    const_i32_ptr last = (const_i32_ptr)(A.groups + 4 * static_cast<int64_t>(g_end - 1));
-    const int e_begin = head[3], e_end = last[3] + (last[2] >> 8);
-    if (A.n_panels == 1) {
+  // Map the row-table entries back to rows.  The arguments are read afresh,
+  // so the stream loop above need not keep them in scalar registers.
+  const PanelArgs E = fresh_args();
+  const_i32_ptr tile_e = (const_i32_ptr)(E.tiles + 4 * static_cast<int64_t>(blockIdx.x));
+  const int64_t row0_e = tile_e[1];
+  if (E.n_panels == 1) {
+    // One panel: each wavefront updates the rows of its own entries (one
+    // contiguous range: its groups' rows in order) as soon as its stream is
+    // done.  The entries were stored by this wavefront's lanes; the fence
+    // orders those stores before the loads below.
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+    const_i32_ptr wg_e =
+        (const_i32_ptr)(E.wave_groups + static_cast<int64_t>(blockIdx.x) * kPanelWaves + wave);
+    const int g_first = wg_e[0], g_last = wg_e[1];
+    if (g_first < g_last) {
+      const_i32_ptr head = (const_i32_ptr)(E.groups + 4 * static_cast<int64_t>(g_first));
+      const_i32_ptr last = (const_i32_ptr)(E.groups + 4 * static_cast<int64_t>(g_last - 1));
+      const int e_begin = head[3], e_end = last[3] + (last[2] >> 8);
       for (int e = e_begin + lane; e < e_end; e += 64) {
-        const int64_t row = row0 + static_cast<int64_t>(A.rows[e]);
+        const int64_t row = row0_e + static_cast<int64_t>(E.rows[e]);
 #pragma unroll
-        for (int j = 0; j < BT; ++j) update(A, row, j, A.sorted[static_cast<int64_t>(e) * BT + j]);
-      }
-    } else {
-      // kMapUnroll entries per lane per round: every load of a round is issued
-      // before its first store (an entry past the end rereads the last one and
-      // is not stored), so a round waits on memory once.
-      constexpr int kMapUnroll = 4;
-      float* const out = A.partials + static_cast<int64_t>(panel) * A.N * BT;
-      for (int e0 = e_begin + lane; e0 < e_end; e0 += 64 * kMapUnroll) {
-        int64_t row[kMapUnroll];
-        float value[kMapUnroll][BT];
-#pragma unroll
-        for (int u = 0; u < kMapUnroll; ++u) {
-          const int e = min(e0 + 64 * u, e_end - 1);
-          row[u] = row0 + static_cast<int64_t>(A.rows[e]);
-#pragma unroll
-          for (int j = 0; j < BT; ++j) value[u][j] = A.sorted[static_cast<int64_t>(e) * BT + j];
-        }
-#pragma unroll
-        for (int u = 0; u < kMapUnroll; ++u)
-          if (e0 + 64 * u < e_end) {
-#pragma unroll
-            for (int j = 0; j < BT; ++j) out[row[u] * BT + j] = value[u][j];
-          }
+        for (int j = 0; j < BT; ++j) update(E, row, j, E.sorted[static_cast<int64_t>(e) * BT + j]);
       }
     }
+    return;
   }
+
+  // Several panels: the tile's sums (one entry per row of the tile) are
+  // gathered into LDS by row, which the panel slice no longer needs, and
+  // stored in row order, so that the stores of a wavefront fill whole cache
+  // lines.  With more rows than LDS holds this goes in chunks of rows.
+  // kMapUnroll entries per thread per round: every load of a round is issued
+  // before its first LDS store (an entry past the end rereads the last one
+  // and is not stored), so a round waits on memory once.
+  constexpr int kMapUnroll = 4;
+  constexpr int kChunkRows = CAP + 1;
+  const int e0 = tile_e[3];
+  const int nrows = static_cast<int>(tile_e[2] - row0_e);
+  float* const out = E.partials + (static_cast<int64_t>(tile_e[0]) * E.N + row0_e) * BT;
+  const bool coherent = E.counters != nullptr;
+  __syncthreads();   // every wavefront's entries stored, the panel slice no longer read
+  for (int c0 = 0; c0 < nrows; c0 += kChunkRows) {
+    const int c1 = min(nrows, c0 + kChunkRows);
+    for (int i0 = tid; i0 < nrows; i0 += kPanelThreads * kMapUnroll) {
+      int r[kMapUnroll];
+      float value[kMapUnroll][BT];
+#pragma unroll
+      for (int u = 0; u < kMapUnroll; ++u) {
+        const int e = e0 + min(i0 + u * kPanelThreads, nrows - 1);
+        r[u] = E.rows[e];
+#pragma unroll
+        for (int j = 0; j < BT; ++j) value[u][j] = E.sorted[static_cast<int64_t>(e) * BT + j];
+      }
+#pragma unroll
+      for (int u = 0; u < kMapUnroll; ++u)
+        if (i0 + u * kPanelThreads < nrows && r[u] >= c0 && r[u] < c1) {
+#pragma unroll
+          for (int j = 0; j < BT; ++j) lds_s[(r[u] - c0) * BT + j] = value[u][j];
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < (c1 - c0) * BT; i += kPanelThreads) {
+      float* const at = out + c0 * BT + i;
+      if (coherent)
+        __hip_atomic_store(at, lds_s[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else
+        *at = lds_s[i];
+    }
+    __syncthreads();
+  }
+  if (coherent) finish_range<BT>(E, row0_e, tile_e[2]);
 }
 
-// Several panels: add each row's panel partial sums in panel order, then
-// update; one neuron (all BT columns) per thread.  Every load (state,
-// parameters, the first kCombineBatch panels' sums) is issued before the first
-// add, so the kernel waits on memory about once rather than once per panel.
-constexpr int kCombineBatch = 8;
+// Several panels, NS_PANEL_COMBINE_LAUNCH: add each row's panel partial sums
+// in panel order, then update; one neuron (all BT columns) per thread.  Every
+// load (state, parameters, the first kCombineBatch panels' sums) is issued
+// before the first add, so the kernel waits on memory about once rather than
+// once per panel.
 
 template <int BT>
 __global__ __launch_bounds__(kThreads) void panel_combine_kernel(PanelArgs A) {
@@ -446,7 +630,7 @@ hipError_t launch_panels(const PanelArgs& A, int fmt, int n_tiles, hipStream_t s
     default: panel_tick_kernel<BT, NS_WEIGHT_NVFP4><<<grid, block, 0, stream>>>(A); break;
   }
   hipError_t err = hipGetLastError();
-  if (err != hipSuccess || A.n_panels == 1) return err;
+  if (err != hipSuccess || A.n_panels == 1 || A.counters) return err;
   const int64_t blocks = (A.N + kThreads - 1) / kThreads;
   panel_combine_kernel<BT><<<dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, stream>>>(A);
   return hipGetLastError();
@@ -481,8 +665,17 @@ int panel_step(const ns_step_args& a, hipStream_t stream) {
       !pl.weight)
     return fail("panel plan tables are required");
   if (pl.n_step_words < pl.n_slots / 64 / 32 + 2) return fail("panel plan's step bitmap is short");
-  if (pl.flags & ~NS_PANEL_PAIRS) return fail("unknown panel layout flags %d", pl.flags);
+  if (pl.flags & ~(NS_PANEL_PAIRS | NS_PANEL_COMBINE_LAUNCH))
+    return fail("unknown panel plan flags %d", pl.flags);
   const bool pairs = (pl.flags & NS_PANEL_PAIRS) != 0;
+  const bool one_launch = pl.n_panels > 1 && !(pl.flags & NS_PANEL_COMBINE_LAUNCH);
+  if (one_launch) {
+    if (!pl.tile_ranges || !pl.range_counters)
+      return fail("panel tile ranges and range counters are required with several panels");
+    if (pl.n_ranges < 1 || static_cast<int64_t>(pl.n_ranges) * pl.n_panels != pl.n_tiles)
+      return fail("%d tiles are not one per panel for each of %d row ranges", pl.n_tiles,
+                  pl.n_ranges);
+  }
   if (a.matrix.format == NS_WEIGHT_NVFP4 && !pairs && !pl.slot_scales)
     return fail("NVFP4 panels require per-slot block scales");
   if (!pl.partials) return fail("the panel path needs its partials workspace");
@@ -505,6 +698,14 @@ int panel_step(const ns_step_args& a, hipStream_t stream) {
       if (overlaps(part, others[i]))
         return fail(i < 4 ? "the partials workspace overlaps an output"
                           : "the partials workspace overlaps an input");
+    if (one_launch) {
+      const Extent counters = extent_of(pl.range_counters, 1, 1, 1, pl.n_ranges);
+      if (overlaps(counters, part)) return fail("the range counters overlap the partials workspace");
+      for (int i = 0; i < 9; ++i)
+        if (overlaps(counters, others[i]))
+          return fail(i < 4 ? "the range counters overlap an output"
+                            : "the range counters overlap an input");
+    }
   }
 
   PanelArgs A{};
@@ -514,7 +715,8 @@ int panel_step(const ns_step_args& a, hipStream_t stream) {
   A.u = plane(a.drive, a.state.data); A.v = plane(a.dendritic_drive, a.state.data);
   for (int i = 0; i < 6; ++i) A.p.v[i] = Vec{a.params[i].data, a.params[i].stride};
   A.width = pl.panel_width; A.n_panels = pl.n_panels;
-  A.tiles = pl.tiles; A.wave_groups = pl.wave_groups; A.groups = pl.groups; A.rows = pl.rows;
+  A.tiles = pl.tiles; A.wave_groups = pl.wave_groups;
+  if (one_launch) { A.tile_ranges = pl.tile_ranges; A.counters = pl.range_counters; } A.groups = pl.groups; A.rows = pl.rows;
   A.last_steps = pl.last_steps;
   A.col = pl.col; A.weight = pl.weight; A.slot_scales = pl.slot_scales;
   A.gscale = a.matrix.global_scale;

@@ -74,9 +74,6 @@ extern "C" int ns_plan_row_blocks(const int32_t* rowptr, int64_t n_rows, int32_t
 
 namespace {
 
-// XCDs of the target (gfx950): the panel planner orders tiles for them.
-constexpr int64_t kXcds = 8;
-
 // Host threads a planner may use (the hosts this runs on give a process
 // about 16 cores).
 constexpr unsigned kPlanThreads = 16;
@@ -115,8 +112,8 @@ void run_on_threads(Work& work, int64_t items) {
 
 // The sliced layout of one graph, in host vectors (built twice: size query, then fill).
 struct PanelLayout {
-  int32_t panel_width = 0, n_panels = 0;
-  std::vector<int32_t> tiles, wave_groups, groups, perm;
+  int32_t panel_width = 0, n_panels = 0, n_ranges = 0;
+  std::vector<int32_t> tiles, tile_ranges, wave_groups, groups, perm;
   std::vector<uint16_t> rows, col;
   std::vector<uint32_t> last_steps;   // bit k: step k (slots 64k..64k+63) ends a group
 };
@@ -326,35 +323,28 @@ int build_panels(const int32_t* rowptr, const int32_t* col, int64_t n, int32_t m
   }
   const int32_t min_lg = pairs ? 1 : 0;
 
-  // Tiles of panel p: consecutive row ranges of about equal cost (segment
-  // edges + 1 per row), at most 65536 rows each (16-bit tile-local rows).
-  const int64_t min_tiles = (n + 65535) / 65536;
-  const int64_t T = std::min<int64_t>(n, std::max<int64_t>(tiles_per_panel, min_tiles));
-  std::vector<int64_t> cost(n + 1);
-  struct Cut { int32_t p; int64_t r0, r1; };
-  std::vector<Cut> cuts;                 // panel-major
-  for (int32_t p = 0; p < P; ++p) {
-    cost[0] = 0;
-    for (int64_t r = 0; r < n; ++r)
-      cost[r + 1] = cost[r] + (it.bucket[r * (P + 1) + p + 1] - it.bucket[r * (P + 1) + p]) + 1;
-    int64_t r0 = 0;
-    for (int64_t t = 1; t <= T && r0 < n; ++t) {
-      int64_t r1 = n;
-      if (t < T) {
-        const int64_t target = (cost[n] * t) / T;
-        r1 = std::lower_bound(cost.begin(), cost.end(), target) - cost.begin();
-        r1 = std::max<int64_t>(r1, r0 + 1);
-      }
-      r1 = std::min<int64_t>(r1, std::min<int64_t>(n, r0 + 65536));
-      if (t == T) r1 = n;
-      while (r1 - r0 > 65536) {          // only possible on the last tile
-        cuts.push_back(Cut{p, r0, r0 + 65536});
-        r0 += 65536;
-      }
-      cuts.push_back(Cut{p, r0, r1});
-      r0 = r1;
-    }
+  // Row ranges shared by every panel: consecutive rows of about equal cost
+  // over all panels (items + 1 per row and panel), at most 65536 rows each
+  // (16-bit tile-local rows).  Panel p's tile of range k covers the range's
+  // rows, so the tiles of one range together cover its rows in every panel.
+  const int64_t min_ranges = (n + 65535) / 65536;
+  const int64_t T = std::min<int64_t>(n, std::max<int64_t>(tiles_per_panel, min_ranges));
+  std::vector<int64_t> cost(n + 1, 0);
+  for (int64_t r = 0; r < n; ++r) cost[r + 1] = cost[r] + (it.base[r + 1] - it.base[r]) + P;
+  std::vector<int64_t> range_rows{0};
+  for (int64_t t = 1; range_rows.back() < n; ++t) {
+    const int64_t r0 = range_rows.back();
+    int64_t r1 = n;
+    if (t < T) r1 = std::lower_bound(cost.begin(), cost.end(), (cost[n] * t) / T) - cost.begin();
+    r1 = std::min<int64_t>(n, std::min<int64_t>(r0 + 65536, std::max<int64_t>(r1, r0 + 1)));
+    range_rows.push_back(r1);
   }
+  const int64_t n_ranges = static_cast<int64_t>(range_rows.size()) - 1;
+  out.n_ranges = static_cast<int32_t>(n_ranges);
+  struct Cut { int32_t p; int64_t r0, r1, k; };
+  std::vector<Cut> cuts;                 // panel-major
+  for (int32_t p = 0; p < P; ++p)
+    for (int64_t k = 0; k < n_ranges; ++k) cuts.push_back(Cut{p, range_rows[k], range_rows[k + 1], k});
   // Workgroups are dealt to the XCDs round-robin by workgroup id.  Tile k of
   // the emitted order runs on XCD k % kXcds, so the panel-major list is cut
   // into runs, one per XCD, that fill that XCD's workgroup ids in turn: the
@@ -377,6 +367,7 @@ int build_panels(const int32_t* rowptr, const int32_t* col, int64_t n, int32_t m
     }
   };
   run_on_threads(work, nt);
+  for (int64_t k = 0; k < nt; ++k) out.tile_ranges.push_back(static_cast<int32_t>(cuts[slot_tile[k]].k));
   for (PanelLayout& part : parts) {
     const int64_t slot0 = static_cast<int64_t>(out.perm.size());
     const int64_t group0 = static_cast<int64_t>(out.groups.size() / 4);
@@ -424,9 +415,9 @@ extern "C" int ns_plan_panels(const int32_t* rowptr, const int32_t* col, int64_t
                               int32_t max_panel_width, int32_t tiles_per_panel, int32_t waves,
                               int32_t lane_target, int32_t flags, ns_panel_plan* plan,
                               int64_t* n_row_entries,
-                              int32_t* tiles, int32_t* wave_groups, int32_t* groups,
-                              uint16_t* rows, uint32_t* last_steps, int32_t* perm,
-                              uint16_t* col_out) {
+                              int32_t* tiles, int32_t* tile_ranges, int32_t* wave_groups,
+                              int32_t* groups, uint16_t* rows, uint32_t* last_steps,
+                              int32_t* perm, uint16_t* col_out) {
   clear_error();
   if (!rowptr || !plan || !n_row_entries) return fail("rowptr, plan and n_row_entries are required");
   if (n_rows <= 0 || n_rows >= (int64_t{1} << 31)) return fail("N must be in [1, 2^31)");
@@ -450,10 +441,12 @@ extern "C" int ns_plan_panels(const int32_t* rowptr, const int32_t* col, int64_t
   plan->n_groups = static_cast<int32_t>(layout.groups.size() / 4);
   plan->waves = waves;
   plan->flags = flags;
+  plan->n_ranges = layout.n_ranges;
   plan->n_slots = static_cast<int64_t>(layout.perm.size());
   plan->n_step_words = static_cast<int64_t>(layout.last_steps.size());
   *n_row_entries = static_cast<int64_t>(layout.rows.size());
   if (tiles) std::copy(layout.tiles.begin(), layout.tiles.end(), tiles);
+  if (tile_ranges) std::copy(layout.tile_ranges.begin(), layout.tile_ranges.end(), tile_ranges);
   if (wave_groups) std::copy(layout.wave_groups.begin(), layout.wave_groups.end(), wave_groups);
   if (groups) std::copy(layout.groups.begin(), layout.groups.end(), groups);
   if (rows) std::copy(layout.rows.begin(), layout.rows.end(), rows);

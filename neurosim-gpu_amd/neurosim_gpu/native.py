@@ -35,7 +35,7 @@ import numpy as np
 import torch
 
 _LIB_NAME = "libneurosim_hip.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 WEIGHT_F32, WEIGHT_F16, WEIGHT_E4M3, WEIGHT_NVFP4 = 0, 1, 2, 3
 _PLAN_CACHE = 64   # row plans kept per extension (one per live topology and batch width)
@@ -72,10 +72,12 @@ class _PanelPlan(ctypes.Structure):
     _fields_ = [("panel_width", ctypes.c_int32), ("n_panels", ctypes.c_int32),
                 ("n_tiles", ctypes.c_int32), ("n_groups", ctypes.c_int32),
                 ("waves", ctypes.c_int32), ("flags", ctypes.c_int32),
-                ("reserved", ctypes.c_int32 * 2), ("n_slots", _c_i64),
-                ("n_step_words", _c_i64), ("tiles", _c_ptr), ("wave_groups", _c_ptr),
+                ("n_ranges", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("n_slots", _c_i64), ("n_step_words", _c_i64), ("tiles", _c_ptr),
+                ("tile_ranges", _c_ptr), ("wave_groups", _c_ptr),
                 ("groups", _c_ptr), ("rows", _c_ptr), ("last_steps", _c_ptr), ("col", _c_ptr),
-                ("weight", _c_ptr), ("slot_scales", _c_ptr), ("partials", _c_ptr)]
+                ("weight", _c_ptr), ("slot_scales", _c_ptr), ("partials", _c_ptr),
+                ("range_counters", _c_ptr)]
 
 
 class _BandPlan(ctypes.Structure):
@@ -174,7 +176,7 @@ def load_library() -> ctypes.CDLL:
     lib.ns_plan_panels.restype = ctypes.c_int
     lib.ns_plan_panels.argtypes = [_c_ptr, _c_ptr, _c_i64, ctypes.c_int32, ctypes.c_int32,
                                    ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
-                                   ctypes.POINTER(_PanelPlan), ctypes.POINTER(_c_i64)] + [_c_ptr] * 7
+                                   ctypes.POINTER(_PanelPlan), ctypes.POINTER(_c_i64)] + [_c_ptr] * 8
     lib.ns_plan_bands.restype = ctypes.c_int
     lib.ns_plan_bands.argtypes = [_c_ptr, _c_ptr, _c_i64, ctypes.c_int32, ctypes.c_int32,
                                   ctypes.c_int32, ctypes.POINTER(_BandPlan)] + [_c_ptr] * 5
@@ -376,6 +378,12 @@ LANE_TARGET = 24   # at most this many edges per lane before a row gets more lan
 
 
 PANEL_PAIRS = 1   # NS_PANEL_PAIRS
+PANEL_COMBINE_LAUNCH = 2   # NS_PANEL_COMBINE_LAUNCH
+# Largest row range the tick kernel's last tile finishes by itself.  Measured
+# at N=166,000, M=25M, B=1 (five panels, 3255-row ranges): the last tile's
+# update of its range took 6.8 us on one compute unit against about 3 us for
+# the second kernel spread over the whole chip.
+ONE_LAUNCH_MAX_RANGE_ROWS = 1024
 
 
 def plan_panels_host(rowptr: torch.Tensor, col: torch.Tensor, batch: int, tiles_per_panel: int,
@@ -394,18 +402,19 @@ def plan_panels_host(rowptr: torch.Tensor, col: torch.Tensor, batch: int, tiles_
     args = (rowptr.ctypes.data, col.ctypes.data if col.size else None, n, width,
             int(tiles_per_panel), waves, int(lane_target), PANEL_PAIRS if pairs else 0,
             ctypes.byref(plan), ctypes.byref(entries))
-    _raise_on(lib.ns_plan_panels(*args, *([None] * 7)), lib)
+    _raise_on(lib.ns_plan_panels(*args, *([None] * 8)), lib)
     tiles = np.empty(4 * plan.n_tiles, np.int32)
+    tile_ranges = np.empty(plan.n_tiles, np.int32)
     wave_groups = np.empty(plan.n_tiles * plan.waves + 1, np.int32)
     groups = np.empty(4 * plan.n_groups, np.int32)
     rows = np.empty(entries.value, np.uint16)
     last_steps = np.empty(plan.n_step_words, np.uint32)
     perm = np.empty(plan.n_slots, np.int32)
     cols = np.empty(plan.n_slots, np.uint16)
-    _raise_on(lib.ns_plan_panels(*args, tiles.ctypes.data, wave_groups.ctypes.data,
-                                 groups.ctypes.data, rows.ctypes.data, last_steps.ctypes.data,
-                                 perm.ctypes.data, cols.ctypes.data), lib)
-    return plan, tiles, wave_groups, groups, rows, last_steps, perm, cols
+    _raise_on(lib.ns_plan_panels(*args, tiles.ctypes.data, tile_ranges.ctypes.data,
+                                 wave_groups.ctypes.data, groups.ctypes.data, rows.ctypes.data,
+                                 last_steps.ctypes.data, perm.ctypes.data, cols.ctypes.data), lib)
+    return plan, tiles, tile_ranges, wave_groups, groups, rows, last_steps, perm, cols
 
 
 def plan_bands_host(rowptr: torch.Tensor, col: torch.Tensor, band_width: int, block_rows: int,
@@ -500,14 +509,20 @@ class PanelLayout(_SlotLayout):
 
     Built once per graph structure on the host from copies of in_rowptr and
     in_col (a synchronisation; set-up only).  Holds the device tables, the
-    slot permutation, the partials workspace and, per weight version
-    and encoding, the weights rearranged into slot order on the device.
-    Launches sharing a layout must be ordered on one stream.
+    slot permutation, the partials workspace, the row ranges' counters and,
+    per weight version and encoding, the weights rearranged into slot order on
+    the device.  Launches sharing a layout must be ordered on one stream.
+    With several panels the panels' sums of a row range are added, and the
+    range's rows updated, either by the tick kernel's last tile of the range
+    (one launch per tick) or by a second kernel (``combine_launch``); the
+    results are bitwise the same.  The last tile updates the whole range on
+    one compute unit, so the default (``combine_launch=None``) takes one launch
+    only for ranges of at most ``ONE_LAUNCH_MAX_RANGE_ROWS`` rows.
     """
 
     def __init__(self, topology, batch: int, device, *, tiles_per_panel: int | None = None,
                  max_panel_width: int | None = None, lane_target: int = LANE_TARGET,
-                 pairs: bool = False) -> None:
+                 pairs: bool = False, combine_launch: bool | None = None) -> None:
         n = topology.n_neurons
         width, _ = panel_geometry(batch)
         panels = -(-n // (min(width, max_panel_width or width) & ~3))
@@ -515,15 +530,23 @@ class PanelLayout(_SlotLayout):
             # One workgroup per compute unit in total.
             units = torch.cuda.get_device_properties(device).multi_processor_count
             tiles_per_panel = max(1, units // panels)
-        plan, tiles, wave_groups, groups, rows, last_steps, perm, cols = plan_panels_host(
-            topology.in_rowptr, topology.in_col, batch, tiles_per_panel, max_panel_width,
-            lane_target, pairs)
-        self.pairs = bool(pairs)
+        plan, tiles, tile_ranges, wave_groups, groups, rows, last_steps, perm, cols = \
+            plan_panels_host(topology.in_rowptr, topology.in_col, batch, tiles_per_panel,
+                             max_panel_width, lane_target, pairs)
+        range_rows = int((tiles.reshape(-1, 4)[:, 2] - tiles.reshape(-1, 4)[:, 1]).max())
+        if combine_launch is None:
+            combine_launch = plan.n_panels > 1 and range_rows > ONE_LAUNCH_MAX_RANGE_ROWS
+        if combine_launch:
+            plan.flags |= PANEL_COMBINE_LAUNCH
+        self.pairs, self.combine_launch = bool(pairs), bool(combine_launch)
         self.batch, self.n = int(batch), n
         self.n_panels, self.n_tiles, self.n_slots = plan.n_panels, plan.n_tiles, plan.n_slots
-        self.n_groups = plan.n_groups
+        self.n_groups, self.n_ranges = plan.n_groups, plan.n_ranges
         self.panel_width = plan.panel_width
         self.tiles = _device_tensor(tiles, device)
+        self.tile_ranges = _device_tensor(tile_ranges, device)
+        # every launch leaves the counters zero again
+        self.range_counters = torch.zeros(plan.n_ranges, dtype=torch.int32, device=device)
         self.wave_groups = _device_tensor(wave_groups, device)
         self.groups = _device_tensor(groups, device)
         self.rows = _device_tensor(rows if rows.size else np.zeros(1, np.uint16), device)
@@ -543,6 +566,8 @@ class PanelLayout(_SlotLayout):
         plan = _PanelPlan()
         ctypes.memmove(ctypes.addressof(plan), ctypes.addressof(self._plan), ctypes.sizeof(plan))
         plan.tiles, plan.wave_groups = self.tiles.data_ptr(), self.wave_groups.data_ptr()
+        plan.tile_ranges = self.tile_ranges.data_ptr()
+        plan.range_counters = self.range_counters.data_ptr()
         plan.groups, plan.rows = self.groups.data_ptr(), self.rows.data_ptr()
         plan.last_steps = self.last_steps.data_ptr()
         plan.col = self.col.data_ptr()

@@ -50,11 +50,12 @@ void check(bool ok, const char* what) {
 struct PanelOut {
   ns_panel_plan plan{};
   int64_t entries = 0;
-  std::vector<int32_t> tiles, wave_groups, groups, perm;
+  std::vector<int32_t> tiles, tile_ranges, wave_groups, groups, perm;
   std::vector<uint16_t> rows, col;
   std::vector<uint32_t> last_steps;
   bool operator==(const PanelOut& o) const {
     return plan.n_panels == o.plan.n_panels && plan.n_slots == o.plan.n_slots &&
+           plan.n_ranges == o.plan.n_ranges && tile_ranges == o.tile_ranges &&
            tiles == o.tiles && wave_groups == o.wave_groups && groups == o.groups &&
            perm == o.perm && rows == o.rows && col == o.col && last_steps == o.last_steps;
   }
@@ -66,10 +67,11 @@ PanelOut plan_panels(const Csr& g, int32_t width, int32_t tiles, int32_t flags) 
   const int32_t* col = g.col.empty() ? nullptr : g.col.data();
   int rc = ns_plan_panels(g.rowptr.data(), col, n, width, tiles, 16, 24, flags, &o.plan,
                           &o.entries, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
-                          nullptr);
+                          nullptr, nullptr);
   check(rc == 0, "panel size query");
   if (rc) return o;
   o.tiles.resize(4 * o.plan.n_tiles);
+  o.tile_ranges.resize(o.plan.n_tiles);
   o.wave_groups.resize(o.plan.n_tiles * 16 + 1);
   o.groups.resize(4 * o.plan.n_groups);
   o.rows.resize(o.entries);
@@ -77,7 +79,7 @@ PanelOut plan_panels(const Csr& g, int32_t width, int32_t tiles, int32_t flags) 
   o.perm.resize(o.plan.n_slots);
   o.col.resize(o.plan.n_slots);
   rc = ns_plan_panels(g.rowptr.data(), col, n, width, tiles, 16, 24, flags, &o.plan, &o.entries,
-                      o.tiles.data(), o.wave_groups.data(), o.groups.data(), o.rows.data(),
+                      o.tiles.data(), o.tile_ranges.data(), o.wave_groups.data(), o.groups.data(), o.rows.data(),
                       o.last_steps.data(), o.perm.data(), o.col.data());
   check(rc == 0, "panel fill");
   return o;
@@ -150,7 +152,8 @@ int main() {
   int64_t entries = 0;
   for (int32_t flags : {0, NS_PANEL_PAIRS})
     check(ns_plan_panels(bad.rowptr.data(), bad.col.data(), 12, 4, 1, 16, 12, flags, &p, &entries,
-                         nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr) != 0,
+                         nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                         nullptr) != 0,
           "panel planner rejects column -1");
   ns_band_plan b{};
   check(ns_plan_bands(bad.rowptr.data(), bad.col.data(), 12, 4, 4, 4, &b, nullptr, nullptr,

@@ -398,3 +398,47 @@ def test_panel_workspace_must_not_overlap_any_operand(lib):
         rc, text = call(lib, args)
         kind = "output" if field.startswith("out_") else "input"
         assert rc != 0 and f"partials workspace overlaps an {kind}" in text, (field, text)
+
+
+def fake_two_panel_plan(n, batch):
+    """Two panels of one row range each, over host arrays (validation only)."""
+    plan, tables = fake_panel_plan(n, batch)
+    width = max(4, -(-n // 8) * 4)
+    partials = np.zeros(2 * 2 * n * batch, np.float32)
+    ranges, counters = np.zeros(2, np.int32), np.zeros(1, np.uint32)
+    tables += [partials, ranges, counters]
+    plan.panel_width, plan.n_panels, plan.n_tiles, plan.n_ranges = width, 2, 2, 1
+    plan.partials, plan.tile_ranges = partials.ctypes.data, ranges.ctypes.data
+    plan.range_counters = counters.ctypes.data
+    return plan, tables
+
+
+def test_panel_range_counters_are_checked(lib):
+    """With several panels the tick kernel's last tile of each row range
+    combines the panels: the ranges and their counters are required, the tiles
+    must be one per panel and range, and the counters may overlap no operand
+    nor the partials workspace."""
+    n, batch = 16, 1
+    args, keep = fake_step_args(n=n, batch=batch)
+    plan, tables = fake_two_panel_plan(n, batch)
+    args.panels = ctypes.addressof(plan)
+    plan.range_counters = None
+    rc, text = call(lib, args)
+    assert rc != 0 and "range counters are required" in text, text
+    plan.range_counters = tables[-1].ctypes.data
+    plan.n_ranges = 2
+    rc, text = call(lib, args)
+    assert rc != 0 and "one per panel for each of 2 row ranges" in text, text
+    plan.n_ranges = 1
+    plan.range_counters = plan.partials
+    rc, text = call(lib, args)
+    assert rc != 0 and "range counters overlap the partials" in text, text
+    plan.range_counters = args.state.data
+    rc, text = call(lib, args)
+    assert rc != 0 and "range counters overlap an input" in text, text
+    plan.range_counters = args.out_state.data
+    rc, text = call(lib, args)
+    assert rc != 0 and "range counters overlap an output" in text, text
+    plan.flags = 4
+    rc, text = call(lib, args)
+    assert rc != 0 and "unknown panel plan flags 4" in text, text

@@ -1,7 +1,8 @@
 """The column-panel tick (batch 1 and 2) on the MI355X.
 
 Several panels are forced with small panel widths so the per-panel partial
-sums and the combine kernel run on small graphs; hub rows take whole
+sums and their combination (in the tick kernel's last tile of each row range,
+or in a second kernel) run on small graphs; hub rows take whole
 wavefronts (64 lanes per row) and rows of every length class mix in one tile.  Bars: float32 within 1e-5 of the
 oracle; fp16/fp8/nvfp4 storage bitwise equal to the panel tick on the
 decoded float32 weights; bitwise repeatable.
@@ -18,6 +19,7 @@ from oracle import precision as op
 from oracle import runtime as ort
 from oracle import topology as otop
 from neurosim_gpu import NativeDendriticMatrixRuntime, SparseTopology, topology_to
+from neurosim_gpu.native import PanelLayout
 
 pytestmark = pytest.mark.gpu
 FIELDS = ("state", "dendritic_state", "adaptation_state")
@@ -61,6 +63,45 @@ def test_panels_match_oracle(gpu, batch, width, tiles, pairs):
     print(f"panels batch={batch} width={width}: {worst:.3e} over 30 ticks "
           f"({native._panels.n_panels} panels, {native._panels.n_tiles} tiles)")
     assert worst <= 1e-5
+
+
+@pytest.mark.parametrize("fmt", ["fp32", "nvfp4"])
+@pytest.mark.parametrize("batch", [1, 2])
+@pytest.mark.parametrize("width,tiles", [(1000, 7), (256, 3), (4096, 40)])
+def test_one_launch_equals_combine_launch(gpu, batch, width, tiles, fmt):
+    """The tick kernel's last tile of each row range adds the panels' sums and
+    updates the range (one launch per tick); a second kernel doing the same
+    (NS_PANEL_COMBINE_LAUNCH) must give bitwise the same states every tick,
+    and every launch leaves the range counters zero."""
+    print(f"case one-launch batch={batch} width={width} tiles={tiles} fmt={fmt}", flush=True)
+    graph, topology, model, params = hub_case(gpu)
+    kwargs = {"weight_format": "nvfp4"} if fmt == "nvfp4" else {}
+    runs = []
+    for combine in (False, True):
+        native = NativeDendriticMatrixRuntime(topology, model,
+                                              torch.zeros(batch, graph.n, device=gpu),
+                                              kernel="panels", panel_width=width,
+                                              panel_tiles=tiles, **kwargs)
+        if combine:
+            native._panels = PanelLayout(topology, batch, gpu, tiles_per_panel=tiles,
+                                         max_panel_width=width, pairs=native._panels.pairs,
+                                         combine_launch=True)
+        runs.append(native)
+    one, two = runs
+    if one._panels.combine_launch:       # ranges too long for one launch by default
+        one._panels = PanelLayout(topology, batch, gpu, tiles_per_panel=tiles,
+                                  max_panel_width=width, pairs=one._panels.pairs,
+                                  combine_launch=False)
+    assert one._panels.n_panels > 1 and not one._panels.combine_launch
+    assert one._panels.n_tiles == one._panels.n_panels * one._panels.n_ranges
+    drive = column_drive(batch).to(gpu)
+    for tick in range(40):
+        for native in runs:
+            native.step(drive if tick < 20 else 0.05, dendritic_drive=0.1)
+        for field in FIELDS:
+            assert torch.equal(getattr(one, field), getattr(two, field)), (tick, field)
+    assert int(one._panels.range_counters.abs().sum()) == 0
+    print(f"one launch: {one._panels.n_panels} panels x {one._panels.n_ranges} ranges bitwise equal")
 
 
 @pytest.mark.parametrize("batch", [1, 2])

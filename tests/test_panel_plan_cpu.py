@@ -42,7 +42,7 @@ GRAPHS = {
 
 def emulate(graph: otop.Graph, batch: int, tiles_per_panel: int, width: int | None,
             source: np.ndarray, lane_target: int = 24, pairs: bool = False):
-    plan, tiles, wave_groups, groups, rows, last_steps, perm, cols = plan_panels_host(
+    plan, tiles, tile_ranges, wave_groups, groups, rows, last_steps, perm, cols = plan_panels_host(
         torch.from_numpy(graph.in_rowptr), torch.from_numpy(graph.in_col), batch, tiles_per_panel,
         width, lane_target, pairs)
     assert plan.flags == (1 if pairs else 0)
@@ -74,6 +74,19 @@ def emulate(graph: otop.Graph, batch: int, tiles_per_panel: int, width: int | No
         assert np.array_equal(np.sort(rows[entry0:entry0 + r1 - r0].astype(np.int64)),
                               np.arange(r1 - r0))
     assert np.all(covered == 1), "each panel's tiles partition the rows"
+    # Row ranges shared by all panels: the tiles of range k are one per panel
+    # and cover the same rows, and the ranges cut the rows in order.
+    R = plan.n_ranges
+    assert R >= 1 and plan.n_tiles == P * R and tile_ranges.size == plan.n_tiles
+    assert tile_ranges.min() == 0 and tile_ranges.max() == R - 1
+    bounds = []
+    for k in range(R):
+        mine = tiles[tile_ranges == k]
+        assert np.array_equal(np.sort(mine[:, 0]), np.arange(P)), "one tile per panel"
+        assert np.all(mine[:, 1] == mine[0, 1]) and np.all(mine[:, 2] == mine[0, 2])
+        bounds.append((mine[0, 1], mine[0, 2]))
+    assert bounds[0][0] == 0 and bounds[-1][1] == n
+    assert all(bounds[k][1] == bounds[k + 1][0] for k in range(R - 1))
 
     rows_of_edge = np.repeat(np.arange(n), np.diff(graph.in_rowptr))
     partial = np.zeros((P, n, batch))
@@ -157,7 +170,7 @@ def test_panel_layout_reproduces_the_csr_product(name, batch, tiles, width, pair
 
 def test_lane_widths_follow_segment_length():
     graph = hub_graph(12_000, 2)
-    plan, tiles, wave_groups, groups, rows, last_steps, perm, cols = plan_panels_host(
+    plan, tiles, tile_ranges, wave_groups, groups, rows, last_steps, perm, cols = plan_panels_host(
         torch.from_numpy(graph.in_rowptr), torch.from_numpy(graph.in_col), 1, 4)
     lg = groups.reshape(-1, 4)[:, 2] & 255
     assert lg.max() == 6, "the 9000-edge hub row takes a whole wavefront"
@@ -166,7 +179,7 @@ def test_lane_widths_follow_segment_length():
 
 def test_waves_are_balanced_within_a_tile():
     graph = otop.random_graph(20_000, 1_000_000, seed=4)
-    plan, tiles, wave_groups, groups, rows, last_steps, perm, cols = plan_panels_host(
+    plan, tiles, tile_ranges, wave_groups, groups, rows, last_steps, perm, cols = plan_panels_host(
         torch.from_numpy(graph.in_rowptr), torch.from_numpy(graph.in_col), 1, 8)
     cost = groups.reshape(-1, 4)[:, 1] + 1
     for t in range(plan.n_tiles):
@@ -185,15 +198,17 @@ def test_planner_rejects_bad_geometry():
     import ctypes
 
     rc = lib.ns_plan_panels(rowptr.ctypes.data, col.ctypes.data, 2, 64, 1, 16, 12, 0,
-                            ctypes.byref(plan), ctypes.byref(entries), *([None] * 7))
+                            ctypes.byref(plan), ctypes.byref(entries), *([None] * 8))
     assert rc != 0 and b"out of range" in lib.ns_last_error()
     col = np.array([0, 1], np.int32)
     rc = lib.ns_plan_panels(rowptr.ctypes.data, col.ctypes.data, 2, 64, 1, 8, 12, 0,
-                            ctypes.byref(plan), ctypes.byref(entries), *([None] * 7))
+                            ctypes.byref(plan), ctypes.byref(entries), *([None] * 8))
     assert rc != 0 and b"wavefronts" in lib.ns_last_error()
-    rc = lib.ns_plan_panels(rowptr.ctypes.data, col.ctypes.data, 2, 64, 1, 16, 12, 2,
-                            ctypes.byref(plan), ctypes.byref(entries), *([None] * 7))
-    assert rc != 0 and b"flags" in lib.ns_last_error()
+    # NS_PANEL_COMBINE_LAUNCH (2) is the caller's to set on a plan, not a layout flag
+    for flags in (2, 4):
+        rc = lib.ns_plan_panels(rowptr.ctypes.data, col.ctypes.data, 2, 64, 1, 16, 12, flags,
+                                ctypes.byref(plan), ctypes.byref(entries), *([None] * 8))
+        assert rc != 0 and b"flags" in lib.ns_last_error()
 
 
 @pytest.mark.parametrize("flags", [0, 1])
@@ -214,7 +229,7 @@ def test_planner_rejects_negative_and_large_columns(flags, rowptr, col, bad):
     plan = native._PanelPlan()
     entries = native._c_i64()
     rc = lib.ns_plan_panels(rowptr.ctypes.data, col.ctypes.data, n, 4, 1, 16, 12, flags,
-                            ctypes.byref(plan), ctypes.byref(entries), *([None] * 7))
+                            ctypes.byref(plan), ctypes.byref(entries), *([None] * 8))
     message = lib.ns_last_error()
     assert rc != 0 and b"out of range" in message
     first = int(np.flatnonzero((col < 0) | (col >= n))[0])
@@ -232,7 +247,8 @@ def test_panel_plan_does_not_depend_on_thread_count(monkeypatch, pairs):
         plans.append(plan_panels_host(torch.from_numpy(graph.in_rowptr),
                                       torch.from_numpy(graph.in_col), 1, 37, 4000, pairs=pairs))
     one, many = plans
-    for field in ("panel_width", "n_panels", "n_tiles", "n_groups", "n_slots", "n_step_words"):
+    for field in ("panel_width", "n_panels", "n_tiles", "n_groups", "n_ranges", "n_slots",
+                  "n_step_words"):
         assert getattr(one[0], field) == getattr(many[0], field)
     for x, y in zip(one[1:], many[1:]):
         assert np.array_equal(x, y)
