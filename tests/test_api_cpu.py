@@ -268,3 +268,37 @@ def test_native_runtime_requires_a_gpu_tensor():
 
     with pytest.raises(ValueError, match="requires CUDA float32"):
         NativeDendriticMatrixRuntime(graph, dynamics, initial)
+
+
+def test_event_scatter_equals_matrix_product_of_the_deltas():
+    from neurosim_gpu.runtime import scatter_out_edges
+
+    graph = random_topology(200, 3000, device="cpu", seed=3, dtype=torch.float64)
+    rng = torch.Generator().manual_seed(5)
+    delta = torch.randn(3, 200, generator=rng, dtype=torch.float64)
+    active = torch.rand(3, 200, generator=rng) < 0.1
+    delta = torch.where(active, delta, torch.zeros_like(delta))
+    expected = delta @ graph.dense_matrix().T
+    torch.testing.assert_close(scatter_out_edges(graph, delta, active), expected,
+                               rtol=1e-12, atol=1e-12)
+    none = torch.zeros_like(active)
+    assert torch.equal(scatter_out_edges(graph, delta, none), torch.zeros_like(delta))
+
+
+def test_auto_policy_samples_every_interval_and_picks_by_edge_fraction():
+    from neurosim_gpu.runtime import _PathPolicy
+
+    graph = random_topology(100, 1000, device="cpu", seed=1)
+    policy = _PathPolicy("auto", 0.12, 4)
+    few = torch.zeros(1, 100, dtype=torch.bool)
+    few[0, int(torch.argmax(graph.out_degree))] = True
+    many = torch.ones(1, 100, dtype=torch.bool)
+    assert policy.choose(0, many, graph, False) == ("matrix", graph.n_edges)
+    assert policy.choose(1, few, graph, False) == ("matrix", -1)      # held until tick 4
+    path, edges = policy.choose(4, few, graph, False)
+    assert path == "event" and edges == int(graph.out_degree.max())
+    assert policy.choose(5, many, graph, True) == ("event", graph.n_edges)   # stats: counted, held
+    assert policy.choose(8, torch.zeros_like(few), graph, False) == ("idle", 0)
+    fixed = _PathPolicy("matrix", 0.12, 4)
+    assert fixed.choose(3, many, graph, False) == ("matrix", -1)
+    assert fixed.choose(3, many, graph, True) == ("matrix", graph.n_edges)

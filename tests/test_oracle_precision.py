@@ -136,3 +136,25 @@ def test_quantize_dequantize_ste_and_validation():
         assert torch.equal(value.grad, torch.ones_like(value))
     with pytest.raises(ValueError, match="precision must be"):
         pp.quantize_dequantize(torch.ones(2), "fp6")
+
+
+def test_product_e2m1_rounding_matches_brute_force():
+    """The product codec rounds on the e2m1 grid's three lattices; brute force:
+    the nearest magnitude, ties to the even code, everything above 6 to 7."""
+    from neurosim_gpu.precision import _NVFP4Codec
+
+    levels = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], np.float32)
+    grid = np.arange(0, 8 * 256 + 1, dtype=np.float32) / 256
+    mids = np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, 6.0], np.float32)
+    near = np.concatenate([np.nextafter(mids, 0), mids, np.nextafter(mids, 9)])
+    x = np.concatenate([grid, near, np.array([7.0, 100.0, 3e38], np.float32)])
+    distance = np.abs(x[:, None].astype(np.float64) - levels[None, :])
+    best = distance.min(1, keepdims=True)
+    candidates = distance == best
+    # ties: the even code of the two; otherwise the only candidate
+    expected = np.where(candidates.sum(1) > 1,
+                        np.argmax(candidates & (np.arange(8) % 2 == 0), 1),
+                        np.argmax(candidates, 1))
+    expected[x > 6] = 7          # float64 distances cannot tell huge values apart
+    got = _NVFP4Codec._nearest_code(torch.from_numpy(x)).numpy()
+    assert np.array_equal(got, expected)
