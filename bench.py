@@ -17,8 +17,10 @@ adds the other workloads, each timed the same way: the batched tick
 B=1, theta 0.02, driven and with inputs withdrawn), the scale-out tick
 (N=1000000, M~100M, B=16, fp8 weights, 200 graph-captured ticks, with the
 CPU oracle on a 10-tick sample), the fp8/NVFP4 device encoding of the
-headline graph's weights, and one recorded tick plus its native backward on
-the headline graph next to autograd through the torch step.
+headline graph's weights, one recorded tick plus its native backward on
+the headline graph next to autograd through the torch step, and headline
+ticks with a new weight version before each.  ``host`` names the CPU model,
+torch and HIP versions; ``cpu_baseline`` also gives the one-thread figure.
 
     python bench.py [--gpus 1] [--steps 1000] [--warmup 50]
 """
@@ -79,6 +81,13 @@ def copy_calibration(mib: int = 256, repeats: int = 10) -> None:
         target.copy_(source)
     torch.cuda.synchronize()
     log(f"copy calibration: {repeats} copies of {mib} MiB")
+
+
+def launches_per_tick(runtime) -> int:
+    """Kernel launches of one tick: two on column panels whose row ranges are
+    finished by the combine kernel, one otherwise."""
+    panels = getattr(runtime, "_panels", None)
+    return 2 if panels is not None and panels.n_panels > 1 and panels.combine_launch else 1
 
 
 def time_ticks(runtime, steps: int, warmup: int) -> tuple[float, MatrixRollout]:
@@ -154,8 +163,8 @@ def column_drive(batch: int, seed: int = 1) -> torch.Tensor:
 
 
 def oracle_tick_ms(topology_cpu, model_cpu, batch: int, drive, ticks: int, warmup: int = 3,
-                   weight=None) -> tuple[float, int]:
-    """ms per float32 tick of the CPU oracle (all host threads)."""
+                   weight=None, threads: int | None = None) -> tuple[float, int]:
+    """ms per float32 tick of the CPU oracle (all host threads unless ``threads``)."""
     sys.path.insert(0, str(ROOT))
     from oracle import dynamics as od
     from oracle import runtime as ort
@@ -169,8 +178,10 @@ def oracle_tick_ms(topology_cpu, model_cpu, batch: int, drive, ticks: int, warmu
         out_weight_index=topology_cpu.out_weight_index.numpy())
     params = od.Params(model_cpu.soma.alpha, model_cpu.soma.gain, model_cpu.dendrite_decay,
                        model_cpu.adaptation_decay, model_cpu.coupling, model_cpu.adaptation_strength)
-    cores = os.cpu_count() or 1
-    threads = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
+    if threads is None:
+        cores = os.cpu_count() or 1
+        threads = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
+    previous = torch.get_num_threads()
     torch.set_num_threads(threads)
     oracle = ort.MatrixOracle(graph, params, torch.zeros(batch, topology_cpu.n_neurons),
                               in_weight=weight)
@@ -179,15 +190,39 @@ def oracle_tick_ms(topology_cpu, model_cpu, batch: int, drive, ticks: int, warmu
     begin = time.perf_counter()
     for _ in range(ticks):
         oracle.step(drive, 0.1)
-    return (time.perf_counter() - begin) * 1000 / ticks, threads
+    elapsed = time.perf_counter() - begin
+    torch.set_num_threads(previous)
+    return elapsed * 1000 / ticks, threads
 
 
-def cpu_baseline(topology_cpu, model_cpu, ticks: int = 20) -> dict:
-    """The CPU oracle's float32 tick on this host (bounded sample, all cores)."""
+def host_info() -> dict:
+    """CPU model (as lscpu names it, from /proc/cpuinfo), thread counts and the
+    software the numbers were taken with."""
+    model = None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cpu_model": model, "host_threads": os.cpu_count(),
+            "torch": torch.__version__, "hip": torch.version.hip,
+            "gpu": torch.cuda.get_device_name(0)}
+
+
+def cpu_baseline(topology_cpu, model_cpu, ticks: int = 20, single_ticks: int = 5) -> dict:
+    """The CPU oracle's float32 tick on this host (bounded samples): on every
+    thread the process may use, and on one thread."""
     ms, threads = oracle_tick_ms(topology_cpu, model_cpu, BATCH, 0.2, ticks)
+    single_ms, _ = oracle_tick_ms(topology_cpu, model_cpu, BATCH, 0.2, single_ticks, warmup=1,
+                                  threads=1)
     return {"value": round(ms, 3), "unit": "ms/tick", "cores": threads, "kind": "port",
             "sample": f"{ticks} fp32 ticks (after 3 warm-up) of the same N=166000 M=24988875 B=1 "
-                      f"graph, torch CPU CSR product + elementwise update, {threads} threads"}
+                      f"graph, torch CPU CSR product + elementwise update, {threads} threads",
+            "single_thread": {"value": round(single_ms, 3), "unit": "ms/tick", "cores": 1,
+                              "sample": f"{single_ticks} fp32 ticks (after 1 warm-up), same "
+                                        "graph and code, one thread"}}
 
 
 def measured_traffic(fmt: str) -> float | None:
@@ -259,7 +294,8 @@ def measure_backward(topology, model, repeats: int = 10) -> dict:
     every parameter, the weights and the state requiring gradients, loss =
     sum of the new state): the native backward against autograd through the
     torch step that the reference runs for such ticks, each timed with HIP
-    events over ``repeats`` forward+backward passes.  The weights do not
+    events over ``repeats`` forward+backward passes (the median pass, and the
+    slowest).  The weights do not
     change between passes, so from the second pass on the native forward runs
     on panels over a slot-order copy of them and the transposed product streams
     a source-major copy (each built once per weight version).
@@ -299,26 +335,72 @@ def measure_backward(topology, model, repeats: int = 10) -> dict:
         try:
             for _ in range(2):
                 once()
-        except RuntimeError as error:      # a torch sparse backward this ROCm build lacks
+        except RuntimeError as error:
+            # torch's sparse CSR backward on this ROCm build asks for an absurd
+            # allocation at this size (HIP out of memory): the leg is skipped.
             out[f"{name}_ms"] = None
-            out[f"{name}_error"] = str(error).splitlines()[0][:200]
+            out[f"{name}_skipped"] = ("torch autograd through the reference step failed: "
+                                      + str(error).splitlines()[0][:160])
             del runtime
+            torch.cuda.empty_cache()
             continue
         torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
+        passes = []
         for _ in range(repeats):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
             once()
-        end.record()
-        torch.cuda.synchronize()
+            end.record()
+            end.synchronize()
+            passes.append(start.elapsed_time(end))
+        ms = sorted(passes)[len(passes) // 2]        # median pass
         if ticks == 1:
-            out[f"{name}_ms"] = round(start.elapsed_time(end) / repeats, 4)
+            out[f"{name}_ms"] = round(ms, 4)
         else:
-            out[f"{name}_ms_per_tick"] = round(start.elapsed_time(end) / repeats / ticks, 4)
+            out[f"{name}_ms_per_tick"] = round(ms / ticks, 4)
+        out[f"{name}_slowest_pass_ms"] = round(max(passes), 4)
         weight.grad = None
         for p in params:
             p.grad = None
         del runtime
+    return out
+
+
+def measure_weight_change(topology, model, device, ticks: int = 20) -> dict:
+    """The headline graph with a new weight version before every tick
+    (``mark_weights_mutated_``, as after an optimizer step or a plasticity
+    update), so each tick first rebuilds what the runtime derives from the
+    weights (the encoded payload, the slot-order copy) and then runs.  ms per
+    tick over ``ticks`` eager ticks, with the weights unchanged next to it."""
+    out = {"workload": f"dendritic matrix tick, N={topology.n_neurons} M={topology.n_edges} B=1, "
+                       "a new weight version before every tick", "ticks": ticks}
+
+    def timed(runtime, mutate: bool) -> float:
+        for _ in range(3):
+            if mutate:
+                topology.mark_weights_mutated_()
+            runtime.step(0.2, dendritic_drive=0.1)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(ticks):
+            if mutate:
+                topology.mark_weights_mutated_()
+            runtime.step(0.2, dendritic_drive=0.1)
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / ticks
+
+    with torch.inference_mode():
+        for fmt in ("fp32", "fp8", "nvfp4"):
+            for kernel in ("auto", "rows"):
+                runtime = build_runtime(fmt, topology, model, device, kernel)
+                out[f"{fmt}_{kernel}"] = {"kernel": runtime.kernel,
+                                          "new_weights_ms_per_tick": round(timed(runtime, True), 4),
+                                          "same_weights_eager_ms_per_tick":
+                                              round(timed(runtime, False), 4)}
+                del runtime
+                torch.cuda.empty_cache()
     return out
 
 
@@ -408,6 +490,12 @@ def measure_pels(device, theta: float = 0.02) -> dict:
 
     result["driven_onset"] = phase(0.2, 0.1)
     result["driven_onset_two_launch"] = phase(0.2, 0.1, two_launch)
+    if theta != 0.0:
+        # theta 0: every changed (neuron, column) emits, the exact matrix-equivalent tick
+        exact = NativeDendriticPELSRuntime(topology, model, torch.zeros(1, n, device=device),
+                                           theta=0.0)
+        result["theta0_driven_onset"] = phase(0.2, 0.1, exact)
+        del exact
     del two_launch
     with torch.inference_mode():
         for _ in range(512):
@@ -482,7 +570,7 @@ def main() -> None:
                           "(batch a multiple of 16) or CSR row blocks")
     cli.add_argument("--copy-calibration", action="store_true",
                      help="only run 256 MiB device copies (PMC byte-counter calibration)")
-    cli.add_argument("--configs", default="encode,backward,batched,pels,scaleout",
+    cli.add_argument("--configs", default="encode,backward,weights,batched,pels,scaleout",
                      help="other workloads to time after the headline one ('none' for none)")
     args = cli.parse_args()
     if args.gpus != 1:
@@ -511,7 +599,9 @@ def main() -> None:
         alg = algorithmic_bytes(fmt, N_NEURONS, m, BATCH)
         results[fmt] = {"ms_per_tick": round(ms, 5), "ticks_per_s": round(1000.0 / ms, 1),
                         "algorithmic_bytes": alg, "achieved_GBps": round(alg / ms / 1e6, 1),
-                        "pct_hbm_peak": round(100 * alg / ms / 1e6 / HBM_PEAK_GBPS, 1)}
+                        "pct_hbm_peak": round(100 * alg / ms / 1e6 / HBM_PEAK_GBPS, 1),
+                        "kernel": runtime.kernel, "launches_per_tick": launches_per_tick(runtime),
+                        "ticks_per_graph": rollout.ticks}
         if fmt == "fp32" and not args.no_mall_flush:
             flushed = mall_flushed_ms(rollout)
             results[fmt]["mall_flushed_ms_per_tick"] = round(flushed, 5)
@@ -529,14 +619,20 @@ def main() -> None:
         "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": WORKLOAD, "n_neurons": N_NEURONS, "n_edges": m, "batch": BATCH,
                    "candidate_edges": CANDIDATES, "seed": SEED, "weights": primary_fmt,
-                   "ticks_per_graph": CHUNK, "kernel": args.kernel},
+                   "ticks_per_graph": primary["ticks_per_graph"], "kernel": primary["kernel"],
+                   "launches_per_tick": primary["launches_per_tick"]},
         "ticks_per_s": primary["ticks_per_s"],
         "achieved_GBps": round(achieved, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": traffic},
         "formats": results,
+        "host": host_info(),
     }
+    if flushed is not None:
+        # the same algorithmic bytes over a tick whose graph was first evicted from the MALL
+        line["roofline"]["frac_mall_flushed"] = round(
+            primary["algorithmic_bytes"] / flushed / 1e6 / HBM_PEAK_GBPS, 4)
     if flushed is not None:
         line["mall_flushed"] = {"ms_per_tick": round(flushed, 5),
                                 "achieved_GBps": round(primary["algorithmic_bytes"] / flushed / 1e6, 1)}
@@ -553,9 +649,13 @@ def main() -> None:
         log("timing backward")
         extra["backward"] = measure_backward(topology, model)
         log(f"backward: {extra['backward']}")
+    if "weights" in configs:
+        log("timing ticks with a new weight version each")
+        extra["weight_change"] = measure_weight_change(topology, model, device)
+        log(f"weight_change: {extra['weight_change']}")
     del topology
     torch.cuda.empty_cache()
-    for name in [c for c in configs if c not in ("encode", "backward")]:
+    for name in [c for c in configs if c not in ("encode", "backward", "weights")]:
         log(f"timing {name}")
         if name == "batched":
             extra[name] = measure_batched(device)

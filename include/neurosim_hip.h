@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 8
+#define NS_ABI_VERSION 9
 
 /* Return codes. */
 #define NS_OK 0
@@ -381,6 +381,21 @@ int ns_plan_panels(const int32_t* rowptr_host, const int32_t* col_host, int64_t 
  * largest panel width and the wavefronts per workgroup (NULL outputs are
  * skipped). */
 int ns_panel_geometry(int64_t batch, int32_t* max_panel_width, int32_t* waves);
+
+/* The weights of a CSR payload (original edge order, format NS_WEIGHT_*)
+ * rearranged into a panel or band layout's slot order: slot k holds edge
+ * perm[k] (perm[k] < 0 or >= n_edges: padding, code 0), as the `weight` (and
+ * `slot_scales`) arrays of ns_panel_plan / ns_band_plan take them.  No
+ * counterpart in the reference (whose kernel reads the CSR in place); it is
+ * what a layout rebuilds when the weights change.  n_slots even.  Outputs:
+ * F32 float[n_slots], F16 uint16[n_slots], E4M3 uint8[n_slots]; NVFP4
+ * uint8[n_slots/2] nibbles (slot 2i low) plus slot_scales uint8[n_slots], or,
+ * with `pairs`, uint16[n_slots/2] words (nibbles low, the pair's first real
+ * edge's block-scale code high) and no slot_scales.  One launch on `stream`. */
+int ns_gather_slot_weights(const int32_t* perm, int64_t n_slots, int64_t n_edges,
+                           int32_t format, int32_t pairs, const void* weight,
+                           const uint8_t* block_scales, void* slots, uint8_t* slot_scales,
+                           void* stream);
 
 
 /* Fused matrix tick.  Replaces dendritic_step

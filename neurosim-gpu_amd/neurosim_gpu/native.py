@@ -35,7 +35,7 @@ import numpy as np
 import torch
 
 _LIB_NAME = "libneurosim_hip.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 WEIGHT_F32, WEIGHT_F16, WEIGHT_E4M3, WEIGHT_NVFP4 = 0, 1, 2, 3
 _PLAN_CACHE = 64   # row plans kept per extension (one per live topology and batch width)
@@ -177,6 +177,9 @@ def load_library() -> ctypes.CDLL:
     lib.ns_plan_panels.argtypes = [_c_ptr, _c_ptr, _c_i64, ctypes.c_int32, ctypes.c_int32,
                                    ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                    ctypes.POINTER(_PanelPlan), ctypes.POINTER(_c_i64)] + [_c_ptr] * 8
+    lib.ns_gather_slot_weights.restype = ctypes.c_int
+    lib.ns_gather_slot_weights.argtypes = [_c_ptr, _c_i64, _c_i64, ctypes.c_int32, ctypes.c_int32,
+                                           _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr]
     lib.ns_plan_bands.restype = ctypes.c_int
     lib.ns_plan_bands.argtypes = [_c_ptr, _c_ptr, _c_i64, ctypes.c_int32, ctypes.c_int32,
                                   ctypes.c_int32, ctypes.POINTER(_BandPlan)] + [_c_ptr] * 5
@@ -451,13 +454,13 @@ def _device_tensor(array: np.ndarray, device) -> torch.Tensor:
 class _SlotLayout:
     """Weights of a CSR payload rearranged into a layout's slot order.
 
-    Subclasses set ``n_slots``, ``perm`` (int64 edge of each slot, 0 for
-    padding) and ``valid`` (slot holds an edge); padding slots get code 0.
+    Subclasses set ``n_slots`` and ``perm`` (int32 on the device: the CSR edge
+    of each slot, -1 for padding); padding slots get code 0.  The copy is made
+    on the device by ns_gather_slot_weights and kept for one weight key.
     """
 
     n_slots: int
     perm: torch.Tensor
-    valid: torch.Tensor
     pairs: bool = False
     _slot_weights: tuple | None = None
     _slot_key = None
@@ -466,41 +469,32 @@ class _SlotLayout:
         """Weights of the CSR payload (original edge order) rearranged into slot order."""
         if self._slot_key == key and self._slot_weights is not None:
             return self._slot_weights
-        with torch.no_grad():
-            if weight.numel() == 0:           # no edges: every slot is padding (code 0)
-                nibbles = block_scales is not None
-                slots = torch.zeros(self.n_slots // 2 if nibbles else self.n_slots,
-                                    dtype=weight.dtype, device=weight.device)
-                scales = (torch.zeros(self.n_slots, dtype=torch.uint8, device=weight.device)
-                          if nibbles else None)
-            elif weight.dtype in (torch.float32, torch.float16):
-                slots = torch.where(self.valid, weight[self.perm], torch.zeros((), dtype=weight.dtype,
-                                                                               device=weight.device))
-                scales = None
-            elif block_scales is None:        # fp8 e4m3 codes
-                slots = torch.where(self.valid, weight[self.perm], torch.zeros((), dtype=torch.uint8,
-                                                                               device=weight.device))
-                scales = None
-            else:                             # nvfp4: one nibble and one block-scale code per slot
-                edge = self.perm
-                nibble = (weight[edge >> 1] >> ((edge & 1) * 4).to(torch.uint8)) & 15
-                nibble = torch.where(self.valid, nibble, torch.zeros_like(nibble))
-                slots = (nibble[0::2] | (nibble[1::2] << 4)).contiguous()
-                if self.pairs:
-                    # Pair layout: both slots of a pair lie in one weight block, so
-                    # the pair's word carries one scale code (the first real slot's).
-                    first_real = self.valid[0::2]
-                    pair_edge = torch.where(first_real, edge[0::2], edge[1::2])
-                    pair_code = torch.where(first_real | self.valid[1::2], block_scales[pair_edge >> 4],
-                                            torch.zeros((), dtype=torch.uint8, device=weight.device))
-                    slots = torch.stack((slots, pair_code), dim=1).contiguous().view(torch.int16)
-                    slots = slots.reshape(-1)
-                    scales = None
-                else:
-                    scales = torch.where(self.valid, block_scales[edge >> 4],
-                                         torch.zeros((), dtype=torch.uint8, device=weight.device))
-            self._slot_weights = (slots.contiguous(), None if scales is None else scales.contiguous())
-            self._slot_key = key
+        device, n = weight.device, self.n_slots
+        nvfp4 = block_scales is not None
+        if not nvfp4:
+            fmt = {torch.float32: WEIGHT_F32, torch.float16: WEIGHT_F16,
+                   torch.uint8: WEIGHT_E4M3}[weight.dtype]
+            slots = torch.empty(n, dtype=weight.dtype, device=device)
+            scales = None
+        elif self.pairs:
+            fmt, slots, scales = WEIGHT_NVFP4, torch.empty(n // 2, dtype=torch.int16, device=device), None
+        else:
+            fmt = WEIGHT_NVFP4
+            slots = torch.empty(n // 2, dtype=torch.uint8, device=device)
+            scales = torch.empty(n, dtype=torch.uint8, device=device)
+        edges = weight.numel() * (2 if nvfp4 else 1)
+        if nvfp4:
+            edges = min(edges, 16 * block_scales.numel())
+        lib = load_library()
+        payload = weight.detach()
+        _raise_on(lib.ns_gather_slot_weights(
+            self.perm.data_ptr(), n, edges, fmt, int(self.pairs and nvfp4),
+            payload.data_ptr() if payload.numel() else None,
+            block_scales.data_ptr() if nvfp4 and block_scales.numel() else None,
+            slots.data_ptr(), scales.data_ptr() if scales is not None else None,
+            ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)), lib)
+        self._slot_weights = (slots, scales)
+        self._slot_key = key
         return self._slot_weights
 
 
@@ -552,9 +546,7 @@ class PanelLayout(_SlotLayout):
         self.rows = _device_tensor(rows if rows.size else np.zeros(1, np.uint16), device)
         self.last_steps = _device_tensor(last_steps.view(np.int32), device)
         self.col = _device_tensor(cols, device)
-        perm_t = torch.from_numpy(perm).to(device)
-        self.valid = perm_t >= 0
-        self.perm = perm_t.clamp_min(0).to(torch.int64)
+        self.perm = torch.from_numpy(perm).to(device)
         # per-panel sums by row, then the same sums in row-table order
         self.partials = torch.empty(2 * plan.n_panels * n * batch, dtype=torch.float32,
                                     device=device)
@@ -624,9 +616,7 @@ class BandLayout(_SlotLayout):
         self.blocks = _device_tensor(blocks, device)
         self.rows = _device_tensor(rows, device)
         self.col = _device_tensor(cols, device)
-        perm_t = torch.from_numpy(perm).to(device)
-        self.valid = perm_t >= 0
-        self.perm = perm_t.clamp_min(0).to(torch.int64)
+        self.perm = torch.from_numpy(perm).to(device)
         self._plan = plan
         self._slot_weights = None
         self._slot_key = None

@@ -36,7 +36,8 @@ def test_every_declared_symbol_is_exported(lib):
                           "ns_encode_weights_no_alloc",
                           "ns_topology_workspace_bytes", "ns_build_topology",
                           "ns_step_backward_workspace_floats", "ns_dendritic_step_backward",
-                          "ns_plan_bands", "ns_band_max_block_rows", "ns_dendritic_step_bands"}
+                          "ns_plan_bands", "ns_band_max_block_rows", "ns_dendritic_step_bands",
+                          "ns_gather_slot_weights"}
     for name in names:
         assert hasattr(lib, name), name
     assert lib.ns_abi_version() == native.ABI_VERSION
@@ -442,3 +443,31 @@ def test_panel_range_counters_are_checked(lib):
     plan.flags = 4
     rc, text = call(lib, args)
     assert rc != 0 and "unknown panel plan flags 4" in text, text
+
+
+def test_slot_gather_validation(lib):
+    """Rejected before any launch (host pointers only)."""
+    perm = np.zeros(8, np.int32)
+    out = np.zeros(8, np.float32)
+    weight = np.zeros(4, np.float32)
+
+    def gather(n_slots=8, n_edges=4, fmt=native.WEIGHT_F32, pairs=0, w=weight, scales=None,
+               slots=out, slot_scales=None, perm_ptr=None):
+        rc = lib.ns_gather_slot_weights(perm_ptr or perm.ctypes.data, n_slots, n_edges, fmt, pairs,
+                                        w.ctypes.data if w is not None else None,
+                                        scales, slots.ctypes.data if slots is not None else None,
+                                        slot_scales, None)
+        return rc, lib.ns_last_error().decode()
+
+    assert gather(n_slots=7) == (1, "n_slots must be even and in [0, 2^32)")
+    assert gather(fmt=7) == (1, "unknown weight format 7")
+    assert gather(pairs=1) == (1, "the pair layout applies to NVFP4 only")
+    assert gather(slots=None) == (1, "perm and slots are required")
+    assert gather(w=None) == (1, "weight is required")
+    assert gather(fmt=native.WEIGHT_NVFP4, pairs=1, w=np.zeros(2, np.uint8)) == (
+        1, "NVFP4 weights require block scales")
+    scales = np.zeros(1, np.uint8)
+    assert gather(fmt=native.WEIGHT_NVFP4, w=np.zeros(2, np.uint8), scales=scales.ctypes.data) == (
+        1, "NVFP4 slots without pairs need slot_scales")
+    assert gather(perm_ptr=perm.ctypes.data + 4) == (1, "perm must be 8-byte aligned")
+    assert gather(n_slots=0) == (0, "")

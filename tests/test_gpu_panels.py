@@ -210,3 +210,38 @@ def test_panel_weight_refresh_after_mutation(gpu):
         native.step(0.2, dendritic_drive=0.1)
         oracle.step(0.2, 0.1)
     assert errors(native, oracle) <= 1e-5
+
+
+@pytest.mark.parametrize("pairs", [False, True])
+def test_slot_gather_matches_host_emulation(gpu, pairs):
+    """ns_gather_slot_weights against a numpy restatement of the slot order:
+    slot k holds edge perm[k] (padding: code 0); NVFP4 nibbles two per byte,
+    scales one per slot or, in pairs, the pair's first real edge's code."""
+    print(f"case slot gather pairs={pairs}", flush=True)
+    graph, topology, model, params = hub_case(gpu, n=6000, seed=9)
+    layout = PanelLayout(topology, 1, gpu, tiles_per_panel=5, max_panel_width=1024, pairs=pairs)
+    perm = layout.perm.cpu().numpy()
+    real = perm >= 0
+    edge = np.where(real, perm, 0)
+    weight32 = topology.in_weight
+    from neurosim_gpu.native import encode_weights
+    codes, block, _ = encode_weights(weight32, "nvfp4")
+    fp8, _, _ = encode_weights(weight32, "fp8")
+    for payload in (weight32, weight32.half(), fp8):
+        slots, scales = layout.slot_weights(("t", payload.dtype), payload, None)
+        host = payload.cpu().numpy()
+        expected = np.where(real, host[edge], np.zeros((), host.dtype))
+        assert scales is None and np.array_equal(slots.cpu().numpy(), expected)
+    slots, scales = layout.slot_weights(("t", "nvfp4"), codes, block)
+    c, b = codes.cpu().numpy(), block.cpu().numpy()
+    nib = np.where(real, (c[edge >> 1] >> ((edge & 1) * 4)) & 15, 0).astype(np.uint8)
+    packed = nib[0::2] | (nib[1::2] << 4)
+    if pairs:
+        first = np.where(real[0::2], edge[0::2], edge[1::2])
+        code = np.where(real[0::2] | real[1::2], b[first >> 4], 0).astype(np.uint16)
+        word = packed.astype(np.uint16) | (code << 8)
+        assert scales is None
+        assert np.array_equal(slots.cpu().numpy().view(np.uint16), word)
+    else:
+        assert np.array_equal(slots.cpu().numpy(), packed)
+        assert np.array_equal(scales.cpu().numpy(), np.where(real, b[edge >> 4], 0))
