@@ -50,25 +50,39 @@ struct EventArgs {
   float* pending_out;
 };
 
+// Everything pair (n, b) reads besides its current.
+struct PairInputs {
+  NeuronParams p;
+  float s, d, a, u, v, emitted, theta;
+};
+
+__device__ __forceinline__ PairInputs load_pair(const EventArgs& A, int64_t n, int64_t b) {
+  return PairInputs{load_params(A.p, n), A.s.get(b, n), A.d.get(b, n), A.a.get(b, n),
+                    A.u.get(b, n),       A.v.get(b, n), A.emitted.get(b, n), A.theta.get(n)};
+}
+
 // Advances pair (n, b) on current j, stores the three states and the
 // emitted state, and returns the pair's delta.
-__device__ __forceinline__ float advance_pair(const EventArgs& A, int64_t n, int64_t b,
-                                              float j) {
-  const NextState x = advance_one(A.p, n, j, A.s.get(b, n), A.d.get(b, n), A.a.get(b, n),
-                                  A.u.get(b, n), A.v.get(b, n));
-  const float previous = A.emitted.get(b, n);
+__device__ __forceinline__ float advance_loaded_pair(const EventArgs& A, int64_t n, int64_t b,
+                                                     float j, const PairInputs& in) {
+  const NextState x = advance_loaded(in.p, j, in.s, in.d, in.a, in.u, in.v);
   float dl;
   {
 #pragma clang fp contract(off)
-    const float residual = x.soma - previous;
-    const bool active = fabsf(residual) >= A.theta.get(n);
+    const float residual = x.soma - in.emitted;
+    const bool active = fabsf(residual) >= in.theta;
     dl = active ? residual : 0.0f;
-    A.oe.put(b, n, previous + dl);
+    A.oe.put(b, n, in.emitted + dl);
   }
   A.os.put(b, n, x.soma);
   A.od.put(b, n, x.dendrite);
   A.oa.put(b, n, x.adaptation);
   return dl;
+}
+
+__device__ __forceinline__ float advance_pair(const EventArgs& A, int64_t n, int64_t b,
+                                              float j) {
+  return advance_loaded_pair(A, n, b, j, load_pair(A, n, b));
 }
 
 __global__ __launch_bounds__(kThreads) void event_advance_kernel(EventArgs A) {
@@ -95,6 +109,8 @@ __device__ __forceinline__ void scatter_chunk(const EventArgs& A, int64_t chunk,
                                               float mine, int64_t start, int64_t end,
                                               float* target, int64_t tb, int64_t tn) {
   const int64_t count = mine != 0.0f ? end - start : 0;
+  // A wavefront without an emitting out-edge has nothing to scatter.
+  if (__ballot(count != 0) == 0) return;
   int64_t incl = count;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
@@ -168,13 +184,17 @@ __global__ __launch_bounds__(kThreads) void event_tick_kernel(EventArgs A) {
   if (i < A.count) {
     const int64_t n = i / A.B;
     const int64_t b = i - n * A.B;
+    // Every load of the pair is issued before its first store, so the pair
+    // waits on memory once.
     start = A.out_rowptr[n];
     end = A.out_rowptr[n + 1];
     float* at = A.current + b * A.csb + n * A.csn;
-    const float j = *at + A.pending_in[i];
+    const float current = *at, pending = A.pending_in[i];
+    const PairInputs in = load_pair(A, n, b);
+    const float j = current + pending;
     *at = j;
     A.pending_in[i] = 0.0f;
-    dl = advance_pair(A, n, b, j);
+    dl = advance_loaded_pair(A, n, b, j, in);
   }
   scatter_chunk(A, chunk, lane, dl, start, end, A.pending_out, 1, A.B);
 }
