@@ -245,8 +245,149 @@ constexpr int kCombineBatch = 8;
 // kPanelThreads * finish_rows rows with at most kCombineBatch panels finishes
 // in one round.
 template <int BT>
-constexpr int finish_rows() {
+constexpr int rows_per_finisher() {
   return BT == 1 ? 4 : 2;
+}
+
+// One launch per tick with several panels: called by every tile after its
+// wavefronts have stored the panel's sums of rows [r0, r1) (agent-scope atomic
+// stores).  The tile counts itself in on its range's counter; the tile that
+// completes the count (all n_panels tiles of the range have stored their
+// sums) sets the counter back to zero for the next launch, then adds each
+// row's sums in panel order and applies the update.  Each round issues every
+// load of its rows (parameters, states, drives, the first kCombineBatch
+// panels' sums) before the first add, so it waits on memory once.
+// Operand views for the finish: global-address-space pointers (the arguments
+// read afresh come back as generic ones) and 32-bit offset arithmetic.
+typedef const __attribute__((address_space(1))) float* gcfloat;
+typedef __attribute__((address_space(1))) float* gfloat;
+
+// Element `i` of `p` as a 32-bit byte offset from the (uniform) base, which
+// the loads and stores take as scalar base plus vector offset.
+template <typename T>
+__device__ __forceinline__ T* element(T* p, uint32_t i) {
+  typedef const __attribute__((address_space(1))) char* raw;
+  return (T*)((raw)p + i * 4u);
+}
+
+template <typename I>
+struct FinishPlane {
+  gcfloat data;
+  I sb, sn;
+  float scalar;
+  uint32_t mask;
+  __device__ __forceinline__ float get(I b, I n) const {
+    const uint32_t x = __builtin_bit_cast(uint32_t, *element(data, b * sb + n * sn));
+    return __builtin_bit_cast(float, (x & mask) | (__builtin_bit_cast(uint32_t, scalar) & ~mask));
+  }
+};
+
+template <typename I>
+struct FinishOut {
+  gfloat data;
+  I sb, sn;
+  __device__ __forceinline__ void put(I b, I n, float x) const { *element(data, b * sb + n * sn) = x; }
+};
+
+template <typename I>
+struct FinishVec {
+  gcfloat data;
+  I stride;
+  __device__ __forceinline__ float get(I n) const { return *element(data, n * stride); }
+};
+
+template <typename I>
+__device__ __forceinline__ FinishPlane<I> finish_view(const Plane& p) {
+  return FinishPlane<I>{(gcfloat)p.data, static_cast<I>(p.sb), static_cast<I>(p.sn), p.scalar, p.mask};
+}
+template <typename I>
+__device__ __forceinline__ FinishOut<I> finish_view(const OutPlane& p) {
+  return FinishOut<I>{(gfloat)p.data, static_cast<I>(p.sb), static_cast<I>(p.sn)};
+}
+
+// Adds the range's sums in panel order and updates rows [r0, r1), with 32-bit
+// offsets (the host launches this path only when every offset fits).
+template <int BT>
+__device__ __forceinline__ void finish_rows(const PanelArgs& A, uint32_t r0, uint32_t r1) {
+  typedef uint32_t I;
+  constexpr int R = rows_per_finisher<BT>();
+  const FinishPlane<I> s = finish_view<I>(A.s), d = finish_view<I>(A.d), a = finish_view<I>(A.a);
+  const FinishPlane<I> u = finish_view<I>(A.u), v = finish_view<I>(A.v);
+  const FinishOut<I> os = finish_view<I>(A.os), od = finish_view<I>(A.od), oa = finish_view<I>(A.oa);
+  const FinishOut<I> oj = finish_view<I>(A.oj);
+  FinishVec<I> prm_v[6];
+#pragma unroll
+  for (int i = 0; i < 6; ++i) prm_v[i] = FinishVec<I>{(gcfloat)A.p.v[i].data, static_cast<I>(A.p.v[i].stride)};
+  const int64_t plane = A.N * BT;
+  auto partial = [&](int p, I n, int j) {
+    const gcfloat base = (gcfloat)A.partials + p * plane;   // uniform
+    return __hip_atomic_load(element(base, n * BT + j), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+  };
+  for (I n0 = r0 + threadIdx.x; n0 < r1; n0 += kPanelThreads * R) {
+    NeuronParams prm[R];
+    float sv[R][BT], dv[R][BT], av[R][BT], uv[R][BT], vv[R][BT];
+    float part[R][kCombineBatch][BT];
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      // Rows past the range and panels past the last reread the last ones
+      // (not used), so that no load waits behind a branch.
+      const I n = min(n0 + static_cast<I>(k * kPanelThreads), r1 - 1);
+      prm[k] = NeuronParams{prm_v[0].get(n), prm_v[1].get(n), prm_v[2].get(n),
+                            prm_v[3].get(n), prm_v[4].get(n), prm_v[5].get(n)};
+#pragma unroll
+      for (int j = 0; j < BT; ++j) {
+        sv[k][j] = s.get(j, n); dv[k][j] = d.get(j, n); av[k][j] = a.get(j, n);
+        uv[k][j] = u.get(j, n); vv[k][j] = v.get(j, n);
+      }
+#pragma unroll
+      for (int q = 0; q < kCombineBatch; ++q)
+#pragma unroll
+        for (int j = 0; j < BT; ++j) part[k][q][j] = partial(min(q, A.n_panels - 1), n, j);
+    }
+    float sum[R][BT];
+#pragma unroll
+    for (int k = 0; k < R; ++k)
+#pragma unroll
+      for (int j = 0; j < BT; ++j) {
+        sum[k][j] = 0.0f;
+#pragma unroll
+        for (int q = 0; q < kCombineBatch; ++q)
+          if (q < A.n_panels) sum[k][j] += part[k][q][j];
+      }
+    for (int p0 = kCombineBatch; p0 < A.n_panels; p0 += kCombineBatch) {
+#pragma unroll
+      for (int k = 0; k < R; ++k) {
+        const I n = min(n0 + static_cast<I>(k * kPanelThreads), r1 - 1);
+#pragma unroll
+        for (int q = 0; q < kCombineBatch; ++q)
+#pragma unroll
+          for (int j = 0; j < BT; ++j) part[k][q][j] = partial(min(p0 + q, A.n_panels - 1), n, j);
+      }
+#pragma unroll
+      for (int k = 0; k < R; ++k)
+#pragma unroll
+        for (int q = 0; q < kCombineBatch; ++q)
+#pragma unroll
+          for (int j = 0; j < BT; ++j)
+            if (p0 + q < A.n_panels) sum[k][j] += part[k][q][j];
+    }
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      const I n = n0 + static_cast<I>(k * kPanelThreads);
+      if (n < r1) {
+#pragma unroll
+        for (int j = 0; j < BT; ++j) {
+          const NextState x = advance_loaded(prm[k], sum[k][j], sv[k][j], dv[k][j], av[k][j],
+                                             uv[k][j], vv[k][j]);
+          os.put(j, n, x.soma);
+          od.put(j, n, x.dendrite);
+          oa.put(j, n, x.adaptation);
+          if (A.oj.data) oj.put(j, n, sum[k][j]);
+        }
+      }
+    }
+  }
 }
 
 // One launch per tick with several panels: called by every tile after its
@@ -274,75 +415,7 @@ __device__ __forceinline__ void finish_range(const PanelArgs& A, int64_t r0, int
   }
   __syncthreads();
   if (!last) return;
-  constexpr int R = finish_rows<BT>();
-  const int64_t plane = A.N * BT;
-  auto partial = [&](int p, int64_t n, int j) {
-    return __hip_atomic_load(A.partials + p * plane + n * BT + j, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-  };
-  for (int64_t n0 = r0 + threadIdx.x; n0 < r1; n0 += kPanelThreads * R) {
-    NeuronParams prm[R];
-    float s[R][BT], d[R][BT], a[R][BT], u[R][BT], v[R][BT];
-    float part[R][kCombineBatch][BT];
-#pragma unroll
-    for (int k = 0; k < R; ++k) {
-      // Rows past the range and panels past the last reread the last ones
-      // (not used), so that no load waits behind a branch.
-      const int64_t n = min(n0 + k * kPanelThreads, r1 - 1);
-      prm[k] = load_params(A.p, n);
-#pragma unroll
-      for (int j = 0; j < BT; ++j) {
-        s[k][j] = A.s.get(j, n); d[k][j] = A.d.get(j, n); a[k][j] = A.a.get(j, n);
-        u[k][j] = A.u.get(j, n); v[k][j] = A.v.get(j, n);
-      }
-#pragma unroll
-      for (int q = 0; q < kCombineBatch; ++q)
-#pragma unroll
-        for (int j = 0; j < BT; ++j) part[k][q][j] = partial(min(q, A.n_panels - 1), n, j);
-    }
-    float sum[R][BT];
-#pragma unroll
-    for (int k = 0; k < R; ++k)
-#pragma unroll
-      for (int j = 0; j < BT; ++j) {
-        sum[k][j] = 0.0f;
-#pragma unroll
-        for (int q = 0; q < kCombineBatch; ++q)
-          if (q < A.n_panels) sum[k][j] += part[k][q][j];
-      }
-    for (int p0 = kCombineBatch; p0 < A.n_panels; p0 += kCombineBatch) {
-#pragma unroll
-      for (int k = 0; k < R; ++k) {
-        const int64_t n = min(n0 + k * kPanelThreads, r1 - 1);
-#pragma unroll
-        for (int q = 0; q < kCombineBatch; ++q)
-#pragma unroll
-          for (int j = 0; j < BT; ++j) part[k][q][j] = partial(min(p0 + q, A.n_panels - 1), n, j);
-      }
-#pragma unroll
-      for (int k = 0; k < R; ++k)
-#pragma unroll
-        for (int q = 0; q < kCombineBatch; ++q)
-#pragma unroll
-          for (int j = 0; j < BT; ++j)
-            if (p0 + q < A.n_panels) sum[k][j] += part[k][q][j];
-    }
-#pragma unroll
-    for (int k = 0; k < R; ++k) {
-      const int64_t n = n0 + k * kPanelThreads;
-      if (n < r1) {
-#pragma unroll
-        for (int j = 0; j < BT; ++j) {
-          const NextState x = advance_loaded(prm[k], sum[k][j], s[k][j], d[k][j], a[k][j],
-                                             u[k][j], v[k][j]);
-          A.os.put(j, n, x.soma);
-          A.od.put(j, n, x.dendrite);
-          A.oa.put(j, n, x.adaptation);
-          if (A.oj.data) A.oj.put(j, n, sum[k][j]);
-        }
-      }
-    }
-  }
+  finish_rows<BT>(A, static_cast<uint32_t>(r0), static_cast<uint32_t>(r1));
 }
 
 template <int BT, int FMT>
@@ -716,7 +789,8 @@ int panel_step(const ns_step_args& a, hipStream_t stream) {
   for (int i = 0; i < 6; ++i) A.p.v[i] = Vec{a.params[i].data, a.params[i].stride};
   A.width = pl.panel_width; A.n_panels = pl.n_panels;
   A.tiles = pl.tiles; A.wave_groups = pl.wave_groups;
-  if (one_launch) { A.tile_ranges = pl.tile_ranges; A.counters = pl.range_counters; } A.groups = pl.groups; A.rows = pl.rows;
+  A.groups = pl.groups; A.rows = pl.rows;
+  if (one_launch) { A.tile_ranges = pl.tile_ranges; A.counters = pl.range_counters; }
   A.last_steps = pl.last_steps;
   A.col = pl.col; A.weight = pl.weight; A.slot_scales = pl.slot_scales;
   A.gscale = a.matrix.global_scale;
@@ -727,6 +801,24 @@ int panel_step(const ns_step_args& a, hipStream_t stream) {
   const bool aligned = reinterpret_cast<uintptr_t>(a.state.data) % 16 == 0;
   A.s_vec = aligned && ((a.batch == 1 && a.state.stride_n == 1) ||
                         (a.batch == 2 && a.state.stride_b == 1 && a.state.stride_n == 2));
+  {
+    // 32-bit offsets in the one-launch finish: every stride non-negative and
+    // every element offset (and n * B + b of the partials) below 2^30, so
+    // byte offsets fit 32 bits.
+    const int64_t B = a.batch, N = a.n_neurons, limit = int64_t{1} << 30;
+    auto fits = [&](int64_t sb, int64_t sn) {
+      return sb >= 0 && sn >= 0 && (B - 1) * sb + (N - 1) * sn < limit;
+    };
+    bool ok = N * B < limit;
+    const Plane ins[5] = {A.s, A.d, A.a, A.u, A.v};
+    for (const Plane& q : ins) ok = ok && fits(q.sb, q.sn);
+    const OutPlane outs[4] = {A.os, A.od, A.oa, A.oj};
+    for (const OutPlane& q : outs) ok = ok && fits(q.sb, q.sn);
+    for (int i = 0; i < 6; ++i) ok = ok && fits(0, A.p.v[i].stride);
+    // The one-launch finish addresses with 32-bit offsets; otherwise the
+    // combine kernel finishes the tick (bitwise the same results).
+    if (!ok) { A.tile_ranges = nullptr; A.counters = nullptr; }
+  }
   const int fmt = a.matrix.format == NS_WEIGHT_NVFP4 && pairs ? kNvfp4Pairs : a.matrix.format;
   const hipError_t err = a.batch == 1 ? launch_panels<1>(A, fmt, pl.n_tiles, stream)
                                       : launch_panels<2>(A, fmt, pl.n_tiles, stream);
