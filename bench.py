@@ -60,9 +60,18 @@ def weight_bytes(fmt: str, m: int) -> int:
             "nvfp4": (m + 1) // 2 + (m + 15) // 16 + 4}[fmt]
 
 
-def algorithmic_bytes(fmt: str, n: int, m: int, batch: int) -> int:
-    """rowptr + col + weights + s,d,a reads + s,d,a writes + six parameter vectors."""
-    return 4 * (n + 1) + 4 * m + weight_bytes(fmt, m) + 24 * batch * n + 24 * n
+def parameter_bytes(model, n: int) -> int:
+    """Bytes of the six parameter vectors: 4N each, 4 for a stride-0 (scalar) one."""
+    vectors = (model.soma.alpha, model.soma.gain, model.dendrite_decay, model.adaptation_decay,
+               model.coupling, model.adaptation_strength)
+    return sum(4 if v.stride(0) == 0 else 4 * n for v in vectors)
+
+
+def algorithmic_bytes(fmt: str, n: int, m: int, batch: int, params: int | None = None) -> int:
+    """rowptr + col + weights + s,d,a reads + s,d,a writes + the parameter vectors
+    (``params`` bytes; six full vectors when not given)."""
+    params = 24 * n if params is None else params
+    return 4 * (n + 1) + 4 * m + weight_bytes(fmt, m) + 24 * batch * n + params
 
 
 def build_runtime(fmt: str, topology, model, device, kernel: str = "auto"):
@@ -143,18 +152,17 @@ def mall_flushed_ms(rollout: MatrixRollout, ticks: int = 20) -> float:
 
 
 def standard_model(n: int, device):
-    """alpha .72, gain .8, dt 1, tau_d 4, tau_a 25, coupling .5, strength .2
-    (rho = exp(-dt/tau) computed on the host), as (host model, device model)."""
-    soma = Dynamics(torch.full((n,), .72), torch.full((n,), .8))
-    model_cpu = DendriticDynamics.from_time_constants(soma, dt=1., tau_dendrite=4.,
-                                                      tau_adaptation=25., coupling=.5,
-                                                      adaptation_strength=.2)
-    model = DendriticDynamics(Dynamics(soma.alpha.to(device), soma.gain.to(device)),
-                              model_cpu.dendrite_decay.to(device),
-                              model_cpu.adaptation_decay.to(device),
-                              model_cpu.coupling.to(device),
-                              model_cpu.adaptation_strength.to(device))
-    return model_cpu, model
+    """alpha .72, gain .8, dt 1, tau_d 4, tau_a 25, coupling .5, strength .2, as
+    (host model, device model).  Each is built where it lives, as the reference's
+    benchmark builds its model on the GPU (benchmarks/compartmental.py:62-65):
+    alpha, gain and the two retention factors are [N] vectors, coupling and
+    strength stride-0 views of one scalar."""
+    def build(where):
+        soma = Dynamics(torch.full((n,), .72, device=where), torch.full((n,), .8, device=where))
+        return DendriticDynamics.from_time_constants(soma, dt=1., tau_dendrite=4.,
+                                                     tau_adaptation=25., coupling=.5,
+                                                     adaptation_strength=.2)
+    return build("cpu"), build(device)
 
 
 def column_drive(batch: int, seed: int = 1) -> torch.Tensor:
@@ -413,7 +421,7 @@ def measure_batched(device) -> dict:
     runtime = NativeDendriticMatrixRuntime(topology_to(topology_cpu, device), model,
                                            torch.zeros(batch, n, device=device))
     ms = rollout_ms(runtime, 100, 10, column_drive(batch).to(device), 0.1)
-    alg = algorithmic_bytes("fp32", n, m, batch) + 4 * batch
+    alg = algorithmic_bytes("fp32", n, m, batch, parameter_bytes(model, n)) + 4 * batch
     return {"workload": f"dendritic matrix tick, N={n} M={m} B={batch}, fp32 weights, "
                         "per-column drive", "kernel": runtime.kernel,
             "ms_per_tick": round(ms, 5), "algorithmic_bytes": alg,
@@ -528,7 +536,7 @@ def measure_scaleout(device, cpu_sample: bool) -> dict:
     layout_s = time.perf_counter() - start
     drive = column_drive(batch)
     ms = rollout_ms(runtime, 100, 2, drive.to(device), 0.1)
-    alg = algorithmic_bytes("fp8", n, m, batch) + 4 * batch
+    alg = algorithmic_bytes("fp8", n, m, batch, parameter_bytes(model, n)) + 4 * batch
     result = {"workload": f"dendritic matrix tick, N={n} M={m} B={batch}, fp8 e4m3 weights, "
                           "per-column drive", "kernel": runtime.kernel, "ticks": 200,
               "ms_per_tick": round(ms, 5), "algorithmic_bytes": alg,
@@ -596,7 +604,7 @@ def main() -> None:
         log(f"timing {fmt}: {args.warmup} warm-up + {args.steps} ticks")
         runtime = build_runtime(fmt, topology, model, device, args.kernel)
         ms, rollout = time_ticks(runtime, args.steps, args.warmup)
-        alg = algorithmic_bytes(fmt, N_NEURONS, m, BATCH)
+        alg = algorithmic_bytes(fmt, N_NEURONS, m, BATCH, parameter_bytes(model, N_NEURONS))
         results[fmt] = {"ms_per_tick": round(ms, 5), "ticks_per_s": round(1000.0 / ms, 1),
                         "algorithmic_bytes": alg, "achieved_GBps": round(alg / ms / 1e6, 1),
                         "pct_hbm_peak": round(100 * alg / ms / 1e6 / HBM_PEAK_GBPS, 1),
