@@ -498,12 +498,20 @@ def measure_pels(device, theta: float = 0.02) -> dict:
 
     result["driven_onset"] = phase(0.2, 0.1)
     result["driven_onset_two_launch"] = phase(0.2, 0.1, two_launch)
+    # The same onset with the emitted deltas propagated by the matrix product
+    # (current += W @ delta after an advance-only launch) instead of the scatter.
+    by_matrix = NativeDendriticPELSRuntime(topology, model, torch.zeros(1, n, device=device),
+                                           theta=theta, propagation="matrix")
+    result["driven_onset_matrix"] = phase(0.2, 0.1, by_matrix)
+    del by_matrix
     if theta != 0.0:
         # theta 0: every changed (neuron, column) emits, the exact matrix-equivalent tick
-        exact = NativeDendriticPELSRuntime(topology, model, torch.zeros(1, n, device=device),
-                                           theta=0.0)
-        result["theta0_driven_onset"] = phase(0.2, 0.1, exact)
-        del exact
+        for name, propagation in (("theta0_driven_onset", "event"),
+                                  ("theta0_driven_onset_matrix", "matrix")):
+            exact = NativeDendriticPELSRuntime(topology, model, torch.zeros(1, n, device=device),
+                                               theta=0.0, propagation=propagation)
+            result[name] = phase(0.2, 0.1, exact)
+            del exact
     del two_launch
     with torch.inference_mode():
         for _ in range(512):

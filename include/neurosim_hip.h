@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 9
+#define NS_ABI_VERSION 10
 
 /* Return codes. */
 #define NS_OK 0
@@ -252,7 +252,17 @@ typedef struct ns_event_args {
      weight[weight_index[e]], so the scatter streams them instead of gathering
      through weight_index (NULL: gather). */
   const float* out_weight;
+  int32_t flags;               /* NS_EVENT_* */
+  int32_t reserved;
 } ns_event_args;
+
+/* ns_event_args flag: run the advance and emission only (the two-launch
+ * tick's first kernel; `delta` required, one-launch buffers not allowed) and
+ * leave the propagation of `delta` to the caller, for instance as
+ * current += W @ delta with ns_csr_spmm (`accumulate`): the reference's matrix
+ * propagation of emitted deltas (runtime.py:233-235), which beats the scatter
+ * when many sources emit. */
+#define NS_EVENT_ADVANCE_ONLY 1
 
 /* Arguments of a plain CSR product J = W @ S (no neuron update). */
 typedef struct ns_spmm_args {
@@ -262,6 +272,9 @@ typedef struct ns_spmm_args {
   ns_csr matrix;
   ns_row_plan plan;
   ns_out_plane out;            /* J, [B,N]; must not overlap `source` */
+  int32_t accumulate;          /* nonzero: out += W @ S (every (b, n) of `out` a distinct
+                                  element) instead of out = W @ S */
+  int32_t reserved;
 } ns_spmm_args;
 
 /* Arguments of the backward of one fused matrix tick (float32 weights). */

@@ -225,22 +225,19 @@ extern "C" int ns_dendritic_event(const ns_event_args* args, void* stream) {
   {
     // The current is updated in place, one element per (b, n): no two pairs
     // may share an element (a zero stride, or strides that interleave).
-    const int64_t B = a.batch, N = a.n_neurons;
-    const int64_t sb = a.current_stride_b < 0 ? -a.current_stride_b : a.current_stride_b;
-    const int64_t sn = a.current_stride_n < 0 ? -a.current_stride_n : a.current_stride_n;
-    const bool distinct = B == 1 ? (N == 1 || sn > 0)
-                          : N == 1 ? sb > 0
-                                   : (sn > 0 && sb >= N * sn) || (sb > 0 && sn >= B * sb);
-    if (!distinct)
+    if (!distinct_elements(a.current_stride_b, a.current_stride_n, a.batch, a.n_neurons))
       return fail("the persistent current must not overlap itself (strides %lld, %lld)",
                   (long long)a.current_stride_b, (long long)a.current_stride_n);
   }
   if (!a.out_state.data || !a.out_dendrite.data || !a.out_adaptation.data ||
       !a.out_emitted.data)
     return fail("four output planes are required");
+  if (a.flags & ~NS_EVENT_ADVANCE_ONLY) return fail("unknown event flags %d", a.flags);
+  const bool advance_only = (a.flags & NS_EVENT_ADVANCE_ONLY) != 0;
   const bool fused = a.pending_in || a.pending_out;
   if (fused && !(a.pending_in && a.pending_out))
     return fail("pending_in and pending_out go together");
+  if (fused && advance_only) return fail("the advance-only tick takes no pending buffers");
   if (!fused && !a.delta) return fail("a delta workspace is required");
   const int64_t B = a.batch, N = a.n_neurons;
   // Written memory: the four planes, then the delta workspace or the two
@@ -301,6 +298,7 @@ extern "C" int ns_dendritic_event(const ns_event_args* args, void* stream) {
   event_advance_kernel<<<dim3(static_cast<unsigned>(advance_blocks)), dim3(kThreads), 0, s>>>(A);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail_launch("event advance", err);
+  if (advance_only) return NS_OK;
   const int64_t scatter_blocks = (A.count + kThreads - 1) / kThreads;
   event_scatter_kernel<<<dim3(static_cast<unsigned>(scatter_blocks)), dim3(kThreads), 0, s>>>(A);
   err = hipGetLastError();

@@ -38,6 +38,16 @@ inline Extent extent(const ns_out_plane& p, int64_t b, int64_t n) {
   return extent_of(p.data, p.stride_b, p.stride_n, b, n);
 }
 
+// Whether a [B,N] view with strides (sb, sn) gives every (b, n) its own element
+// (no zero stride, and the two strides do not interleave).
+inline bool distinct_elements(int64_t sb, int64_t sn, int64_t B, int64_t N) {
+  sb = sb < 0 ? -sb : sb;
+  sn = sn < 0 ? -sn : sn;
+  if (B <= 1) return N <= 1 || sn > 0;
+  if (N <= 1) return sb > 0;
+  return (sn > 0 && sb >= N * sn) || (sb > 0 && sn >= B * sb);
+}
+
 inline bool overlaps(const Extent& x, const Extent& y) {
   if (x.lo == x.hi || y.lo == y.hi) return false;
   return x.lo < y.hi && y.lo < x.hi;

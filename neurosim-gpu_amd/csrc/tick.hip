@@ -66,6 +66,7 @@ struct TickArgs {
   int32_t quad_loads;   // col/weight pointers aligned for one-quad vector loads
   int32_t s_vec4;       // s is neuron-major with 16-byte aligned column groups
   int32_t spmm_only;    // write j to `os` instead of advancing
+  int32_t spmm_accumulate;  // with spmm_only: add j to `os` instead
 };
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -140,7 +141,7 @@ __device__ __forceinline__ float load_weight(const TickArgs& A, int64_t e, float
 
 __device__ __forceinline__ void finish(const TickArgs& A, int64_t n, int64_t b, float j) {
   if (A.spmm_only) {
-    A.os.put(b, n, j);
+    A.os.put(b, n, A.spmm_accumulate ? A.os.data[b * A.os.sb + n * A.os.sn] + j : j);
     return;
   }
   const NextState x = advance_one(A.p, n, j, A.s.get(b, n), A.d.get(b, n), A.a.get(b, n),
@@ -327,7 +328,8 @@ __global__ __launch_bounds__(kThreads) void tick_kernel(TickArgs A) {
     for (int off = cols_at_once; off < group; off <<= 1) acc += __shfl_xor(acc, off, 64);
     if (row_ok && h == 0 && b0 + j < A.B) {
       if (A.spmm_only) {
-        A.os.put(b0 + j, n, acc);
+        const int64_t b = b0 + j;
+        A.os.put(b, n, A.spmm_accumulate ? A.os.data[b * A.os.sb + n * A.os.sn] + acc : acc);
       } else {
         const NextState x = advance_loaded(prm, acc, us[round], ud[round], ua[round], uu[round],
                                            uv[round]);
@@ -531,7 +533,9 @@ extern "C" int ns_csr_spmm(const ns_spmm_args* args, void* stream) {
   if (!a.out.data) return fail("an output plane is required");
   if (overlaps(extent(a.out, a.batch, a.n_neurons), extent(a.source, a.batch, a.n_neurons)))
     return fail("output plane must not overlap the source");
-  if (a.batch == 0) return NS_OK;
+  if (a.accumulate && !distinct_elements(a.out.stride_b, a.out.stride_n, a.batch, a.n_neurons))
+    return fail("an accumulated output plane must not overlap itself (strides %lld, %lld)",
+                (long long)a.out.stride_b, (long long)a.out.stride_n);
 
   TickArgs A{};
   A.N = a.n_neurons; A.B = a.batch; A.M = a.matrix.n_edges;
@@ -543,6 +547,7 @@ extern "C" int ns_csr_spmm(const ns_spmm_args* args, void* stream) {
   A.quad_loads = quad_aligned(a.matrix);
   A.s_vec4 = neuron_major_vec4(a.source, a.batch);
   A.spmm_only = 1;
+  A.spmm_accumulate = a.accumulate != 0;
   const hipError_t err = launch_tick(A, a.matrix.format, static_cast<hipStream_t>(stream));
   if (err != hipSuccess) return fail_launch("CSR product", err);
   return NS_OK;

@@ -35,7 +35,7 @@ import numpy as np
 import torch
 
 _LIB_NAME = "libneurosim_hip.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 WEIGHT_F32, WEIGHT_F16, WEIGHT_E4M3, WEIGHT_NVFP4 = 0, 1, 2, 3
 _PLAN_CACHE = 64   # row plans kept per extension (one per live topology and batch width)
@@ -111,12 +111,15 @@ class _EventArgs(ctypes.Structure):
                 ("out_state", _OutPlane), ("out_dendrite", _OutPlane),
                 ("out_adaptation", _OutPlane), ("out_emitted", _OutPlane),
                 ("delta", _c_ptr), ("pending_in", _c_ptr), ("pending_out", _c_ptr),
-                ("out_weight", _c_ptr)]
+                ("out_weight", _c_ptr), ("flags", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+
+EVENT_ADVANCE_ONLY = 1   # NS_EVENT_ADVANCE_ONLY
 
 
 class _SpmmArgs(ctypes.Structure):
     _fields_ = [("n_neurons", _c_i64), ("batch", _c_i64), ("source", _Plane),
-                ("matrix", _Csr), ("plan", _RowPlan), ("out", _OutPlane)]
+                ("matrix", _Csr), ("plan", _RowPlan), ("out", _OutPlane),
+                ("accumulate", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
 class _StepGradArgs(ctypes.Structure):
@@ -755,7 +758,7 @@ class NativeExtension:
     def dendritic_event(self, state, dendrite, adaptation, params, current, emitted, theta,
                         rowptr, dst, weight_index, weight, input, input_scalar,
                         dendritic_input, dendritic_scalar, delta=None, pending=None,
-                        out_weight=None):
+                        out_weight=None, advance_only=False):
         """One PELS tick (ns_dendritic_event); returns the four new planes.
 
         Without ``pending`` the tick is two launches and ``current`` is updated
@@ -765,7 +768,10 @@ class NativeExtension:
         is added into pending_out (zero on entry), so the persistent current
         afterwards is current + pending_out.  ``out_weight`` optionally gives
         the weights in source-major order (``weight[weight_index]``), which the
-        scatter then streams instead of gathering."""
+        scatter then streams instead of gathering.  ``advance_only`` runs the
+        advance and emission only (NS_EVENT_ADVANCE_ONLY): ``delta`` (entry
+        n*B + b) receives the emitted deltas and ``current`` is left as it was,
+        for the caller to propagate."""
         _check_state(state)
         args = _EventArgs()
         args.state = _plane(state, state, "state")
@@ -805,6 +811,10 @@ class NativeExtension:
                     or out_weight.device != state.device):
                 raise RuntimeError("out_weight must be M contiguous float32 on the state's device")
             args.out_weight = out_weight.data_ptr()
+        if advance_only:
+            if pending is not None:
+                raise RuntimeError("the advance-only tick takes no pending buffers")
+            args.flags = EVENT_ADVANCE_ONLY
         if pending is not None:
             pending_in, pending_out = pending
             for buffer in (pending_in, pending_out):
@@ -894,7 +904,11 @@ class NativeExtension:
         _raise_on(self.lib.ns_dendritic_step_backward(ctypes.byref(args), stream), self.lib)
         return (*planes[:3], d_drive, d_dendritic, d_weight, d_params)
 
-    def csr_spmm(self, source, rowptr, col, weight, block_scales=None, global_scale=None):
+    def csr_spmm(self, source, rowptr, col, weight, block_scales=None, global_scale=None, *,
+                 accumulate_into=None):
+        """W @ source as a new neuron-major [B,N] plane, or, with
+        ``accumulate_into`` (a [B,N] float32 tensor on the device whose elements
+        are distinct), added into that tensor in place, which is returned."""
         _check_state(source)
         args = _SpmmArgs()
         args.source = _plane(source, source, "source")
@@ -902,7 +916,14 @@ class NativeExtension:
         batch, n = source.shape
         args.n_neurons, args.batch = n, batch
         args.plan = self.plan_for(rowptr, batch)
-        (out,) = new_planes(1, batch, n, source)
+        if accumulate_into is None:
+            (out,) = new_planes(1, batch, n, source)
+        else:
+            out = accumulate_into
+            _check_float(out, source, "accumulated output")
+            if out.shape != source.shape:
+                raise RuntimeError("the accumulated output must be [B,N]")
+            args.accumulate = 1
         args.out = _out(out)
         stream = torch.cuda.current_stream(source.device).cuda_stream
         _raise_on(self.lib.ns_csr_spmm(ctypes.byref(args), stream), self.lib)

@@ -410,7 +410,11 @@ class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
     graph use fixed buffers: replays of an even number of ticks chain as they
     are, after an odd number read ``persistent_current`` (which folds) before
     the next replay.  ``one_launch=False`` runs
-    the two-launch tick (advance, then scatter into the current).  Float32
+    the two-launch tick (advance, then scatter into the current).
+    ``propagation="matrix"`` propagates the emitted deltas as the reference's
+    matrix path does (runtime.py:233-235), current += W @ delta over the
+    destination-major CSR, after an advance-only launch: no atomics, so it is
+    the faster choice when many sources emit (theta = 0, driven onsets).  Float32
     atomics make the scatter's summation order, and therefore the last bits
     of the current, run-dependent.  Statistics and autograd requests use the
     reference step.
@@ -422,15 +426,19 @@ class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
 
     def __init__(self, topology: SparseTopology, dynamics: DendriticDynamics,
                  initial_state: torch.Tensor, *, theta: float | torch.Tensor,
-                 extension=None, one_launch: bool = True) -> None:
+                 extension=None, one_launch: bool = True, propagation: str = "event") -> None:
         _require_gpu_float32(initial_state)
+        if propagation not in ("event", "matrix"):
+            raise ValueError("native PELS propagation must be 'event' or 'matrix'")
         self._pending = None
         self.extension = extension if extension is not None else load_native_extension()
-        super().__init__(topology, dynamics, initial_state, theta=theta, propagation="event")
+        super().__init__(topology, dynamics, initial_state, theta=theta, propagation=propagation)
         self._init_native(initial_state, self.extension)
         batch, n = initial_state.shape
         self.source_major_weights = SourceMajorWeights(build_after=1)
-        if one_launch and isinstance(self.extension, NativeExtension):
+        if propagation == "matrix" or not isinstance(self.extension, NativeExtension):
+            one_launch = False
+        if one_launch:
             self._pending = torch.zeros(2, batch * n, dtype=torch.float32,
                                         device=initial_state.device)
             self._parity = 0
@@ -499,9 +507,12 @@ class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
         # pending buffers are separate, so nothing outstanding is lost.
         if not self._current.is_contiguous():
             self._current = self._current.contiguous()
+        matrix = self.propagation == "matrix" and isinstance(self.extension, NativeExtension)
         if self._pending is not None:
             # pending[parity] holds the last tick's scatter (or zeros); the other is zero.
             extra = {"pending": (self._pending[self._parity], self._pending[1 - self._parity])}
+        elif matrix:
+            extra = {"delta": self._delta, "advance_only": True}
         elif isinstance(self.extension, NativeExtension):
             extra = {"delta": self._delta}
         else:
@@ -515,8 +526,16 @@ class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
                 self._current, self.emitted_state, self.theta,
                 self.topology.out_rowptr, self.topology.dst, self.topology.out_weight_index,
                 self.topology.in_weight, u, us, v, vs, **extra))
+        if matrix:
+            # current += W @ delta over the destination-major CSR: the matrix
+            # propagation of the emitted deltas (entry n*B + b of the workspace).
+            batch, n = self.state.shape
+            delta = torch.as_strided(self._delta, (batch, n), (1, batch))
+            topology = self.topology
+            self.extension.csr_spmm(delta, topology.in_rowptr, topology.in_col,
+                                    topology.in_weight, accumulate_into=self._current)
         if self._pending is not None:
             self._parity ^= 1
         self._tick += 1
-        self.last_backend = "native"
+        self.last_backend = "native-matrix" if matrix else "native"
         return self.state

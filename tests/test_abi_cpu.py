@@ -471,3 +471,33 @@ def test_slot_gather_validation(lib):
         1, "NVFP4 slots without pairs need slot_scales")
     assert gather(perm_ptr=perm.ctypes.data + 4) == (1, "perm must be 8-byte aligned")
     assert gather(n_slots=0) == (0, "")
+
+
+def test_event_flags_are_checked(lib):
+    def call(args):
+        rc = lib.ns_dendritic_event(ctypes.byref(args), None)
+        return rc, lib.ns_last_error().decode()
+
+    args, keep = fake_event_args()
+    args.flags = 2
+    assert call(args) == (1, "unknown event flags 2")
+    args.flags = native.EVENT_ADVANCE_ONLY
+    args.pending_in, args.pending_out = keep[0][10].ctypes.data, keep[0][11].ctypes.data
+    assert call(args) == (1, "the advance-only tick takes no pending buffers")
+
+
+def test_accumulated_spmm_output_must_not_overlap_itself(lib):
+    n, batch = 8, 2
+    rowptr = np.zeros(n + 1, np.int32)
+    bounds = np.array([0, 0, n, 0], np.int32)
+    source = np.zeros((batch, n), np.float32)
+    out = np.zeros(1, np.float32)
+    args = native._SpmmArgs()
+    args.n_neurons, args.batch = n, batch
+    args.source = native._Plane(source.ctypes.data, n, 1, 0.0)
+    args.matrix = native._Csr(n, 0, rowptr.ctypes.data, None, None, native.WEIGHT_F32, None, None)
+    args.plan = native._RowPlan(bounds.ctypes.data, 1, lib.ns_block_edges(batch), 0)
+    args.out = native._OutPlane(out.ctypes.data, 0, 0)
+    args.accumulate = 1
+    rc = lib.ns_csr_spmm(ctypes.byref(args), None)
+    assert rc == 1 and "must not overlap itself" in lib.ns_last_error().decode()

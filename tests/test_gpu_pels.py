@@ -24,13 +24,19 @@ def state_error(native, oracle) -> float:
     return max(max_err(getattr(native, f), getattr(oracle, f)) for f in FIELDS)
 
 
-@pytest.mark.parametrize("one_launch", [True, False])
-def test_theta_zero_long_rollout_matches_matrix(gpu, one_launch):
+# one launch (scatter into pending buffers), two launches (advance, scatter),
+# or matrix propagation (advance only, then current += W @ delta)
+MODES = {"one_launch": dict(one_launch=True), "two_launch": dict(one_launch=False),
+         "matrix": dict(propagation="matrix")}
+
+
+@pytest.mark.parametrize("mode", list(MODES))
+def test_theta_zero_long_rollout_matches_matrix(gpu, mode):
     """Reference test_native_compartmental.py:99-110 (N=1024, B=2, 16000 edges, 500 ticks)."""
     case = make_case(1024, 16000, 83, gpu, kind="reference")
     state = torch.full((2, 1024), 0.2)
     native = NativeDendriticPELSRuntime(case.topology, case.model, state.to(gpu), theta=0,
-                                        one_launch=one_launch)
+                                        **MODES[mode])
     matrix = ort.MatrixOracle(case.graph, case.params, state)
     for t in range(500):
         value = 0.2 if t % 70 < 35 else 0.05
@@ -41,15 +47,15 @@ def test_theta_zero_long_rollout_matches_matrix(gpu, one_launch):
     assert max_err(native.persistent_current, current) <= 1e-5
 
 
-@pytest.mark.parametrize("one_launch", [True, False])
-def test_nonzero_theta_emission_and_weight_mutation(gpu, one_launch):
+@pytest.mark.parametrize("mode", list(MODES))
+def test_nonzero_theta_emission_and_weight_mutation(gpu, mode):
     """Reference test_native_compartmental.py:142-164 (theta .02, weights x0.7 at tick 25)."""
     from oracle import topology as otop
 
     case = make_case(97, 600, 83, gpu, kind="reference")
     state = torch.full((3, 97), 0.2)
     native = NativeDendriticPELSRuntime(case.topology, case.model, state.to(gpu), theta=0.02,
-                                        one_launch=one_launch)
+                                        **MODES[mode])
     oracle = ort.PelsOracle(case.graph, case.params, state, theta=0.02)
     for t in range(50):
         if t == 25:
@@ -69,7 +75,7 @@ def test_nonzero_theta_emission_and_weight_mutation(gpu, one_launch):
     assert native.last_backend == "reference-stats" and stats.active_edges >= 0
     native.step(0.3)
     oracle.step(0.3)
-    assert native.last_backend == "native"
+    assert native.last_backend == ("native-matrix" if mode == "matrix" else "native")
     assert state_error(native, oracle) <= 1e-3
 
 
@@ -89,13 +95,15 @@ def test_idle_updates_traces_and_retains_returned_state(gpu):
     assert not torch.equal(first_adaptation, native.adaptation_state)
 
 
+@pytest.mark.parametrize("propagation", ["event", "matrix"])
 @pytest.mark.parametrize("theta", [0.0, 0.02])
-def test_cfg4_event_path_warmup_then_withdrawn(gpu, theta):
+def test_cfg4_event_path_warmup_then_withdrawn(gpu, theta, propagation):
     """N=50000, M~1M, B=1: 512 ticks drive .2/.1, then 4096 ticks with inputs withdrawn."""
-    print(f"case cfg4 N=50000 M=1000000 theta={theta}", flush=True)
+    print(f"case cfg4 N=50000 M=1000000 theta={theta} propagation={propagation}", flush=True)
     case = make_case(50_000, 1_000_000, 0, gpu)
     native = NativeDendriticPELSRuntime(case.topology, case.model,
-                                        torch.zeros(1, 50_000, device=gpu), theta=theta)
+                                        torch.zeros(1, 50_000, device=gpu), theta=theta,
+                                        propagation=propagation)
     oracle = ort.PelsOracle(case.graph, case.params, torch.zeros(1, 50_000), theta=theta)
     bar = 1e-5 if theta == 0 else 1e-3
     worst = worst_current = 0.0
@@ -117,7 +125,7 @@ def test_cfg4_event_path_warmup_then_withdrawn(gpu, theta):
             else:
                 # theta = 0: every pair is active, so emitted tracks the state itself
                 assert max_err(native.emitted_state, native.state) <= 1e-6
-    print(f"cfg4 theta={theta}: state {worst:.3e} current {worst_current:.3e} "
+    print(f"cfg4 theta={theta} {propagation}: state {worst:.3e} current {worst_current:.3e} "
           f"emit-mask mismatches {mismatches}/{checked}")
     assert worst <= bar
     assert worst_current <= bar
@@ -230,3 +238,33 @@ def test_hub_sources_scatter_many_rounds(gpu, one_launch, theta):
     bar = 1e-5 if theta == 0 else 1e-3
     assert max_err(native.persistent_current, exact) <= 1e-5
     assert state_error(native, oracle) <= bar
+
+
+def test_matrix_propagation_rejects_unknown_modes(gpu):
+    case = make_case(97, 600, 83, gpu, kind="reference")
+    with pytest.raises(ValueError, match="'event' or 'matrix'"):
+        NativeDendriticPELSRuntime(case.topology, case.model, torch.zeros(1, 97, device=gpu),
+                                   theta=0.0, propagation="auto")
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_csr_spmm_accumulates_in_place(gpu, batch):
+    """ns_csr_spmm with accumulate: out += W @ S, any distinct-element strides."""
+    case = make_case(2000, 30_000, 7, gpu)
+    gen = torch.Generator().manual_seed(batch)
+    source = torch.rand(batch, 2000, generator=gen).to(gpu)
+    start = torch.rand(2000, batch, generator=gen).to(gpu).t()     # neuron-major view
+    out = start.clone().t().contiguous().t()
+    native = NativeDendriticPELSRuntime(case.topology, case.model,
+                                        torch.zeros(batch, 2000, device=gpu), theta=0.0)
+    t = case.topology
+    product = native.extension.csr_spmm(source, t.in_rowptr, t.in_col, t.in_weight)
+    returned = native.extension.csr_spmm(source, t.in_rowptr, t.in_col, t.in_weight,
+                                         accumulate_into=out)
+    assert returned is out
+    assert torch.equal(out, start + product)
+    expected = ort.propagate(ort.csr_matrix(case.graph), source.cpu()) + start.cpu()
+    assert max_err(out, expected) <= 1e-5
+    with pytest.raises(RuntimeError, match="must not overlap itself"):
+        native.extension.csr_spmm(source, t.in_rowptr, t.in_col, t.in_weight,
+                                  accumulate_into=torch.zeros(1, device=gpu).expand(batch, 2000))
