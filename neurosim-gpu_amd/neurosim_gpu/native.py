@@ -385,11 +385,14 @@ LANE_TARGET = 24   # at most this many edges per lane before a row gets more lan
 
 PANEL_PAIRS = 1   # NS_PANEL_PAIRS
 PANEL_COMBINE_LAUNCH = 2   # NS_PANEL_COMBINE_LAUNCH
-# Largest row range the tick kernel's last tile finishes by itself.  Measured
-# at N=166,000, M=25M, B=1 (five panels, 3255-row ranges): the last tile's
-# update of its range took 6.8 us on one compute unit against about 3 us for
-# the second kernel spread over the whole chip.
-ONE_LAUNCH_MAX_RANGE_ROWS = 1024
+# Largest row range the tick kernel's last tile finishes by itself when the
+# caller leaves the choice to the layout.  The last tile updates its whole
+# range on one compute unit, and in every measurement so far the combine
+# kernel, spread over the chip, was faster: N=166,000, M=25M, B=1 (3255-row
+# ranges) 35.6 against 33.3 us per tick; N=50,000, M=1M (390-row ranges) 9.5
+# against 8.8 us at B=1 and 12.1 against 10.4 at B=2.  So one launch is taken
+# only on request (combine_launch=False).
+ONE_LAUNCH_MAX_RANGE_ROWS = 0
 
 
 def plan_panels_host(rowptr: torch.Tensor, col: torch.Tensor, batch: int, tiles_per_panel: int,
@@ -514,7 +517,8 @@ class PanelLayout(_SlotLayout):
     (one launch per tick) or by a second kernel (``combine_launch``); the
     results are bitwise the same.  The last tile updates the whole range on
     one compute unit, so the default (``combine_launch=None``) takes one launch
-    only for ranges of at most ``ONE_LAUNCH_MAX_RANGE_ROWS`` rows.
+    only for ranges of at most ``ONE_LAUNCH_MAX_RANGE_ROWS`` rows (none, as
+    measured so far).
     """
 
     def __init__(self, topology, batch: int, device, *, tiles_per_panel: int | None = None,

@@ -27,7 +27,7 @@ import torch
 
 from .compartmental import DendriticDynamics, DendriticMatrixRuntime, DendriticPELSRuntime
 from .native import (BAND_WIDTH, BandLayout, NativeExtension, PanelLayout, encode_weights,
-                     load_native_extension, new_planes)
+                     load_native_extension, new_planes, panel_geometry)
 from .topology import SparseTopology
 
 
@@ -172,6 +172,25 @@ class _NativeTick(torch.autograd.Function):
                 d_adaptation if needs[3] else None, d_weight, d_drive, d_dendritic, *d_params)
 
 
+# "auto" takes column panels (batch 1-2) when the graph has at least
+# PANEL_AUTO_MIN_SEGMENT edges per (row, panel) on average and at least
+# PANEL_AUTO_MIN_EDGES edges; sparser or smaller graphs run faster on row
+# blocks.  Measured (us per tick, rows / panels): N=50k M=1M B=1 8.2 / 8.8;
+# N=166k M=2M B=1 15.0 / 13.0, B=2 20.5 / 22.5; N=400k M=4M B=1 26.8 / 28.6,
+# B=2 39.8 / 76.4; N=400k M=16M B=2 121.8 / 82.1; N=166k M=25M B=1 117 / 33.
+PANEL_AUTO_MIN_SEGMENT = 2.0
+PANEL_AUTO_MIN_EDGES = 2_000_000
+
+
+def panels_pay_off(topology, batch: int) -> bool:
+    """Whether column panels beat row blocks for this graph and batch (see above)."""
+    width, _ = panel_geometry(batch)
+    n = max(topology.n_neurons, 1)
+    panels = -(-n // (width & ~3))
+    return (topology.n_edges >= PANEL_AUTO_MIN_EDGES
+            and topology.n_edges >= PANEL_AUTO_MIN_SEGMENT * panels * n)
+
+
 # Fewest source bands (of BAND_WIDTH neurons) for which "auto" picks the band
 # kernel: below that the whole 16-column state is a few L2s and the row kernel
 # gathers it from cache as well.
@@ -193,9 +212,10 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
     built once, at construction), "bands" streams a band-sorted copy of the
     graph whose gathers stay within an L2-sized band of sources at a time
     (batch a multiple of 16; built once), "rows" streams the CSR as is and
-    gathers the state from cache.  "auto" uses panels whenever the batch
-    allows, bands when the batch is a multiple of 16 and the graph spans at
-    least ``BAND_AUTO_MIN_BANDS`` bands, rows otherwise.  ``panel_width`` caps
+    gathers the state from cache.  "auto" uses panels when the batch allows
+    and the graph is dense enough for them (``panels_pay_off``), bands when
+    the batch is a multiple of 16 and the graph spans at least
+    ``BAND_AUTO_MIN_BANDS`` bands, rows otherwise.  ``panel_width`` caps
     the neurons per panel (default: what LDS holds) and ``panel_tiles`` sets
     the workgroups per panel (default: compute units / panels).
     ``panel_pairs`` builds the pair layout (``NS_PANEL_PAIRS``: every row at least
@@ -240,7 +260,8 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         if kernel == "bands" and (batch % 16 or batch == 0 or not native):
             raise ValueError("the band kernel needs a batch that is a multiple of 16 and the "
                              "native extension")
-        use_panels = kernel == "panels" or (kernel == "auto" and batch in (1, 2) and native)
+        use_panels = kernel == "panels" or (kernel == "auto" and batch in (1, 2) and native
+                                            and panels_pay_off(topology, batch))
         use_bands = kernel == "bands" or (
             kernel == "auto" and native and batch > 0 and batch % 16 == 0
             and topology.n_neurons >= BAND_AUTO_MIN_BANDS * BAND_WIDTH)

@@ -206,8 +206,10 @@ def test_recorded_ticks_move_to_panels_for_a_reused_weight_version(gpu):
     topo.in_weight.requires_grad_(True)
     soma = Dynamics(torch.full((4000,), .72, device=gpu), torch.full((4000,), .8, device=gpu))
     mdl = DendriticDynamics.from_time_constants(soma, dt=1., tau_dendrite=4., tau_adaptation=25.)
-    plain = NativeDendriticMatrixRuntime(topo, mdl, torch.zeros(1, 4000, device=gpu))
-    recorded = NativeDendriticMatrixRuntime(topo, mdl, torch.zeros(1, 4000, device=gpu))
+    plain = NativeDendriticMatrixRuntime(topo, mdl, torch.zeros(1, 4000, device=gpu),
+                                         kernel="panels")
+    recorded = NativeDendriticMatrixRuntime(topo, mdl, torch.zeros(1, 4000, device=gpu),
+                                            kernel="panels")
     assert recorded.kernel == "panels"
     for tick in range(5):
         with torch.no_grad():

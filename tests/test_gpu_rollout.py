@@ -98,11 +98,12 @@ def test_rollout_keeps_its_weights_after_the_runtime_moves_on(gpu, batch):
     topology_cpu = random_topology(n, 10 * n, device="cpu", seed=9)
     model, _ = standard_model(n)
     model = model_to(model, gpu)
+    kernel = "panels" if batch == 1 else "bands"
     runtime = NativeDendriticMatrixRuntime(topology_to(topology_cpu, gpu), model,
-                                           torch.zeros(batch, n, device=gpu))
-    assert runtime.kernel == ("panels" if batch == 1 else "bands")
+                                           torch.zeros(batch, n, device=gpu), kernel=kernel)
+    assert runtime.kernel == kernel
     witness = NativeDendriticMatrixRuntime(topology_to(topology_cpu, gpu), model,
-                                           torch.zeros(batch, n, device=gpu))
+                                           torch.zeros(batch, n, device=gpu), kernel=kernel)
     rollout = MatrixRollout(runtime, 8, drive=0.2, dendritic_drive=0.1)
     if batch == 1:
         runtime.state = torch.full((1, n), 0.3, device=gpu, requires_grad=True)
