@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 10
+#define NS_ABI_VERSION 11
 
 /* Return codes. */
 #define NS_OK 0
@@ -167,11 +167,14 @@ typedef struct ns_panel_plan {
  * bands in order and finally applies the update.  Each of its 4 wavefronts
  * owns a fixed set of the block's rows (dealt by degree, longest first onto
  * the least-loaded wavefront).  Per band, a wavefront's rows with edges in
- * the band are sorted by segment length and cut into groups of 64 rows, one
- * row per lane; a group's slots are step-major (slot (step k, lane l) is
- * 64*first_step + 64*k + l) and lane l takes its row's segment in CSR order.
- * A group is cut into register blocks of at most `block_steps` steps; the
- * wavefront's blocks are consecutive in `blocks` and their slots contiguous.
+ * the band are packed into groups of 64 lanes: a group's first rows are the
+ * 64 longest segments left (longest first), and the group lasts as many steps
+ * as its longest.  A lane takes its first row's segment in CSR order and, in
+ * the steps after it, possibly a second row's segment (the longest left that
+ * fits, lanes with the most spare steps choosing first).  A group's slots are
+ * step-major (slot (step k, lane l) is 64*first_step + 64*k + l).  A group is
+ * cut into register blocks of at most `block_steps` steps; the wavefront's
+ * blocks are consecutive in `blocks` and their slots contiguous.
  * Padding slots have source index 0xFFFF and weight code 0.  Slot k is
  * original CSR edge perm[k] (or padding).  The kernel reads one block record
  * and one register block of slots ahead, so the tables end with a sentinel
@@ -189,9 +192,13 @@ typedef struct ns_band_plan {
   int64_t n_slots;
   const int32_t* wave_blocks;  /* [n_row_blocks*4 + 1]: wavefront w of row block q owns
                                   blocks wave_blocks[4q+w] .. wave_blocks[4q+w+1]-1 */
-  const int32_t* blocks;       /* [n_blocks+1][4]: first step, band, steps | last << 8
-                                  (last: the block ends its group), group */
-  const uint16_t* rows;        /* [n_groups][64]: block-local row of each lane, 0xFFFF none */
+  const int32_t* blocks;       /* [n_blocks+1][4]: first step, band,
+                                  steps | last << 8 | step in group << 9 (last: the block
+                                  ends its group), group */
+  const uint32_t* rows;        /* [n_groups][64] lane words: block-local first row (bits
+                                  0-11) and second row (bits 12-23), 0xFFF none, and the
+                                  step in the group where the second row starts (bits
+                                  24-31; 0 without a second row) */
   const uint16_t* col;         /* [n_slots] source index minus the band's first neuron */
   const void* weight;          /* [n_slots] weights in slot order, encoding of the matrix */
   const uint8_t* slot_scales;  /* NVFP4: e4m3 block-scale code of each slot's edge */
@@ -422,13 +429,13 @@ int ns_dendritic_step(const ns_step_args* args, void* stream);
  * steps (1..8).  Call once with all output pointers NULL to get the sizes in
  * *plan (n_bands, n_row_blocks, n_blocks, n_groups, n_slots), then again with
  * wave_blocks int32[4*n_row_blocks+1], blocks int32[4*(n_blocks+1)], rows
- * uint16[64*n_groups], perm int32[n_slots] (-1 for padding), col
+ * uint32[64*n_groups], perm int32[n_slots] (-1 for padding), col
  * uint16[n_slots].  Pointer fields of *plan are not touched.  blocks holds
  * n_blocks records plus the sentinel, rows n_groups groups including the
  * sentinel group, and the slots end with 8*64 padding slots. */
 int ns_plan_bands(const int32_t* rowptr_host, const int32_t* col_host, int64_t n_rows,
                   int32_t band_width, int32_t block_rows, int32_t block_steps,
-                  ns_band_plan* plan, int32_t* wave_blocks, int32_t* blocks, uint16_t* rows,
+                  ns_band_plan* plan, int32_t* wave_blocks, int32_t* blocks, uint32_t* rows,
                   int32_t* perm, uint16_t* col);
 
 /* Largest block_rows the band kernel's LDS holds. */

@@ -15,11 +15,13 @@
 //    tile.  Its row sums live in LDS for the whole tick, so no partial sums
 //    leave the compute unit.  Each wavefront owns a fixed set of the block's
 //    rows, so its LDS updates race with no other wavefront.
-//  * Per band a wavefront's rows are grouped 64 at a time, one row per lane,
-//    longest segment first; lane l walks its row's segment, gathering the
-//    whole 64-byte source row with four 16-byte loads per edge and keeping
-//    16 running sums in registers.  At the group's end the lane adds them to
-//    its row's LDS sums.
+//  * Per band a wavefront's rows are packed 64 lanes at a time, longest
+//    segments first; lane l walks its row's segment, gathering the whole
+//    64-byte source row with four 16-byte loads per edge and keeping 16
+//    running sums in registers.  A lane whose row ends early may take a
+//    second, shorter row in the group's remaining steps: at the switch step it
+//    adds its sums to the first row's LDS sums and starts again from zero.
+//    At the group's end the lane adds them to its (last) row's LDS sums.
 //  * Register blocks of up to D steps are software-pipelined: the slots of
 //    block b+1 are loaded while block b's gathers are in flight.
 //  * After the last band the workgroup applies the update to its rows.
@@ -46,7 +48,7 @@ struct BandArgs {
   int32_t band_width, block_rows;
   const int32_t* wave_blocks;
   const int32_t* blocks;
-  const uint16_t* rows;
+  const uint32_t* rows;   // lane words: first row, second row, switch step
   const uint16_t* col;
   const void* weight;
   const uint8_t* slot_scales;
@@ -64,17 +66,17 @@ struct BandSlot {
 };
 
 struct BandBlock {
-  int32_t step0, band, steps, last, group;
+  int32_t step0, band, steps, last, t0, group;   // t0: the block's first step in its group
 };
 
 __device__ __forceinline__ BandBlock load_band_block(const BandArgs& A, int32_t b) {
   const int32_t* q = A.blocks + 4 * static_cast<int64_t>(b);
   const int32_t info = q[2];
-  return BandBlock{q[0], q[1], info & 0xFF, info >> 8, q[3]};
+  return BandBlock{q[0], q[1], info & 0xFF, (info >> 8) & 1, info >> 9, q[3]};
 }
 
-// This lane's D slots from the block's first step, and its row in the block's
-// group.  The loads do not depend on the block's step count (the slot array
+// This lane's D slots from the block's first step, and its lane word in the
+// block's group.  The loads do not depend on the block's step count (the slot array
 // has D padding steps past its end, the block table a sentinel record), so
 // the compiler can count them and wait for exactly the ones it needs.
 template <int FMT, int D>
@@ -95,6 +97,17 @@ __device__ __forceinline__ void load_band_slots(const BandArgs& A, const BandBlo
     }
   }
   row = A.rows[int64_t{64} * blk.group + lane];
+}
+
+// Adds a lane's 16 running sums to its row's LDS sums.
+__device__ __forceinline__ void add_to_row(v4f* sums4, uint32_t row, const float (&acc)[16]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    v4f t = sums4[row * 4 + q];
+    t.x += acc[4 * q + 0]; t.y += acc[4 * q + 1];
+    t.z += acc[4 * q + 2]; t.w += acc[4 * q + 3];
+    sums4[row * 4 + q] = t;
+  }
 }
 
 // Source of padding slots and of steps past a block's end: 16 zeros.
@@ -141,7 +154,7 @@ __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) 
 
   BandBlock cur{0, 0, 0, 0, 0};
   BandSlot here[D];
-  uint32_t row = kBandPad;
+  uint32_t row = kBandNoRow | (kBandNoRow << kBandRowBits);
   if (b_begin < b_end) {
     cur = load_band_block(A, b_begin);
     load_band_slots<FMT, D>(A, cur, lane, here, row);
@@ -170,6 +183,9 @@ __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) 
     BandSlot ahead[D];
     uint32_t row_ahead;
     load_band_slots<FMT, D>(A, nxt, lane, ahead, row_ahead);
+    // A lane with a second row switches after block step `turn` (none: out of range).
+    const uint32_t first_row = row & kBandNoRow;
+    const int turn = static_cast<int>(row >> 24) - cur.t0 - 1;
 #pragma unroll
     for (int k = 0; k < D; ++k) {
       if (k < cur.steps) {
@@ -181,18 +197,17 @@ __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) 
           acc[4 * q + 2] += w * g[k][q].z;
           acc[4 * q + 3] += w * g[k][q].w;
         }
+        if (k == turn) {
+          add_to_row(sums4, first_row, acc);
+#pragma unroll
+          for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+        }
       }
     }
     if (cur.last) {
-      if (row != kBandPad) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          v4f t = sums4[row * 4 + q];
-          t.x += acc[4 * q + 0]; t.y += acc[4 * q + 1];
-          t.z += acc[4 * q + 2]; t.w += acc[4 * q + 3];
-          sums4[row * 4 + q] = t;
-        }
-      }
+      const uint32_t second_row = (row >> kBandRowBits) & kBandNoRow;
+      const uint32_t last_row = second_row != kBandNoRow ? second_row : first_row;
+      if (last_row != kBandNoRow) add_to_row(sums4, last_row, acc);
 #pragma unroll
       for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
     }
@@ -273,7 +288,8 @@ int band_step(const ns_step_args& a, const ns_band_plan& pl, hipStream_t stream)
   if (a.matrix.format == NS_WEIGHT_NVFP4 && !pl.slot_scales)
     return fail("NVFP4 bands require per-slot block scales");
   const uintptr_t need = a.matrix.format == NS_WEIGHT_F32 ? 4 : a.matrix.format == NS_WEIGHT_F16 ? 2 : 1;
-  if (reinterpret_cast<uintptr_t>(pl.col) % 2 || reinterpret_cast<uintptr_t>(pl.weight) % need)
+  if (reinterpret_cast<uintptr_t>(pl.col) % 2 || reinterpret_cast<uintptr_t>(pl.weight) % need ||
+      reinterpret_cast<uintptr_t>(pl.rows) % 4)
     return fail("band arrays are misaligned");
   if (static_cast<int64_t>(pl.n_row_blocks) > 0x7FFFFFFF || a.batch / 16 > 65535)
     return fail("band grid too large");

@@ -19,5 +19,11 @@ constexpr int kPanelTailSlots = 2 * kPanelMaxPrefetch * 64;
 constexpr int kBandWaves = 4;                           // wavefronts per band workgroup
 constexpr int kBandMaxBlockRows = 2496;                 // 16 float row sums each in LDS (156 KB)
 constexpr int kBandMaxBlockSteps = 8;                   // steps per register block, at most
+// A band lane word: first row (bits 0-11), second row (bits 12-23) and the
+// step at which the lane moves on to its second row (bits 24-31).
+constexpr unsigned kBandNoRow = 0xFFF;
+constexpr int kBandRowBits = 12;
+constexpr int kBandMaxSwitch = 255;
+static_assert(kBandMaxBlockRows <= static_cast<int>(kBandNoRow), "block rows fit a lane word");
 
 }  // namespace ns

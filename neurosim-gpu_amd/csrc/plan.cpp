@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <atomic>
 #include <functional>
+#include <map>
 #include <system_error>
 #include <thread>
 #include <cstdio>
@@ -462,13 +463,16 @@ namespace {
 struct BandLayout {
   int64_t n_groups = 0, n_slots = 0;
   std::vector<int32_t> wave_blocks, blocks, perm;
-  std::vector<uint16_t> rows, col;
+  std::vector<uint32_t> rows;
+  std::vector<uint16_t> col;
 };
 
 
 // Lays out row block [r0, r1): rows dealt to the wavefronts by degree, then
-// per wavefront and band the rows with edges in the band, longest segment
-// first (ties by row), in groups of 64 rows cut into register blocks.
+// per wavefront and band the rows with edges in the band in groups of 64
+// lanes, cut into register blocks.  A lane takes one row's segment (the
+// group's 64 longest left, longest first) and, in the steps after it, a
+// second, shorter row's segment where one fits.
 void append_band_block(BandLayout& out, const int32_t* rowptr, const int32_t* col,
                        int64_t r0, int64_t r1, int32_t band_width, int32_t n_bands,
                        int32_t block_steps, bool fill) {
@@ -514,37 +518,71 @@ void append_band_block(BandLayout& out, const int32_t* rowptr, const int32_t* co
           order[row_base[i] + at[col[e] / band_width]++] = static_cast<int32_t>(e);
       }
     }
-    std::vector<int32_t> cand;
+    // Rows with edges in the band, by segment length (within a length, in row
+    // order): a cursor into each length's list, the length dropped once empty.
+    std::map<int32_t, std::pair<size_t, std::vector<int32_t>>> by_len;
+    auto take = [&](std::map<int32_t, std::pair<size_t, std::vector<int32_t>>>::iterator it) {
+      const int32_t i = it->second.second[it->second.first++];
+      if (it->second.first == it->second.second.size()) by_len.erase(it);
+      return i;
+    };
     for (int32_t k = 0; k < n_bands; ++k) {
       auto seg_len = [&](int32_t i) -> int32_t {
         const int32_t* st = start.data() + static_cast<int64_t>(i) * (n_bands + 1);
         return st[k + 1] - st[k];
       };
-      cand.clear();
+      auto edge_at = [&](int32_t i, int32_t t) -> int32_t {
+        return order[row_base[i] + start[static_cast<int64_t>(i) * (n_bands + 1) + k] + t];
+      };
+      by_len.clear();
       for (int64_t i = 0; i < nw; ++i)
-        if (seg_len(static_cast<int32_t>(i)) > 0) cand.push_back(static_cast<int32_t>(i));
-      std::stable_sort(cand.begin(), cand.end(),
-                       [&](int32_t x, int32_t y) { return seg_len(x) > seg_len(y); });
-      for (size_t g0 = 0; g0 < cand.size(); g0 += 64) {
-        const size_t gn = std::min<size_t>(64, cand.size() - g0);
-        const int32_t steps = seg_len(cand[g0]);
+        if (seg_len(static_cast<int32_t>(i)) > 0)
+          by_len[seg_len(static_cast<int32_t>(i))].second.push_back(static_cast<int32_t>(i));
+      while (!by_len.empty()) {
+        // A group's first rows: the 64 longest segments left, longest first;
+        // the group lasts as many steps as the first of them.
+        int32_t first[64], second[64];
+        int gn = 0;
+        while (gn < 64 && !by_len.empty()) first[gn++] = take(std::prev(by_len.end()));
+        const int32_t steps = seg_len(first[0]);
+        // Second rows: a lane's steps after its first row's segment take the
+        // longest segment left that fits them, lanes with the most such steps
+        // first.  The lane's word holds the switch step in 8 bits.
+        for (int l = 0; l < 64; ++l) second[l] = -1;
+        for (int l = gn - 1; l >= 0 && !by_len.empty(); --l) {
+          const int32_t len = seg_len(first[l]);
+          if (len > kBandMaxSwitch) break;
+          auto it = by_len.upper_bound(steps - len);
+          if (it == by_len.begin()) break;   // no lane after this one has more room
+          second[l] = take(std::prev(it));
+        }
         const int32_t group = static_cast<int32_t>(out.n_groups++);
         if (fill)
-          for (size_t l = 0; l < 64; ++l)
-            out.rows.push_back(l < gn ? static_cast<uint16_t>(rows_w[cand[g0 + l]]) : uint16_t{0xFFFF});
+          for (int l = 0; l < 64; ++l) {
+            uint32_t word = kBandNoRow | (kBandNoRow << kBandRowBits);
+            if (l < gn) {
+              word = static_cast<uint32_t>(rows_w[first[l]]);
+              word |= second[l] < 0 ? kBandNoRow << kBandRowBits
+                                    : (static_cast<uint32_t>(rows_w[second[l]]) << kBandRowBits) |
+                                          (static_cast<uint32_t>(seg_len(first[l])) << 24);
+            }
+            out.rows.push_back(word);
+          }
         for (int32_t t0 = 0; t0 < steps; t0 += block_steps) {
           const int32_t nst = std::min(block_steps, steps - t0);
           const int32_t last = t0 + block_steps >= steps ? 1 : 0;
-          const int32_t rec[4] = {static_cast<int32_t>(out.n_slots / 64), k, nst | (last << 8), group};
+          const int32_t rec[4] = {static_cast<int32_t>(out.n_slots / 64), k,
+                                  nst | (last << 8) | (t0 << 9), group};
           out.blocks.insert(out.blocks.end(), rec, rec + 4);
           out.n_slots += int64_t{64} * nst;
           if (!fill) continue;
           for (int32_t t = t0; t < t0 + nst; ++t)
-            for (size_t l = 0; l < 64; ++l) {
+            for (int l = 0; l < 64; ++l) {
               int32_t edge = -1;
               if (l < gn) {
-                const int32_t i = cand[g0 + l];
-                if (t < seg_len(i)) edge = order[row_base[i] + start[static_cast<int64_t>(i) * (n_bands + 1) + k] + t];
+                const int32_t la = seg_len(first[l]);
+                if (t < la) edge = edge_at(first[l], t);
+                else if (second[l] >= 0 && t - la < seg_len(second[l])) edge = edge_at(second[l], t - la);
               }
               out.perm.push_back(edge);
               out.col.push_back(edge < 0 ? uint16_t{0xFFFF}
@@ -563,7 +601,7 @@ extern "C" int32_t ns_band_max_block_rows(void) { return kBandMaxBlockRows; }
 extern "C" int ns_plan_bands(const int32_t* rowptr, const int32_t* col, int64_t n_rows,
                              int32_t band_width, int32_t block_rows, int32_t block_steps,
                              ns_band_plan* plan, int32_t* wave_blocks, int32_t* blocks,
-                             uint16_t* rows, int32_t* perm, uint16_t* col_out) {
+                             uint32_t* rows, int32_t* perm, uint16_t* col_out) {
   clear_error();
   if (!rowptr || !plan) return fail("rowptr and plan are required");
   if (n_rows <= 0 || n_rows >= (int64_t{1} << 31)) return fail("N must be in [1, 2^31)");
@@ -633,7 +671,7 @@ extern "C" int ns_plan_bands(const int32_t* rowptr, const int32_t* col, int64_t 
     *wb = n_blocks;
     const int32_t sentinel[4] = {0, 0, 0, sentinel_group};
     std::copy(sentinel, sentinel + 4, blocks + 4 * block0);
-    std::fill(rows + 64 * group0, rows + 64 * (group0 + 1), uint16_t{0xFFFF});
+    std::fill(rows + 64 * group0, rows + 64 * (group0 + 1), kBandNoRow | (kBandNoRow << kBandRowBits));
     std::fill(perm + slot0, perm + slot0 + kBandMaxBlockSteps * 64, -1);
     std::fill(col_out + slot0, col_out + slot0 + kBandMaxBlockSteps * 64, uint16_t{0xFFFF});
   }

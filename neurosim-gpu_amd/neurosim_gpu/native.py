@@ -35,7 +35,7 @@ import numpy as np
 import torch
 
 _LIB_NAME = "libneurosim_hip.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 WEIGHT_F32, WEIGHT_F16, WEIGHT_E4M3, WEIGHT_NVFP4 = 0, 1, 2, 3
 _PLAN_CACHE = 64   # row plans kept per extension (one per live topology and batch width)
@@ -439,7 +439,7 @@ def plan_bands_host(rowptr: torch.Tensor, col: torch.Tensor, band_width: int, bl
     _raise_on(lib.ns_plan_bands(*args, *([None] * 5)), lib)
     wave_blocks = np.empty(4 * plan.n_row_blocks + 1, np.int32)
     blocks = np.empty(4 * (plan.n_blocks + 1), np.int32)
-    rows = np.empty(64 * plan.n_groups, np.uint16)
+    rows = np.empty(64 * plan.n_groups, np.uint32)
     perm = np.empty(plan.n_slots, np.int32)
     cols = np.empty(plan.n_slots, np.uint16)
     _raise_on(lib.ns_plan_bands(*args, wave_blocks.ctypes.data, blocks.ctypes.data,
@@ -454,6 +454,8 @@ def band_max_block_rows() -> int:
 def _device_tensor(array: np.ndarray, device) -> torch.Tensor:
     if array.dtype == np.uint16:
         array = array.view(np.int16)
+    elif array.dtype == np.uint32:
+        array = array.view(np.int32)
     return torch.from_numpy(np.ascontiguousarray(array)).to(device)
 
 

@@ -88,7 +88,8 @@ PanelOut plan_panels(const Csr& g, int32_t width, int32_t tiles, int32_t flags) 
 struct BandOut {
   ns_band_plan plan{};
   std::vector<int32_t> wave_blocks, blocks, perm;
-  std::vector<uint16_t> rows, col;
+  std::vector<uint32_t> rows;
+  std::vector<uint16_t> col;
   bool operator==(const BandOut& o) const {
     return plan.n_slots == o.plan.n_slots && wave_blocks == o.wave_blocks &&
            blocks == o.blocks && perm == o.perm && rows == o.rows && col == o.col;

@@ -3,8 +3,10 @@ emulation of the band kernel's decomposition against the plain CSR product.
 
 The invariants: every edge lands in exactly one slot, with its band-local
 source index; a wavefront's register blocks walk the bands in order, their
-slots contiguous; a group's lane keeps one row, takes the row's segment of the
-band in CSR order, and the group's last block is marked; each row of a block
+slots contiguous, each record carrying its first step within the group; a
+group's lane takes its first row's segment of the band in CSR order and, from
+its switch step on, possibly a second row's; the group lasts as long as its
+longest first segment, and its last block is marked; each row of a block
 belongs to one wavefront and meets each band at most once; the tables end with
 the sentinel block, the sentinel group and the tail padding.  The emulation
 follows the kernel's summation order (per row: bands in order, within a band
@@ -23,7 +25,14 @@ from neurosim_gpu import native
 from neurosim_gpu.native import band_max_block_rows, plan_bands_host
 
 PAD = 0xFFFF
+NO_ROW = 0xFFF
 TAIL = 8 * 64
+
+
+def lane_rows(word):
+    """(first row, second row, switch step) of a lane word."""
+    word = int(word)
+    return word & NO_ROW, (word >> 12) & NO_ROW, word >> 24
 
 
 def random_csr(n, m, seed, hubs=()):
@@ -77,7 +86,7 @@ def test_band_layout_invariants(n, m, seed, hubs, width, rows, steps):
 
     # sentinel block, sentinel group, tail padding
     assert tuple(blocks[-1]) == (0, 0, 0, plan.n_groups - 1)
-    assert np.all(group_rows[-1] == PAD)
+    assert np.all(group_rows[-1] == NO_ROW | NO_ROW << 12)
     assert np.all(perm[-TAIL:] == -1)
 
     row_of_edge = np.repeat(np.arange(n), np.diff(rowptr))
@@ -97,43 +106,55 @@ def test_band_layout_invariants(n, m, seed, hubs, width, rows, steps):
                 group, band = blocks[b, 3], blocks[b, 1]
                 assert band >= prev_band
                 prev_band = band
-                lanes = group_rows[group]
-                members = [int(r) for r in lanes if r != PAD]
+                lanes = [lane_rows(word) for word in group_rows[group]]
+                seg = lambda r: segments.get((r0 + r, int(band)), [])
+                members = []
+                for first, second, switch in lanes:
+                    if first == NO_ROW:
+                        assert (second, switch) == (NO_ROW, 0)
+                        continue
+                    members.append(first)
+                    if second == NO_ROW:
+                        assert switch == 0
+                    else:
+                        assert switch == len(seg(first)) and switch <= 255
+                        members.append(second)
                 assert len(set(members)) == len(members)
                 for r in members:
                     assert 0 <= r < min(rows, n - r0)
                     assert owner.setdefault(r0 + r, (q, w)) == (q, w)       # one wavefront per row
                     assert (r0 + r, band) not in seen_bands                 # one group per band
                     seen_bands[(r0 + r, band)] = True
+                    assert len(seg(r)) > 0
                 t = 0
                 while True:
                     start, bband, info, bgroup = blocks[b]
                     assert (bband, bgroup) == (band, group) and start == step
-                    count, last = info & 0xFF, info >> 8
-                    assert 1 <= count <= steps
+                    count, last, t0 = info & 0xFF, (info >> 8) & 1, info >> 9
+                    assert 1 <= count <= steps and t0 == t
                     for k in range(count):
                         slots = np.arange(64) + 64 * (start + k)
-                        for lane in range(64):
+                        for lane, (first, second, switch) in enumerate(lanes):
                             e = perm[slots[lane]]
-                            if lanes[lane] == PAD:
-                                assert e == -1
-                                continue
-                            row = r0 + int(lanes[lane])
-                            seg = segments.get((row, int(band)), [])
-                            if t + k < len(seg):
-                                assert e == seg[t + k]
+                            expected = -1
+                            if first != NO_ROW and t + k < len(seg(first)):
+                                expected = seg(first)[t + k]
+                            elif second != NO_ROW and 0 <= t + k - switch < len(seg(second)):
+                                expected = seg(second)[t + k - switch]
+                            assert e == expected
+                            if e >= 0:
                                 assert cols[slots[lane]] == col[e] - band * width
-                                assert row_of_edge[e] == row
-                            else:
-                                assert e == -1
                     step += count
                     t += count
                     b += 1
                     if last:
                         break
-                # the group's longest segment fills its blocks exactly
-                lengths = [len(segments.get((r0 + r, int(band)), [])) for r in members]
-                assert min(lengths) > 0 and t == max(lengths)
+                # the group lasts as long as its longest first segment (lane 0's);
+                # a second segment fits in the steps after its lane's first
+                assert t == len(seg(lanes[0][0]))
+                for first, second, switch in lanes:
+                    if first != NO_ROW:
+                        assert len(seg(first)) + (len(seg(second)) if second != NO_ROW else 0) <= t
     assert 64 * step + TAIL == plan.n_slots
 
 
@@ -153,6 +174,7 @@ def test_band_emulation_matches_csr_product(n, m, seed, hubs, width, rows, steps
             acc = np.zeros((64, 16), np.float32)
             for b in range(wave_blocks[4 * q + w], wave_blocks[4 * q + w + 1]):
                 start, band, info, group = blocks[b]
+                lanes = [lane_rows(word) for word in group_rows[group]]
                 for k in range(info & 0xFF):
                     slots = np.arange(64) + 64 * (start + k)
                     c = cols[slots].astype(np.int64)
@@ -160,10 +182,15 @@ def test_band_emulation_matches_csr_product(n, m, seed, hubs, width, rows, steps
                     g = np.zeros((64, 16), np.float32)
                     g[real] = s[band * width + c[real]]
                     acc += slot_w[slots][:, None] * g
-                if info >> 8:
-                    lanes = group_rows[group]
-                    for lane in np.nonzero(lanes != PAD)[0]:
-                        sums[r0 + lanes[lane]] += acc[lane]
+                    for lane, (first, second, switch) in enumerate(lanes):
+                        if (info >> 9) + k + 1 == switch:       # the lane moves to its second row
+                            sums[r0 + first] += acc[lane]
+                            acc[lane] = 0
+                if (info >> 8) & 1:
+                    for lane, (first, second, switch) in enumerate(lanes):
+                        row = second if second != NO_ROW else first
+                        if row != NO_ROW:
+                            sums[r0 + row] += acc[lane]
                     acc[:] = 0
     expected = np.zeros((n, 16), np.float64)
     np.add.at(expected, np.repeat(np.arange(n), np.diff(rowptr)),
@@ -209,3 +236,20 @@ def test_band_plan_does_not_depend_on_thread_count(monkeypatch):
         assert getattr(one[0], field) == getattr(many[0], field)
     for x, y in zip(one[1:], many[1:]):
         assert np.array_equal(x, y)
+
+
+def test_band_padding_at_scale_out_density():
+    """About 3.3 edges per (row, band), as at N=1M, M=100M with bands of 32,768
+    sources, and 977-row blocks: with a second row per lane where one fits the
+    layout holds at most 1.2 slots per edge (one row per lane: about 1.48)."""
+    rng = np.random.default_rng(5)
+    n, m = 100_000, 10_000_000
+    dst = np.sort(rng.integers(0, n, m))
+    rowptr = np.zeros(n + 1, np.int64)
+    rowptr[1:] = np.cumsum(np.bincount(dst, minlength=n))
+    col = rng.integers(0, n, m).astype(np.int32)
+    plan = plan_bands_host(torch.from_numpy(rowptr.astype(np.int32)), torch.from_numpy(col),
+                           3277, 977, 4)[0]
+    ratio = (plan.n_slots - TAIL) / m
+    print(f"slots per edge {ratio:.3f}")
+    assert ratio <= 1.2
