@@ -67,11 +67,15 @@ constexpr bool kPacedWaves = true;
 
 // Steps per register block: enough 64-lane loads in flight per wavefront to
 // cover HBM latency with 16 wavefronts per compute unit, within 128 VGPRs.
+// Measured at N=166k, M=25M, B=1 (µs per tick, graph replays): fp32 8/9/10/11/12
+// steps 33.7/33.3/32.4/33.9/35.1; fp16 8/10/12/14 25.1/25.0/26.4/27.4; e4m3
+// 8/10/12/16 22.0/22.1/22.7/23.7; NVFP4 pairs 10/12/13/16 23.0/22.6/23.2/23.7.
 template <int BT, int FMT>
 constexpr int block_steps() {
-  if constexpr (FMT == NS_WEIGHT_F32) return 8;
-  else if constexpr (FMT == NS_WEIGHT_F16) return BT == 1 ? 12 : 8;
-  else if constexpr (FMT == NS_WEIGHT_E4M3 || FMT == kNvfp4Pairs) return BT == 1 ? 16 : 12;
+  if constexpr (FMT == NS_WEIGHT_F32) return BT == 1 ? 10 : 8;
+  else if constexpr (FMT == NS_WEIGHT_F16) return BT == 1 ? 10 : 8;
+  else if constexpr (FMT == NS_WEIGHT_E4M3) return BT == 1 ? 10 : 12;
+  else if constexpr (FMT == kNvfp4Pairs) return 12;
   else return BT == 1 ? 12 : 8;
 }
 
