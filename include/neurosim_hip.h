@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 11
+#define NS_ABI_VERSION 12
 
 /* Return codes. */
 #define NS_OK 0
@@ -317,6 +317,17 @@ typedef struct ns_step_grad_args {
                                   out_weight[e] == matrix.weight[out_weight_index[e]];
                                   when set, the transposed product streams it instead of
                                   gathering through out_weight_index (NULL: gather) */
+  const ns_panel_plan* transposed_panels;  /* optional, batch 1 or 2: a panel plan (built
+                                  by ns_plan_panels with batch B) of the transposed
+                                  matrix, whose rows are the sources (out_rowptr, dst) and
+                                  whose slot weights are matrix.weight in its slot order
+                                  (slot k: matrix.weight[out_weight_index[e]] for the
+                                  source-major edge e the plan's perm names).  When set,
+                                  the transposed product runs the panel kernel's stream
+                                  and per-panel sums (then a second kernel adds them into
+                                  d_state) instead of the out-edge walk; out_weight is
+                                  then unused.  Its partials workspace must not overlap
+                                  the gradient planes or the workspace. */
 } ns_step_grad_args;
 
 /* Arguments of one weight encoding (fp8 e4m3 or NVFP4 CSR payload). */

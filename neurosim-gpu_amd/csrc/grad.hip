@@ -173,6 +173,10 @@ __global__ __launch_bounds__(kGradThreads) void weight_gradient_kernel(
 }  // namespace
 }  // namespace ns
 
+namespace ns {
+int panel_step(const ns_step_args& a, hipStream_t stream, int product, bool launch);
+}  // namespace ns
+
 using namespace ns;
 
 extern "C" int64_t ns_step_backward_workspace_floats(int64_t n_neurons, int64_t batch) {
@@ -197,6 +201,7 @@ extern "C" int ns_dendritic_step_backward(const ns_step_grad_args* args, void* s
   if (!a.out_rowptr || !a.dst || !a.out_weight_index)
     return fail("the source-major view (out_rowptr, dst, out_weight_index) is required");
   if (!a.workspace) return fail("a workspace of 2*B*N floats is required");
+  if (a.transposed_panels && batch > 2) return fail("transposed panels need batch 1 or 2");
   const Extent outs[5] = {extent(a.d_state, batch, n), extent(a.d_dendrite, batch, n),
                           extent(a.d_adaptation, batch, n), extent(a.d_drive, batch, n),
                           extent(a.d_dendritic_drive, batch, n)};
@@ -241,13 +246,38 @@ extern "C" int ns_dendritic_step_backward(const ns_step_grad_args* args, void* s
   G.gu = out_plane(a.d_drive); G.gv = out_plane(a.d_dendritic_drive);
   G.gj = gj;
   for (int i = 0; i < 6; ++i) G.gp[i] = a.d_params[i];
+  // The transposed product on panels: W^T @ gj added into d_state.
+  ns_step_args transposed{};
+  if (a.transposed_panels && a.matrix.n_edges > 0) {
+    transposed.n_neurons = n; transposed.batch = batch;
+    transposed.state = ns_plane{gj, 1, batch, 0.0f};
+    transposed.matrix.n_rows = n; transposed.matrix.n_edges = a.matrix.n_edges;
+    transposed.matrix.format = NS_WEIGHT_F32;
+    transposed.panels = a.transposed_panels;
+    transposed.out_state = a.d_state;
+    if (int rc = panel_step(transposed, s, 2, false)) return rc;
+    const ns_panel_plan& tp = *a.transposed_panels;
+    const Extent part = extent_of(tp.partials, 1, 1, 1, 2 * int64_t{tp.n_panels} * n * batch);
+    if (overlaps(part, work)) return fail("the transposed panels' partials overlap the workspace");
+    for (int o = 0; o < 5; ++o)
+      if (overlaps(part, outs[o]))
+        return fail("the transposed panels' partials overlap a gradient plane");
+  }
   const unsigned per_neuron = static_cast<unsigned>((n + kGradThreads - 1) / kGradThreads);
   const unsigned per_row = static_cast<unsigned>((n + kGradThreads / 64 - 1) / (kGradThreads / 64));
   advance_backward_kernel<<<per_neuron, kGradThreads, 0, s>>>(G);
   if (a.matrix.n_edges > 0) {
-    transposed_product_kernel<<<per_row, kGradThreads, 0, s>>>(
-        a.out_rowptr, a.dst, a.out_weight_index, static_cast<const float*>(a.matrix.weight),
-        a.out_weight, gj, n, batch, out_plane(a.d_state));
+    if (a.transposed_panels) {
+      // d_state += W^T @ gj on the transposed matrix's panel layout (checked
+      // before the first launch).
+      if (const hipError_t e = hipGetLastError(); e != hipSuccess)
+        return fail_launch("tick backward", e);
+      if (int rc = panel_step(transposed, s, 2, true)) return rc;
+    } else {
+      transposed_product_kernel<<<per_row, kGradThreads, 0, s>>>(
+          a.out_rowptr, a.dst, a.out_weight_index, static_cast<const float*>(a.matrix.weight),
+          a.out_weight, gj, n, batch, out_plane(a.d_state));
+    }
     if (a.d_weight)
       weight_gradient_kernel<<<per_row, kGradThreads, 0, s>>>(
           a.matrix.rowptr, a.matrix.col, gj, plane(a.state, a.state.data), n, batch, a.d_weight);

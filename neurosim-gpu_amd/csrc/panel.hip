@@ -100,7 +100,14 @@ struct PanelArgs {
   OutPlane os, od, oa;
   OutPlane oj;       // optional: j as well (data null: not written)
   int32_t s_vec;   // s.sn == 1 (B == 1) or neuron-major B == 2, 16-byte aligned
+  int32_t product;  // 0: the tick; 1: W @ s stored into os; 2: W @ s added to os
 };
+
+// The product modes' store of one row's sum.
+__device__ __forceinline__ void store_product(const PanelArgs& A, int64_t n, int64_t b, float j) {
+  float* const at = A.os.data + b * A.os.sb + n * A.os.sn;
+  *at = A.product == 2 ? *at + j : j;
+}
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v2f __attribute__((ext_vector_type(2)));
@@ -597,7 +604,11 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
       for (int e = e_begin + lane; e < e_end; e += 64) {
         const int64_t row = row0_e + static_cast<int64_t>(E.rows[e]);
 #pragma unroll
-        for (int j = 0; j < BT; ++j) update(E, row, j, E.sorted[static_cast<int64_t>(e) * BT + j]);
+        for (int j = 0; j < BT; ++j) {
+          const float sum = E.sorted[static_cast<int64_t>(e) * BT + j];
+          if (E.product) store_product(E, row, j, sum);
+          else update(E, row, j, sum);
+        }
       }
     }
     return;
@@ -660,6 +671,16 @@ __global__ __launch_bounds__(kThreads) void panel_combine_kernel(PanelArgs A) {
   const int64_t n = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (n >= A.N) return;
   const int64_t plane = A.N * BT;
+  if (A.product) {
+    // W @ s alone: the panels' sums in panel order, stored or added.
+#pragma unroll
+    for (int j = 0; j < BT; ++j) {
+      float sum = 0.0f;
+      for (int p = 0; p < A.n_panels; ++p) sum += A.partials[p * plane + n * BT + j];
+      store_product(A, n, j, sum);
+    }
+    return;
+  }
   const NeuronParams prm = load_params(A.p, n);
   float s[BT], d[BT], a[BT], u[BT], v[BT];
 #pragma unroll
@@ -721,8 +742,10 @@ int panel_geometry(int64_t batch, int32_t* width, int32_t* waves) {
   return NS_OK;
 }
 
-// Validation and launch of the panel path for ns_dendritic_step.
-int panel_step(const ns_step_args& a, hipStream_t stream) {
+// Validation and launch of the panel path for ns_dendritic_step (product 0)
+// and for the product W @ s alone (1: stored into out_state, 2: added to it).
+// With launch false it only validates.
+int panel_step(const ns_step_args& a, hipStream_t stream, int product, bool launch) {
   const ns_panel_plan& pl = *a.panels;
   int32_t cap = 0, waves = 0;
   if (int rc = panel_geometry(a.batch, &cap, &waves)) return rc;
@@ -745,7 +768,8 @@ int panel_step(const ns_step_args& a, hipStream_t stream) {
   if (pl.flags & ~(NS_PANEL_PAIRS | NS_PANEL_COMBINE_LAUNCH))
     return fail("unknown panel plan flags %d", pl.flags);
   const bool pairs = (pl.flags & NS_PANEL_PAIRS) != 0;
-  const bool one_launch = pl.n_panels > 1 && !(pl.flags & NS_PANEL_COMBINE_LAUNCH);
+  // The products always finish in the second kernel.
+  const bool one_launch = !product && pl.n_panels > 1 && !(pl.flags & NS_PANEL_COMBINE_LAUNCH);
   if (one_launch) {
     if (!pl.tile_ranges || !pl.range_counters)
       return fail("panel tile ranges and range counters are required with several panels");
@@ -755,6 +779,14 @@ int panel_step(const ns_step_args& a, hipStream_t stream) {
   }
   if (a.matrix.format == NS_WEIGHT_NVFP4 && !pairs && !pl.slot_scales)
     return fail("NVFP4 panels require per-slot block scales");
+  if (product) {
+    if (!a.out_state.data) return fail("the product needs an output plane");
+    if (overlaps(extent(a.out_state, a.batch, a.n_neurons), extent(a.state, a.batch, a.n_neurons)))
+      return fail("the product's output must not overlap its source");
+    if (!distinct_elements(a.out_state.stride_b, a.out_state.stride_n, a.batch, a.n_neurons))
+      return fail("the product's output must not overlap itself (strides %lld, %lld)",
+                  (long long)a.out_state.stride_b, (long long)a.out_state.stride_n);
+  }
   if (!pl.partials) return fail("the panel path needs its partials workspace");
   const uintptr_t need = a.matrix.format == NS_WEIGHT_F32 ? 4
                          : (a.matrix.format == NS_WEIGHT_F16 ||
@@ -803,6 +835,7 @@ int panel_step(const ns_step_args& a, hipStream_t stream) {
   A.os = out_plane(a.out_state); A.od = out_plane(a.out_dendrite);
   A.oa = out_plane(a.out_adaptation); A.oj = out_plane(a.out_current);
   const bool aligned = reinterpret_cast<uintptr_t>(a.state.data) % 16 == 0;
+  A.product = product;
   A.s_vec = aligned && ((a.batch == 1 && a.state.stride_n == 1) ||
                         (a.batch == 2 && a.state.stride_b == 1 && a.state.stride_n == 2));
   {
@@ -823,6 +856,7 @@ int panel_step(const ns_step_args& a, hipStream_t stream) {
     // combine kernel finishes the tick (bitwise the same results).
     if (!ok) { A.tile_ranges = nullptr; A.counters = nullptr; }
   }
+  if (!launch) return NS_OK;
   const int fmt = a.matrix.format == NS_WEIGHT_NVFP4 && pairs ? kNvfp4Pairs : a.matrix.format;
   const hipError_t err = a.batch == 1 ? launch_panels<1>(A, fmt, pl.n_tiles, stream)
                                       : launch_panels<2>(A, fmt, pl.n_tiles, stream);

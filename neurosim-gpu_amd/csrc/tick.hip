@@ -384,7 +384,7 @@ hipError_t launch_tick(const TickArgs& A, int fmt, hipStream_t stream) {
   }
 }
 
-int panel_step(const ns_step_args& a, hipStream_t stream);
+int panel_step(const ns_step_args& a, hipStream_t stream, int product, bool launch);
 
 // Host-side validation shared by the tick and the plain product.
 int check_csr(const ns_csr& m, int64_t n) {
@@ -499,7 +499,7 @@ extern "C" int ns_dendritic_step(const ns_step_args* args, void* stream) {
     if (int rc = check_matrix(a.matrix, a.n_neurons, a.plan, a.batch)) return rc;
   if (a.batch == 0) return NS_OK;  // empty planes may carry null pointers
   if (int rc = check_step_planes(a)) return rc;
-  if (a.panels) return panel_step(a, static_cast<hipStream_t>(stream));
+  if (a.panels) return panel_step(a, static_cast<hipStream_t>(stream), 0, true);
 
   TickArgs A{};
   A.N = a.n_neurons; A.B = a.batch; A.M = a.matrix.n_edges;

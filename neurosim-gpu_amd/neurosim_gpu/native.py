@@ -35,7 +35,7 @@ import numpy as np
 import torch
 
 _LIB_NAME = "libneurosim_hip.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 WEIGHT_F32, WEIGHT_F16, WEIGHT_E4M3, WEIGHT_NVFP4 = 0, 1, 2, 3
 _PLAN_CACHE = 64   # row plans kept per extension (one per live topology and batch width)
@@ -132,7 +132,7 @@ class _StepGradArgs(ctypes.Structure):
                 ("d_state", _OutPlane), ("d_dendrite", _OutPlane), ("d_adaptation", _OutPlane),
                 ("d_drive", _OutPlane), ("d_dendritic_drive", _OutPlane),
                 ("d_weight", _c_ptr), ("d_params", _c_ptr * 6), ("workspace", _c_ptr),
-                ("current", _c_ptr), ("out_weight", _c_ptr)]
+                ("current", _c_ptr), ("out_weight", _c_ptr), ("transposed_panels", _c_ptr)]
 
 
 class _EncodeArgs(ctypes.Structure):
@@ -844,7 +844,7 @@ class NativeExtension:
                                 out_rowptr, dst, weight_index, grad_state, grad_dendrite,
                                 grad_adaptation, *, need_drive=False, need_dendritic=False,
                                 need_weight=False, need_params=(False,) * 6, out_weight=None,
-                                current=None):
+                                current=None, transposed_panels=None):
         """Gradients of one float32 tick (ns_dendritic_step_backward).
 
         Returns (d_state, d_dendrite, d_adaptation, d_drive, d_dendritic_drive,
@@ -854,6 +854,8 @@ class NativeExtension:
         transposed product then streams instead of gathering.  ``current``
         optionally gives the forward's j = W @ s as ``dendritic_step`` wrote it
         (``current_out``, a neuron-major [B,N] plane), which spares recomputing it.
+        ``transposed_panels`` (a ``_PanelPlan`` of ``TransposedPanels.plan``,
+        batch 1 or 2) runs the transposed product on the panel kernel.
         """
         _check_state(state)
         batch, n = state.shape
@@ -881,6 +883,8 @@ class NativeExtension:
             if out_weight.numel() != weight.numel() or not out_weight.is_contiguous():
                 raise RuntimeError("source-major weights must be a contiguous [M] vector")
             args.out_weight = out_weight.data_ptr() if out_weight.numel() else None
+        if transposed_panels is not None:
+            args.transposed_panels = ctypes.addressof(transposed_panels)
         if current is not None:
             _check_float(current, state, "current")
             if current.shape != state.shape or current.stride() != (1, batch):

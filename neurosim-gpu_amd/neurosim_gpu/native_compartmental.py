@@ -23,6 +23,8 @@ library raises at construction, nothing falls back silently.
 
 from __future__ import annotations
 
+from types import SimpleNamespace
+
 import torch
 
 from .compartmental import DendriticDynamics, DendriticMatrixRuntime, DendriticPELSRuntime
@@ -125,6 +127,42 @@ class SourceMajorWeights:
         return self._values
 
 
+class TransposedPanels:
+    """Column-panel layout of the transposed matrix, for the backward's W^T @ g.
+
+    Its rows are the sources (``out_rowptr``, ``dst``: the source-major view)
+    and its slots name CSR positions through ``out_weight_index``, so the slot
+    weights are gathered from the CSR-order weights directly.  That gather is
+    one random read per edge, as costly as the out-edge walk it replaces, so
+    it is made on the second request for one weight version (backpropagation
+    through several ticks, or repeated passes on fixed weights); the first
+    request returns None and the backward walks the out-edges.  Built on the
+    host from the source-major view (set-up only, like the forward's layout)."""
+
+    def __init__(self, topology, batch: int, device, *, max_panel_width: int | None = None) -> None:
+        view = SimpleNamespace(n_neurons=topology.n_neurons, n_edges=topology.n_edges,
+                               in_rowptr=topology.out_rowptr, in_col=topology.dst)
+        self.layout = PanelLayout(view, batch, device, max_panel_width=max_panel_width,
+                                  combine_launch=True)
+        perm = self.layout.perm
+        owi = topology.out_weight_index.to(device=device, dtype=torch.int32)
+        self.layout.perm = torch.where(perm >= 0, owi[perm.clamp(min=0).long()],
+                                       perm).to(torch.int32).contiguous()
+        self._key, self._source, self._seen = None, None, 0
+
+    def plan(self, weight: torch.Tensor):
+        """The plan struct with ``weight`` (float32, CSR order) in slot order,
+        or None on the first request for this weight version."""
+        key = _weight_key(weight)
+        if key != self._key or self._source is not weight:
+            self._key, self._source, self._seen = key, weight, 0
+        self._seen += 1
+        if self._seen < 2:
+            return None
+        slots, _ = self.layout.slot_weights(key, weight, None)
+        return self.layout.plan_struct(slots, None)
+
+
 class _NativeTick(torch.autograd.Function):
     """One float32 fused tick (ns_dendritic_step) whose backward is native too
     (ns_dendritic_step_backward): gradients of the states, tensor drives, the
@@ -133,7 +171,7 @@ class _NativeTick(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, info, state, dendrite, adaptation, weight, drive, dendritic_drive, *params):
-        extension, topology, us, vs, width, extra, _ = info
+        extension, topology, us, vs, width, extra, _, _ = info
         # j = W @ s kept for the backward, which then needs no product of its own
         current = new_planes(1, state.shape[0], state.shape[1], state)[0]
         outs = extension.dendritic_step(state, dendrite, adaptation, list(params),
@@ -151,7 +189,7 @@ class _NativeTick(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_state, grad_dendrite, grad_adaptation):
-        extension, topology, us, vs, _, _, source_major = ctx.info
+        extension, topology, us, vs, _, _, source_major, transposed = ctx.info
         saved = list(ctx.saved_tensors)
         state, dendrite, adaptation, weight = saved[:4]
         params = saved[4:10]
@@ -159,6 +197,9 @@ class _NativeTick(torch.autograd.Function):
         drive = next(rest) if ctx.has_drive[0] else None
         dendritic_drive = next(rest) if ctx.has_drive[1] else None
         needs = ctx.needs_input_grad
+        panels = transposed.plan(weight) if transposed is not None else None
+        out_weight = (None if panels is not None
+                      else source_major.get(weight, topology.out_weight_index))
         (d_state, d_dendrite, d_adaptation, d_drive, d_dendritic, d_weight,
          d_params) = extension.dendritic_step_backward(
             state, dendrite, adaptation, params, topology.in_rowptr, topology.in_col, weight,
@@ -166,7 +207,7 @@ class _NativeTick(torch.autograd.Function):
             topology.out_weight_index, grad_state, grad_dendrite, grad_adaptation,
             need_drive=bool(needs[5]), need_dendritic=bool(needs[6]), need_weight=bool(needs[4]),
             need_params=tuple(bool(x) for x in needs[7:13]),
-            out_weight=source_major.get(weight, topology.out_weight_index), current=ctx.current)
+            out_weight=out_weight, current=ctx.current, transposed_panels=panels)
         ctx.current = None
         return (None, d_state if needs[1] else None, d_dendrite if needs[2] else None,
                 d_adaptation if needs[3] else None, d_weight, d_drive, d_dendritic, *d_params)
@@ -274,6 +315,10 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
                         if use_panels else None)
         self.source_major_weights = SourceMajorWeights()
         self._recorded_key, self._recorded_source, self._recorded_seen = None, None, 0
+        # The backward's transposed product on panels (False: the out-edge walk).
+        self.transposed_panels_enabled = True
+        self._transposed: TransposedPanels | None = None
+        self._panel_width = panel_width
         self._bands = (BandLayout(topology, initial_state.device,
                                   band_width=band_width or BAND_WIDTH, block_rows=band_rows,
                                   block_steps=band_steps)
@@ -395,6 +440,18 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         return self.state
 
 
+    def _transposed_layout(self) -> TransposedPanels | None:
+        """The transposed matrix's panel layout for the backward, built on the
+        first recorded tick when the forward runs on panels (the graph is dense
+        enough for them); None otherwise."""
+        if self._panels is None or not self.transposed_panels_enabled:
+            return None
+        if self._transposed is None:
+            self._transposed = TransposedPanels(self.topology, self.state.shape[0],
+                                                self.state.device,
+                                                max_panel_width=self._panel_width)
+        return self._transposed
+
     def _autograd_step(self, drive, dendritic_drive) -> torch.Tensor:
         """A float32 tick recorded for autograd, native forward and backward."""
         u, us = self._drive(drive)
@@ -405,7 +462,7 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         if plan is not None:
             extra["panels"] = plan
         info = (self.extension, self.topology, us, vs, self.threads_per_row, extra,
-                self.source_major_weights)
+                self.source_major_weights, self._transposed_layout())
         self.state, self.dendritic_state, self.adaptation_state = _NativeTick.apply(
             info, self.state, self.dendritic_state, self.adaptation_state, weight, u, v,
             *self._parameters())

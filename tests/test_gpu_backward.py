@@ -67,7 +67,7 @@ def base(p):
 
 
 def run(runtime_cls, g, inputs, dtype, device, ticks, *, scalar_drives, expanded,
-        source_major=True, **kw):
+        source_major=True, transposed_panels=True, **kw):
     topo = topology(g, dtype, device)
     topo.in_weight.requires_grad_(True)
     mdl = model(inputs["params"], dtype, device, expanded)
@@ -75,6 +75,8 @@ def run(runtime_cls, g, inputs, dtype, device, ticks, *, scalar_drives, expanded
     rt = runtime_cls(topo, mdl, state0.detach(), **kw)
     if hasattr(rt, "source_major_weights"):
         rt.source_major_weights.enabled = source_major
+    if hasattr(rt, "transposed_panels_enabled"):
+        rt.transposed_panels_enabled = transposed_panels
     rt.state = state0
     rt.dendritic_state = leaf(inputs["dendrite"], dtype, device)
     rt.adaptation_state = leaf(inputs["adaptation"], dtype, device)
@@ -163,6 +165,30 @@ def test_gradients_match_the_oracle(gpu, ticks, batch, scalar_drives, expanded):
     native, rt = run(NativeDendriticMatrixRuntime, g, inputs, torch.float32, gpu, ticks, **kw)
     assert rt.last_backend == "native-autograd"
     compare(native, oracle_gradients(g, inputs, ticks, **kw))
+
+
+@pytest.mark.parametrize("ticks,batch,width", [(2, 1, 1000), (4, 2, 1000), (3, 1, None)])
+def test_transposed_product_on_panels_matches_the_oracle(gpu, ticks, batch, width):
+    """With the forward on column panels the backward's transposed product
+    W^T @ g runs, from the second backward of a weight version on, on a panel
+    layout of the transposed matrix (rows = sources; three panels at width
+    1000, so a second kernel adds the per-panel sums into d_state); the
+    gradients through several ticks match the oracle, and the out-edge walk
+    to float32 summation order."""
+    print(f"case backward transposed panels ticks={ticks} batch={batch} width={width}",
+          flush=True)
+    g = graph(3000, 90_000, 17)
+    inputs = inputs_for(g, batch, 40 + batch)
+    kw = dict(scalar_drives=False, expanded=False, kernel="panels", panel_width=width)
+    native, rt = run(NativeDendriticMatrixRuntime, g, inputs, torch.float32, gpu, ticks, **kw)
+    assert rt._transposed is not None and rt._transposed._seen == ticks
+    assert rt._transposed.layout._slot_weights is not None     # the panels ran
+    assert rt._transposed.layout.n_panels == (3 if width else 1)
+    compare(native, oracle_gradients(g, inputs, ticks, scalar_drives=False, expanded=False))
+    walked, rt2 = run(NativeDendriticMatrixRuntime, g, inputs, torch.float32, gpu, ticks,
+                      transposed_panels=False, **kw)
+    assert rt2._transposed is None
+    compare(native, {k: v.detach().double().cpu() for k, v in walked.items()}, rtol=1e-5)
 
 
 def test_backward_is_repeatable(gpu):
