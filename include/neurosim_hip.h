@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 12
+#define NS_ABI_VERSION 13
 
 /* Return codes. */
 #define NS_OK 0
@@ -164,7 +164,7 @@ typedef struct ns_panel_plan {
  * every workgroup on that XCD gathers from it.  Destination rows are cut into
  * `n_row_blocks` blocks of `block_rows` rows; one workgroup owns one block
  * (and one 16-column tile), keeps the block's row sums in LDS, walks the
- * bands in order and finally applies the update.  Each of its 4 wavefronts
+ * bands in order and finally applies the update.  Each of its 8 wavefronts
  * owns a fixed set of the block's rows (dealt by degree, longest first onto
  * the least-loaded wavefront).  Per band, a wavefront's rows with edges in
  * the band are packed into groups of 64 lanes: a group's first rows are the
@@ -190,8 +190,8 @@ typedef struct ns_band_plan {
   int32_t block_steps;         /* steps per register block the plan was cut for */
   int32_t reserved;
   int64_t n_slots;
-  const int32_t* wave_blocks;  /* [n_row_blocks*4 + 1]: wavefront w of row block q owns
-                                  blocks wave_blocks[4q+w] .. wave_blocks[4q+w+1]-1 */
+  const int32_t* wave_blocks;  /* [n_row_blocks*8 + 1]: wavefront w of row block q owns
+                                  blocks wave_blocks[8q+w] .. wave_blocks[8q+w+1]-1 */
   const int32_t* blocks;       /* [n_blocks+1][4]: first step, band,
                                   steps | last << 8 | step in group << 9 (last: the block
                                   ends its group), group */
@@ -439,7 +439,7 @@ int ns_dendritic_step(const ns_step_args* args, void* stream);
  * (1..ns_band_max_block_rows()), register blocks of at most `block_steps`
  * steps (1..8).  Call once with all output pointers NULL to get the sizes in
  * *plan (n_bands, n_row_blocks, n_blocks, n_groups, n_slots), then again with
- * wave_blocks int32[4*n_row_blocks+1], blocks int32[4*(n_blocks+1)], rows
+ * wave_blocks int32[8*n_row_blocks+1], blocks int32[4*(n_blocks+1)], rows
  * uint32[64*n_groups], perm int32[n_slots] (-1 for padding), col
  * uint16[n_slots].  Pointer fields of *plan are not touched.  blocks holds
  * n_blocks records plus the sentinel, rows n_groups groups including the

@@ -11,10 +11,17 @@
 //    about twice as fast.  So sources are cut into bands, and every
 //    workgroup walks the bands in the same order: the workgroups resident on
 //    one XCD gather from about one band at a time.
-//  * One 256-lane workgroup owns a block of destination rows and one 16-column
-//    tile.  Its row sums live in LDS for the whole tick, so no partial sums
-//    leave the compute unit.  Each wavefront owns a fixed set of the block's
-//    rows, so its LDS updates race with no other wavefront.
+//  * One 512-lane workgroup (one per compute unit) owns a block of
+//    destination rows and one 16-column tile.  Its row sums live in LDS for
+//    the whole tick, so no partial sums leave the compute unit.  Each
+//    wavefront owns a fixed set of the block's rows, so its LDS updates race
+//    with no other wavefront.  The wavefronts finish each band before any
+//    starts the next (a workgroup barrier per band): a compute unit's eight
+//    wavefronts then gather from one band, and the workgroups of an XCD, which
+//    start together with equal work, stay within a band or two of each other.
+//    (Two 256-lane workgroups per compute unit drifted apart by up to a dozen
+//    bands, the older one issuing first; L2 then held about half the
+//    gathers, against nearly nine in ten with the barrier.)
 //  * Per band a wavefront's rows are packed 64 lanes at a time, longest
 //    segments first; lane l walks its row's segment, gathering the whole
 //    64-byte source row with four 16-byte loads per edge and keeping 16
@@ -46,6 +53,7 @@ struct BandArgs {
   const float* s_rows;   // neuron-major state: source n's columns at s_rows + n * s_stride
   int64_t s_stride;
   int32_t band_width, block_rows;
+  int32_t n_bands, reserved;
   const int32_t* wave_blocks;
   const int32_t* blocks;
   const uint32_t* rows;   // lane words: first row, second row, switch step
@@ -159,7 +167,10 @@ __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) 
     cur = load_band_block(A, b_begin);
     load_band_slots<FMT, D>(A, cur, lane, here, row);
   }
-  for (int32_t b = b_begin; b < b_end; ++b) {
+  // Every wavefront passes exactly n_bands barriers, whatever its blocks.
+  int32_t b = b_begin;
+  for (int32_t band = 0; band < A.n_bands; ++band) {
+  for (; b < b_end && cur.band == band; ++b) {
     // Gathers of this block: the whole 16-column row of each slot's source.
     const int64_t base = static_cast<int64_t>(cur.band) * A.band_width;
     // A padding slot (or a step past the block's end) reads the zero row: the
@@ -217,6 +228,7 @@ __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) 
     for (int k = 0; k < D; ++k) here[k] = ahead[k];
   }
   __syncthreads();
+  }
 
   // The update: consecutive lanes take consecutive columns of a row.
   for (int i = tid; i < nrows * 16; i += kBandWaves * 64) {
@@ -301,7 +313,7 @@ int band_step(const ns_step_args& a, const ns_band_plan& pl, hipStream_t stream)
   A.u = plane(a.drive, a.state.data); A.v = plane(a.dendritic_drive, a.state.data);
   for (int i = 0; i < 6; ++i) A.p.v[i] = Vec{a.params[i].data, a.params[i].stride};
   A.s_rows = a.state.data; A.s_stride = a.state.stride_n;
-  A.band_width = pl.band_width; A.block_rows = pl.block_rows;
+  A.band_width = pl.band_width; A.block_rows = pl.block_rows; A.n_bands = pl.n_bands;
   A.wave_blocks = pl.wave_blocks; A.blocks = pl.blocks; A.rows = pl.rows; A.col = pl.col;
   A.weight = pl.weight; A.slot_scales = pl.slot_scales; A.gscale = a.matrix.global_scale;
   A.os = out_plane(a.out_state); A.od = out_plane(a.out_dendrite);

@@ -35,7 +35,7 @@ import numpy as np
 import torch
 
 _LIB_NAME = "libneurosim_hip.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 WEIGHT_F32, WEIGHT_F16, WEIGHT_E4M3, WEIGHT_NVFP4 = 0, 1, 2, 3
 _PLAN_CACHE = 64   # row plans kept per extension (one per live topology and batch width)
@@ -437,7 +437,7 @@ def plan_bands_host(rowptr: torch.Tensor, col: torch.Tensor, band_width: int, bl
     args = (rowptr.ctypes.data, col.ctypes.data if col.size else None, n, int(band_width),
             int(block_rows), int(block_steps), ctypes.byref(plan))
     _raise_on(lib.ns_plan_bands(*args, *([None] * 5)), lib)
-    wave_blocks = np.empty(4 * plan.n_row_blocks + 1, np.int32)
+    wave_blocks = np.empty(BAND_WAVES * plan.n_row_blocks + 1, np.int32)
     blocks = np.empty(4 * (plan.n_blocks + 1), np.int32)
     rows = np.empty(64 * plan.n_groups, np.uint32)
     perm = np.empty(plan.n_slots, np.int32)
@@ -585,18 +585,19 @@ class PanelLayout(_SlotLayout):
 # Sources per band: 32768 neurons x 16 columns x 4 bytes = 2 MB of state, which
 # stays resident in one XCD's 4 MB L2 beside the streamed slots.
 BAND_WIDTH = 32768
-# Rows per band workgroup such that two workgroups fit one compute unit's LDS.
-BAND_ROWS_TWO_PER_UNIT = 1248
+# Wavefronts per band workgroup (kBandWaves): one workgroup per compute unit.
+BAND_WAVES = 8
 
 
 def default_band_rows(n: int, units: int) -> int:
-    """Destination rows per band workgroup: two workgroups per compute unit, in
-    whole rounds (the grid is a multiple of 2 * units), as few rounds as fit LDS.
+    """Destination rows per band workgroup: one workgroup per compute unit, in
+    whole rounds (the grid is a multiple of ``units``), as few rounds as fit LDS.
     Workgroups of one round start together and so walk the bands together."""
+    limit = band_max_block_rows()
     rounds = 1
-    while -(-n // (2 * units * rounds)) > BAND_ROWS_TWO_PER_UNIT:
+    while -(-n // (units * rounds)) > limit:
         rounds += 1
-    return max(1, -(-n // (2 * units * rounds)))
+    return max(1, -(-n // (units * rounds)))
 
 
 class BandLayout(_SlotLayout):

@@ -264,8 +264,8 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
     slots carry one block-scale byte per pair instead of per slot; the default
     uses it for NVFP4 weights only.
     ``band_width`` sets the sources per band (default ``BAND_WIDTH``),
-    ``band_rows`` the destination rows per band workgroup (default: two
-    workgroups per compute unit, ``default_band_rows``) and ``band_steps`` the
+    ``band_rows`` the destination rows per band workgroup (default: one
+    workgroup per compute unit, ``default_band_rows``) and ``band_steps`` the
     register block (2, 4 or 8 steps).
     """
 

@@ -146,7 +146,7 @@ def test_step_validation_messages(lib):
 
 
 def fake_band_plan(n, width=4, rows=4):
-    tables = [np.zeros(4 * (-(-n // rows)) + 1, np.int32), np.zeros(4, np.int32),
+    tables = [np.zeros(native.BAND_WAVES * (-(-n // rows)) + 1, np.int32), np.zeros(4, np.int32),
               np.full(64, 0xFFFFFF, np.uint32), np.full(8 * 64, 0xFFFF, np.uint16),
               np.zeros(8 * 64, np.float32)]
     plan = native._BandPlan()

@@ -26,6 +26,7 @@ from neurosim_gpu.native import band_max_block_rows, plan_bands_host
 
 PAD = 0xFFFF
 NO_ROW = 0xFFF
+WAVES = native.BAND_WAVES
 TAIL = 8 * 64
 
 
@@ -74,7 +75,7 @@ def test_band_layout_invariants(n, m, seed, hubs, width, rows, steps):
     n_row_blocks = -(-n // rows)
     assert (plan.n_bands, plan.n_row_blocks, plan.block_rows, plan.band_width) == (
         n_bands, n_row_blocks, rows, width)
-    assert wave_blocks.size == 4 * n_row_blocks + 1 and wave_blocks[0] == 0
+    assert wave_blocks.size == WAVES * n_row_blocks + 1 and wave_blocks[0] == 0
     assert wave_blocks[-1] == plan.n_blocks and np.all(np.diff(wave_blocks) >= 0)
     assert blocks.shape == (plan.n_blocks + 1, 4) and group_rows.shape == (plan.n_groups, 64)
     assert perm.size == cols.size == plan.n_slots
@@ -97,11 +98,11 @@ def test_band_layout_invariants(n, m, seed, hubs, width, rows, steps):
     owner = {}
     for q in range(n_row_blocks):
         r0 = q * rows
-        for w in range(4):
+        for w in range(WAVES):
             seen_bands = {}
             prev_band = -1
-            b = wave_blocks[4 * q + w]
-            while b < wave_blocks[4 * q + w + 1]:
+            b = wave_blocks[WAVES * q + w]
+            while b < wave_blocks[WAVES * q + w + 1]:
                 # one group: consecutive blocks of one group and band, the last marked
                 group, band = blocks[b, 3], blocks[b, 1]
                 assert band >= prev_band
@@ -170,9 +171,9 @@ def test_band_emulation_matches_csr_product(n, m, seed, hubs, width, rows, steps
     sums = np.zeros((n, 16), np.float32)
     for q in range(plan.n_row_blocks):
         r0 = q * rows
-        for w in range(4):
+        for w in range(WAVES):
             acc = np.zeros((64, 16), np.float32)
-            for b in range(wave_blocks[4 * q + w], wave_blocks[4 * q + w + 1]):
+            for b in range(wave_blocks[WAVES * q + w], wave_blocks[WAVES * q + w + 1]):
                 start, band, info, group = blocks[b]
                 lanes = [lane_rows(word) for word in group_rows[group]]
                 for k in range(info & 0xFF):
@@ -240,8 +241,9 @@ def test_band_plan_does_not_depend_on_thread_count(monkeypatch):
 
 def test_band_padding_at_scale_out_density():
     """About 3.3 edges per (row, band), as at N=1M, M=100M with bands of 32,768
-    sources, and 977-row blocks: with a second row per lane where one fits the
-    layout holds at most 1.2 slots per edge (one row per lane: about 1.48)."""
+    sources, and 1954-row blocks of 8 wavefronts (244 rows each, as there):
+    with a second row per lane where one fits the layout holds at most 1.2
+    slots per edge (one row per lane: about 1.48)."""
     rng = np.random.default_rng(5)
     n, m = 100_000, 10_000_000
     dst = np.sort(rng.integers(0, n, m))
@@ -249,7 +251,7 @@ def test_band_padding_at_scale_out_density():
     rowptr[1:] = np.cumsum(np.bincount(dst, minlength=n))
     col = rng.integers(0, n, m).astype(np.int32)
     plan = plan_bands_host(torch.from_numpy(rowptr.astype(np.int32)), torch.from_numpy(col),
-                           3277, 977, 4)[0]
+                           3277, 1954, 4)[0]
     ratio = (plan.n_slots - TAIL) / m
     print(f"slots per edge {ratio:.3f}")
     assert ratio <= 1.2
