@@ -23,9 +23,10 @@
 //    bands, the older one issuing first; L2 then held about half the
 //    gathers, against nearly nine in ten with the barrier.)
 //  * Per band a wavefront's rows are packed 64 lanes at a time, longest
-//    segments first; lane l walks its row's segment, gathering the whole
-//    64-byte source row with four 16-byte loads per edge and keeping 16
-//    running sums in registers.  A lane whose row ends early may take a
+//    segments first; lane l walks its row's segment.  The four lanes of a
+//    quad gather their four rows' 64-byte source rows together, each lane
+//    one 16-byte quarter of each, and each lane keeps the running sums of its
+//    quarter's four columns for the quad's four rows (16 registers).  A lane whose row ends early may take a
 //    second, shorter row in the group's remaining steps: at the switch step it
 //    adds its sums to the first row's LDS sums and starts again from zero.
 //    At the group's end the lane adds them to its (last) row's LDS sums.
@@ -107,15 +108,14 @@ __device__ __forceinline__ void load_band_slots(const BandArgs& A, const BandBlo
   row = A.rows[int64_t{64} * blk.group + lane];
 }
 
-// Adds a lane's 16 running sums to its row's LDS sums.
-__device__ __forceinline__ void add_to_row(v4f* sums4, uint32_t row, const float (&acc)[16]) {
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    v4f t = sums4[row * 4 + q];
-    t.x += acc[4 * q + 0]; t.y += acc[4 * q + 1];
-    t.z += acc[4 * q + 2]; t.w += acc[4 * q + 3];
-    sums4[row * 4 + q] = t;
-  }
+// Adds four running sums (acc[4j .. 4j+3]: columns 4*seg .. 4*seg+3 of one
+// row) to that row's LDS sums.
+__device__ __forceinline__ void add_quarter(v4f* sums4, uint32_t row, int seg, float (&acc)[16],
+                                            int j) {
+  v4f t = sums4[row * 4 + seg];
+  t.x += acc[4 * j + 0]; t.y += acc[4 * j + 1];
+  t.z += acc[4 * j + 2]; t.w += acc[4 * j + 3];
+  sums4[row * 4 + seg] = t;
 }
 
 // Source of padding slots and of steps past a block's end: 16 zeros.
@@ -136,6 +136,19 @@ __device__ __forceinline__ float decode_band(const BandSlot& x, int lane, float 
     const ns_v2f pair = e2m1_pair(x.w & 0xFFu);
     return ((lane & 1) ? pair.y : pair.x) * (e4m3_to_float(x.sc) * gscale);
   }
+}
+
+// Value `v` of lane J of each group of four lanes (a quad), for every lane of
+// the quad: a DPP quad permutation.
+template <int J>
+__device__ __forceinline__ uint32_t from_quad_lane(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v),
+                                                        J | (J << 2) | (J << 4) | (J << 6),
+                                                        0xF, 0xF, false));
+}
+__device__ __forceinline__ void quad_values(uint32_t v, uint32_t (&out)[4]) {
+  out[0] = from_quad_lane<0>(v); out[1] = from_quad_lane<1>(v);
+  out[2] = from_quad_lane<2>(v); out[3] = from_quad_lane<3>(v);
 }
 
 template <int FMT, int D>
@@ -171,21 +184,32 @@ __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) 
   int32_t b = b_begin;
   for (int32_t band = 0; band < A.n_bands; ++band) {
   for (; b < b_end && cur.band == band; ++b) {
-    // Gathers of this block: the whole 16-column row of each slot's source.
+    // Gathers of this block: each slot's whole 16-column source row.
     const int64_t base = static_cast<int64_t>(cur.band) * A.band_width;
-    // A padding slot (or a step past the block's end) reads the zero row: the
-    // two global addresses are blended by a mask, so the choice stays a
-    // select and the loads stay global loads.
+    // The four lanes of a quad gather together: at step k, instruction j loads
+    // quarter `seg` (16 bytes) of the source row of the quad's lane j, so one
+    // load instruction touches 16 rows, each in one 64-byte piece, rather than
+    // 64 rows as when each lane loads its own row in four instructions: a
+    // quarter of the cache-line accesses.  Lane l then accumulates columns
+    // 4*seg .. 4*seg+3 of the rows of its quad's four lanes (acc[4j..4j+3] for
+    // lane j's row), in step order, and adds them to those rows' LDS sums at
+    // each row's switch or end.  A padding slot (or a step past the block's
+    // end) reads the zero row: the two global addresses are blended by a mask,
+    // so the choice stays a select and the loads stay global loads.
+    const int seg = lane & 3;
     v4f g[D][4];
 #pragma unroll
     for (int k = 0; k < D; ++k) {
-      const bool real = k < cur.steps && here[k].c != kBandPad;
-      const uint64_t mask = 0ull - static_cast<uint64_t>(real);
-      const uint64_t at = reinterpret_cast<uint64_t>(srow + (base + here[k].c) * A.s_stride);
-      const uint64_t src = (at & mask) | (zero_row & ~mask);
-      const global_v4f_ptr p = reinterpret_cast<global_v4f_ptr>(src);
+      uint32_t cq[4];
+      quad_values(here[k].c, cq);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) g[k][q] = p[q];
+      for (int j = 0; j < 4; ++j) {
+        const bool real = k < cur.steps && cq[j] != kBandPad;
+        const uint64_t mask = 0ull - static_cast<uint64_t>(real);
+        const uint64_t at = reinterpret_cast<uint64_t>(srow + (base + cq[j]) * A.s_stride + 4 * seg);
+        const uint64_t src = (at & mask) | ((zero_row + 16u * seg) & ~mask);
+        g[k][j] = *reinterpret_cast<global_v4f_ptr>(src);
+      }
     }
     // The next block's slots load while the gathers are in flight (past the
     // wavefront's last block this reads the next wavefront's first block or
@@ -194,31 +218,41 @@ __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) 
     BandSlot ahead[D];
     uint32_t row_ahead;
     load_band_slots<FMT, D>(A, nxt, lane, ahead, row_ahead);
-    // A lane with a second row switches after block step `turn` (none: out of range).
-    const uint32_t first_row = row & kBandNoRow;
-    const int turn = static_cast<int>(row >> 24) - cur.t0 - 1;
+    // The quad's lane words: lane j's rows and the step where it switches.
+    uint32_t rowq[4];
+    quad_values(row, rowq);
 #pragma unroll
     for (int k = 0; k < D; ++k) {
       if (k < cur.steps) {
         const float w = decode_band<FMT>(here[k], lane, gscale);
+        uint32_t wq[4];
+        quad_values(__builtin_bit_cast(uint32_t, w), wq);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          acc[4 * q + 0] += w * g[k][q].x;
-          acc[4 * q + 1] += w * g[k][q].y;
-          acc[4 * q + 2] += w * g[k][q].z;
-          acc[4 * q + 3] += w * g[k][q].w;
+        for (int j = 0; j < 4; ++j) {
+          const float wj = __builtin_bit_cast(float, wq[j]);
+          acc[4 * j + 0] += wj * g[k][j].x;
+          acc[4 * j + 1] += wj * g[k][j].y;
+          acc[4 * j + 2] += wj * g[k][j].z;
+          acc[4 * j + 3] += wj * g[k][j].w;
         }
-        if (k == turn) {
-          add_to_row(sums4, first_row, acc);
 #pragma unroll
-          for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+        for (int j = 0; j < 4; ++j) {
+          const int turn_j = static_cast<int>(rowq[j] >> 24) - cur.t0 - 1;
+          if (k == turn_j) {   // lane j moves on to its second row
+            add_quarter(sums4, rowq[j] & kBandNoRow, seg, acc, j);
+            acc[4 * j + 0] = acc[4 * j + 1] = acc[4 * j + 2] = acc[4 * j + 3] = 0.0f;
+          }
         }
       }
     }
     if (cur.last) {
-      const uint32_t second_row = (row >> kBandRowBits) & kBandNoRow;
-      const uint32_t last_row = second_row != kBandNoRow ? second_row : first_row;
-      if (last_row != kBandNoRow) add_to_row(sums4, last_row, acc);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t first_j = rowq[j] & kBandNoRow;
+        const uint32_t second_j = (rowq[j] >> kBandRowBits) & kBandNoRow;
+        const uint32_t r = second_j != kBandNoRow ? second_j : first_j;
+        if (r != kBandNoRow) add_quarter(sums4, r, seg, acc, j);
+      }
 #pragma unroll
       for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
     }

@@ -582,9 +582,12 @@ class PanelLayout(_SlotLayout):
         return plan
 
 
-# Sources per band: 32768 neurons x 16 columns x 4 bytes = 2 MB of state, which
-# stays resident in one XCD's 4 MB L2 beside the streamed slots.
-BAND_WIDTH = 32768
+# Sources per band: the most a 16-bit band-local index holds (0xFFFF marks
+# padding), 65535 neurons x 16 columns x 4 bytes = 4 MB of state, an XCD's L2.
+# Measured at N=1M, M=100M, B=16 (ms per tick): 24576 sources 1.10, 32768 1.01,
+# 45056 0.91, 53248 0.88, 65535 0.88; fewer bands mean fewer barriers, groups
+# and flushes, and the gathers stay mostly in L2.
+BAND_WIDTH = 65535
 # Wavefronts per band workgroup (kBandWaves): one workgroup per compute unit.
 BAND_WAVES = 8
 

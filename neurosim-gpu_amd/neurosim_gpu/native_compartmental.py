@@ -232,10 +232,10 @@ def panels_pay_off(topology, batch: int) -> bool:
             and topology.n_edges >= PANEL_AUTO_MIN_SEGMENT * panels * n)
 
 
-# Fewest source bands (of BAND_WIDTH neurons) for which "auto" picks the band
-# kernel: below that the whole 16-column state is a few L2s and the row kernel
-# gathers it from cache as well.
-BAND_AUTO_MIN_BANDS = 4
+# Fewest neurons for which "auto" picks the band kernel (8 MB of 16-column
+# state): below that the whole state is a few L2s and the row kernel gathers it
+# from cache as well.
+BAND_AUTO_MIN_NEURONS = 4 * 32768
 
 
 class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
@@ -255,8 +255,8 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
     (batch a multiple of 16; built once), "rows" streams the CSR as is and
     gathers the state from cache.  "auto" uses panels when the batch allows
     and the graph is dense enough for them (``panels_pay_off``), bands when
-    the batch is a multiple of 16 and the graph spans at least
-    ``BAND_AUTO_MIN_BANDS`` bands, rows otherwise.  ``panel_width`` caps
+    the batch is a multiple of 16 and the graph has at least
+    ``BAND_AUTO_MIN_NEURONS`` neurons, rows otherwise.  ``panel_width`` caps
     the neurons per panel (default: what LDS holds) and ``panel_tiles`` sets
     the workgroups per panel (default: compute units / panels).
     ``panel_pairs`` builds the pair layout (``NS_PANEL_PAIRS``: every row at least
@@ -305,7 +305,7 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
                                             and panels_pay_off(topology, batch))
         use_bands = kernel == "bands" or (
             kernel == "auto" and native and batch > 0 and batch % 16 == 0
-            and topology.n_neurons >= BAND_AUTO_MIN_BANDS * BAND_WIDTH)
+            and topology.n_neurons >= BAND_AUTO_MIN_NEURONS)
         self.kernel = "panels" if use_panels else "bands" if use_bands else "rows"
         if panel_pairs is None:
             panel_pairs = weight_format == "nvfp4"

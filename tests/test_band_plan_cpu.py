@@ -241,9 +241,10 @@ def test_band_plan_does_not_depend_on_thread_count(monkeypatch):
 
 def test_band_padding_at_scale_out_density():
     """About 3.3 edges per (row, band), as at N=1M, M=100M with bands of 32,768
-    sources, and 1954-row blocks of 8 wavefronts (244 rows each, as there):
-    with a second row per lane where one fits the layout holds at most 1.2
-    slots per edge (one row per lane: about 1.48)."""
+    sources (the default 65,535 gives 6.6, with less padding), and 1954-row
+    blocks of 8 wavefronts (244 rows each, as there): with a second row per
+    lane where one fits the layout holds at most 1.2 slots per edge (one row
+    per lane: about 1.48)."""
     rng = np.random.default_rng(5)
     n, m = 100_000, 10_000_000
     dst = np.sort(rng.integers(0, n, m))

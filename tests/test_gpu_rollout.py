@@ -94,7 +94,7 @@ def test_rollout_keeps_its_weights_after_the_runtime_moves_on(gpu, batch):
     recorded (autograd) ticks and a weight change on the runtime rebuild its
     slot copies; the replays must still equal eager ticks on the old weights."""
     print(f"case rollout weight lifetime B={batch}", flush=True)
-    n = 140_000 if batch == 16 else 5000     # bands need >= 4 bands of 32768 sources
+    n = 140_000 if batch == 16 else 5000     # "auto" takes bands from 131,072 neurons
     topology_cpu = random_topology(n, 10 * n, device="cpu", seed=9)
     model, _ = standard_model(n)
     model = model_to(model, gpu)
