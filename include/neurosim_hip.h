@@ -164,17 +164,19 @@ typedef struct ns_panel_plan {
  * every workgroup on that XCD gathers from it.  Destination rows are cut into
  * `n_row_blocks` blocks of `block_rows` rows; one workgroup owns one block
  * (and one 16-column tile), keeps the block's row sums in LDS, walks the
- * bands in order and finally applies the update.  Each of its 8 wavefronts
- * owns a fixed set of the block's rows (dealt by degree, longest first onto
- * the least-loaded wavefront).  Per band, a wavefront's rows with edges in
- * the band are packed into groups of 64 lanes: a group's first rows are the
- * 64 longest segments left (longest first), and the group lasts as many steps
- * as its longest.  A lane takes its first row's segment in CSR order and, in
- * the steps after it, possibly a second row's segment (the longest left that
- * fits, lanes with the most spare steps choosing first).  A group's slots are
+ * bands in order, passing a workgroup barrier after each, and finally applies
+ * the update.  Per band, the block's rows with edges in the band are packed
+ * into groups of 64 lanes: a group's first rows are the 64 longest segments
+ * left (longest first), and the group lasts as many steps as its longest.  A
+ * lane takes its first row's segment in CSR order and, in the steps after it,
+ * possibly a second row's segment (the longest left that fits, lanes with the
+ * most spare steps choosing first).  Each group goes to the one of the 8
+ * wavefronts with the fewest steps in the band so far, so a row's groups of
+ * different bands may lie in different wavefronts.  A group's slots are
  * step-major (slot (step k, lane l) is 64*first_step + 64*k + l).  A group is
- * cut into register blocks of at most `block_steps` steps; the wavefront's
- * blocks are consecutive in `blocks` and their slots contiguous.
+ * cut into register blocks of at most `block_steps` steps; a wavefront's
+ * blocks are consecutive in `blocks`, in band order, and their slots
+ * contiguous.
  * Padding slots have source index 0xFFFF and weight code 0.  Slot k is
  * original CSR edge perm[k] (or padding).  The kernel reads one block record
  * and one register block of slots ahead, so the tables end with a sentinel

@@ -13,17 +13,20 @@
 //    one XCD gather from about one band at a time.
 //  * One 512-lane workgroup (one per compute unit) owns a block of
 //    destination rows and one 16-column tile.  Its row sums live in LDS for
-//    the whole tick, so no partial sums leave the compute unit.  Each
-//    wavefront owns a fixed set of the block's rows, so its LDS updates race
-//    with no other wavefront.  The wavefronts finish each band before any
-//    starts the next (a workgroup barrier per band): a compute unit's eight
+//    the whole tick, so no partial sums leave the compute unit.  A row's
+//    edges in one band lie in one group of one wavefront, so within a band
+//    its LDS updates race with no other wavefront; its groups of different
+//    bands may lie in different wavefronts, which the barrier after each band
+//    orders.  The wavefronts finish each band before any starts the next: a
+//    compute unit's eight
 //    wavefronts then gather from one band, and the workgroups of an XCD, which
 //    start together with equal work, stay within a band or two of each other.
 //    (Two 256-lane workgroups per compute unit drifted apart by up to a dozen
 //    bands, the older one issuing first; L2 then held about half the
 //    gathers, against nearly nine in ten with the barrier.)
-//  * Per band a wavefront's rows are packed 64 lanes at a time, longest
-//    segments first; lane l walks its row's segment.  The four lanes of a
+//  * Per band the block's rows are packed 64 lanes at a time, longest
+//    segments first, and each group goes to the wavefront with the fewest
+//    steps in the band so far; lane l walks its row's segment.  The four lanes of a
 //    quad gather their four rows' 64-byte source rows together, each lane
 //    one 16-byte quarter of each, and each lane keeps the running sums of its
 //    quarter's four columns for the quad's four rows (16 registers).  A lane whose row ends early may take a

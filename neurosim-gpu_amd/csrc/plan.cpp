@@ -468,129 +468,134 @@ struct BandLayout {
 };
 
 
-// Lays out row block [r0, r1): rows dealt to the wavefronts by degree, then
-// per wavefront and band the rows with edges in the band in groups of 64
-// lanes, cut into register blocks.  A lane takes one row's segment (the
-// group's 64 longest left, longest first) and, in the steps after it, a
-// second, shorter row's segment where one fits.
+// Lays out row block [r0, r1).  Per band, the block's rows with edges in the
+// band are packed into groups of 64 lanes, cut into register blocks: a lane
+// takes one row's segment (the group's 64 longest left, longest first) and, in
+// the steps after it, a second, shorter row's segment where one fits.  Each
+// group goes to the wavefront with the fewest steps in that band so far, so
+// the band's work is balanced across the wavefronts; the kernel's barrier
+// after each band lets a row's groups of different bands lie in different
+// wavefronts.  A wavefront's blocks are band-ordered and its slots contiguous.
 void append_band_block(BandLayout& out, const int32_t* rowptr, const int32_t* col,
                        int64_t r0, int64_t r1, int32_t band_width, int32_t n_bands,
                        int32_t block_steps, bool fill) {
   const int64_t nr = r1 - r0;
-  std::vector<int32_t> by_degree(nr);
-  for (int64_t i = 0; i < nr; ++i) by_degree[i] = static_cast<int32_t>(i);
-  auto degree = [&](int64_t i) -> int64_t { return rowptr[r0 + i + 1] - rowptr[r0 + i]; };
-  std::stable_sort(by_degree.begin(), by_degree.end(),
-                   [&](int32_t x, int32_t y) { return degree(x) > degree(y); });
-  std::vector<int64_t> load(kBandWaves, 0);
-  std::vector<std::vector<int32_t>> mine(kBandWaves);
-  for (int32_t i : by_degree) {
-    const int32_t w = static_cast<int32_t>(std::min_element(load.begin(), load.end()) - load.begin());
-    load[w] += degree(i) + 1;
-    mine[w].push_back(i);
+  // Each row's edges grouped by band (stable counting sort): start[i][k].
+  std::vector<int32_t> start(nr * (n_bands + 1), 0);
+  std::vector<int64_t> row_base(nr + 1, 0);
+  for (int64_t i = 0; i < nr; ++i) {
+    const int64_t r = r0 + i;
+    int32_t* st = start.data() + i * (n_bands + 1);
+    for (int64_t e = rowptr[r]; e < rowptr[r + 1]; ++e) ++st[col[e] / band_width + 1];
+    for (int32_t k = 0; k < n_bands; ++k) st[k + 1] += st[k];
+    row_base[i + 1] = row_base[i] + (rowptr[r + 1] - rowptr[r]);
   }
-  for (int32_t w = 0; w < kBandWaves; ++w) {
-    out.wave_blocks.push_back(static_cast<int32_t>(out.blocks.size() / 4));
-    std::vector<int32_t>& rows_w = mine[w];
-    std::sort(rows_w.begin(), rows_w.end());
-    const int64_t nw = static_cast<int64_t>(rows_w.size());
-    // Each row's edges grouped by band (stable counting sort): start[i][k].
-    std::vector<int32_t> start(nw * (n_bands + 1), 0);
-    int64_t total = 0;
-    for (int64_t i = 0; i < nw; ++i) {
-      const int64_t r = r0 + rows_w[i];
-      int32_t* st = start.data() + i * (n_bands + 1);
-      for (int64_t e = rowptr[r]; e < rowptr[r + 1]; ++e) ++st[col[e] / band_width + 1];
-      for (int32_t k = 0; k < n_bands; ++k) st[k + 1] += st[k];
-      total += rowptr[r + 1] - rowptr[r];
+  std::vector<int32_t> order;   // per row, its edges in band order (CSR order within a band)
+  if (fill) {
+    order.assign(row_base[nr], 0);
+    std::vector<int32_t> at(n_bands);
+    for (int64_t i = 0; i < nr; ++i) {
+      const int32_t* st = start.data() + i * (n_bands + 1);
+      for (int32_t k = 0; k < n_bands; ++k) at[k] = st[k];
+      for (int64_t e = rowptr[r0 + i]; e < rowptr[r0 + i + 1]; ++e)
+        order[row_base[i] + at[col[e] / band_width]++] = static_cast<int32_t>(e);
     }
-    std::vector<int32_t> order;   // per row, its edges in band order (CSR order within a band)
-    std::vector<int64_t> row_base(nw + 1, 0);
-    for (int64_t i = 0; i < nw; ++i) row_base[i + 1] = row_base[i] + (rowptr[r0 + rows_w[i] + 1] - rowptr[r0 + rows_w[i]]);
-    if (fill) {
-      order.assign(total, 0);
-      std::vector<int32_t> at(n_bands);
-      for (int64_t i = 0; i < nw; ++i) {
-        const int64_t r = r0 + rows_w[i];
-        const int32_t* st = start.data() + i * (n_bands + 1);
-        for (int32_t k = 0; k < n_bands; ++k) at[k] = st[k];
-        for (int64_t e = rowptr[r]; e < rowptr[r + 1]; ++e)
-          order[row_base[i] + at[col[e] / band_width]++] = static_cast<int32_t>(e);
-      }
-    }
-    // Rows with edges in the band, by segment length (within a length, in row
-    // order): a cursor into each length's list, the length dropped once empty.
-    std::map<int32_t, std::pair<size_t, std::vector<int32_t>>> by_len;
-    auto take = [&](std::map<int32_t, std::pair<size_t, std::vector<int32_t>>>::iterator it) {
-      const int32_t i = it->second.second[it->second.first++];
-      if (it->second.first == it->second.second.size()) by_len.erase(it);
-      return i;
+  }
+  // The wavefronts' parts, concatenated in wavefront order at the end.
+  std::vector<BandLayout> waves(kBandWaves);
+  // Rows with edges in the band, by segment length (within a length, in row
+  // order): a cursor into each length's list, the length dropped once empty.
+  std::map<int32_t, std::pair<size_t, std::vector<int32_t>>> by_len;
+  auto take = [&](std::map<int32_t, std::pair<size_t, std::vector<int32_t>>>::iterator it) {
+    const int32_t i = it->second.second[it->second.first++];
+    if (it->second.first == it->second.second.size()) by_len.erase(it);
+    return i;
+  };
+  for (int32_t k = 0; k < n_bands; ++k) {
+    auto seg_len = [&](int32_t i) -> int32_t {
+      const int32_t* st = start.data() + static_cast<int64_t>(i) * (n_bands + 1);
+      return st[k + 1] - st[k];
     };
-    for (int32_t k = 0; k < n_bands; ++k) {
-      auto seg_len = [&](int32_t i) -> int32_t {
-        const int32_t* st = start.data() + static_cast<int64_t>(i) * (n_bands + 1);
-        return st[k + 1] - st[k];
-      };
-      auto edge_at = [&](int32_t i, int32_t t) -> int32_t {
-        return order[row_base[i] + start[static_cast<int64_t>(i) * (n_bands + 1) + k] + t];
-      };
-      by_len.clear();
-      for (int64_t i = 0; i < nw; ++i)
-        if (seg_len(static_cast<int32_t>(i)) > 0)
-          by_len[seg_len(static_cast<int32_t>(i))].second.push_back(static_cast<int32_t>(i));
-      while (!by_len.empty()) {
-        // A group's first rows: the 64 longest segments left, longest first;
-        // the group lasts as many steps as the first of them.
-        int32_t first[64], second[64];
-        int gn = 0;
-        while (gn < 64 && !by_len.empty()) first[gn++] = take(std::prev(by_len.end()));
-        const int32_t steps = seg_len(first[0]);
-        // Second rows: a lane's steps after its first row's segment take the
-        // longest segment left that fits them, lanes with the most such steps
-        // first.  The lane's word holds the switch step in 8 bits.
-        for (int l = 0; l < 64; ++l) second[l] = -1;
-        for (int l = gn - 1; l >= 0 && !by_len.empty(); --l) {
-          const int32_t len = seg_len(first[l]);
-          if (len > kBandMaxSwitch) break;
-          auto it = by_len.upper_bound(steps - len);
-          if (it == by_len.begin()) break;   // no lane after this one has more room
-          second[l] = take(std::prev(it));
-        }
-        const int32_t group = static_cast<int32_t>(out.n_groups++);
-        if (fill)
-          for (int l = 0; l < 64; ++l) {
-            uint32_t word = kBandNoRow | (kBandNoRow << kBandRowBits);
-            if (l < gn) {
-              word = static_cast<uint32_t>(rows_w[first[l]]);
-              word |= second[l] < 0 ? kBandNoRow << kBandRowBits
-                                    : (static_cast<uint32_t>(rows_w[second[l]]) << kBandRowBits) |
-                                          (static_cast<uint32_t>(seg_len(first[l])) << 24);
-            }
-            out.rows.push_back(word);
+    auto edge_at = [&](int32_t i, int32_t t) -> int32_t {
+      return order[row_base[i] + start[static_cast<int64_t>(i) * (n_bands + 1) + k] + t];
+    };
+    by_len.clear();
+    for (int64_t i = 0; i < nr; ++i)
+      if (seg_len(static_cast<int32_t>(i)) > 0)
+        by_len[seg_len(static_cast<int32_t>(i))].second.push_back(static_cast<int32_t>(i));
+    std::vector<int64_t> band_steps(kBandWaves, 0);
+    while (!by_len.empty()) {
+      // A group's first rows: the 64 longest segments left, longest first;
+      // the group lasts as many steps as the first of them.
+      int32_t first[64], second[64];
+      int gn = 0;
+      while (gn < 64 && !by_len.empty()) first[gn++] = take(std::prev(by_len.end()));
+      const int32_t steps = seg_len(first[0]);
+      // Second rows: a lane's steps after its first row's segment take the
+      // longest segment left that fits them, lanes with the most such steps
+      // first.  The lane's word holds the switch step in 8 bits.
+      for (int l = 0; l < 64; ++l) second[l] = -1;
+      for (int l = gn - 1; l >= 0 && !by_len.empty(); --l) {
+        const int32_t len = seg_len(first[l]);
+        if (len > kBandMaxSwitch) break;
+        auto it = by_len.upper_bound(steps - len);
+        if (it == by_len.begin()) break;   // no lane after this one has more room
+        second[l] = take(std::prev(it));
+      }
+      // The wavefront with the fewest steps in this band takes the group.
+      const int32_t w = static_cast<int32_t>(
+          std::min_element(band_steps.begin(), band_steps.end()) - band_steps.begin());
+      band_steps[w] += steps;
+      BandLayout& part = waves[w];
+      const int32_t group = static_cast<int32_t>(part.n_groups++);
+      if (fill)
+        for (int l = 0; l < 64; ++l) {
+          uint32_t word = kBandNoRow | (kBandNoRow << kBandRowBits);
+          if (l < gn) {
+            word = static_cast<uint32_t>(first[l]);
+            word |= second[l] < 0 ? kBandNoRow << kBandRowBits
+                                  : (static_cast<uint32_t>(second[l]) << kBandRowBits) |
+                                        (static_cast<uint32_t>(seg_len(first[l])) << 24);
           }
-        for (int32_t t0 = 0; t0 < steps; t0 += block_steps) {
-          const int32_t nst = std::min(block_steps, steps - t0);
-          const int32_t last = t0 + block_steps >= steps ? 1 : 0;
-          const int32_t rec[4] = {static_cast<int32_t>(out.n_slots / 64), k,
-                                  nst | (last << 8) | (t0 << 9), group};
-          out.blocks.insert(out.blocks.end(), rec, rec + 4);
-          out.n_slots += int64_t{64} * nst;
-          if (!fill) continue;
-          for (int32_t t = t0; t < t0 + nst; ++t)
-            for (int l = 0; l < 64; ++l) {
-              int32_t edge = -1;
-              if (l < gn) {
-                const int32_t la = seg_len(first[l]);
-                if (t < la) edge = edge_at(first[l], t);
-                else if (second[l] >= 0 && t - la < seg_len(second[l])) edge = edge_at(second[l], t - la);
-              }
-              out.perm.push_back(edge);
-              out.col.push_back(edge < 0 ? uint16_t{0xFFFF}
-                                         : static_cast<uint16_t>(col[edge] - int64_t{k} * band_width));
-            }
+          part.rows.push_back(word);
         }
+      for (int32_t t0 = 0; t0 < steps; t0 += block_steps) {
+        const int32_t nst = std::min(block_steps, steps - t0);
+        const int32_t last = t0 + block_steps >= steps ? 1 : 0;
+        const int32_t rec[4] = {static_cast<int32_t>(part.n_slots / 64), k,
+                                nst | (last << 8) | (t0 << 9), group};
+        part.blocks.insert(part.blocks.end(), rec, rec + 4);
+        part.n_slots += int64_t{64} * nst;
+        if (!fill) continue;
+        for (int32_t t = t0; t < t0 + nst; ++t)
+          for (int l = 0; l < 64; ++l) {
+            int32_t edge = -1;
+            if (l < gn) {
+              const int32_t la = seg_len(first[l]);
+              if (t < la) edge = edge_at(first[l], t);
+              else if (second[l] >= 0 && t - la < seg_len(second[l])) edge = edge_at(second[l], t - la);
+            }
+            part.perm.push_back(edge);
+            part.col.push_back(edge < 0 ? uint16_t{0xFFFF}
+                                        : static_cast<uint16_t>(col[edge] - int64_t{k} * band_width));
+          }
       }
     }
+  }
+  // Concatenate the wavefronts' parts, shifting their step and group numbers.
+  for (const BandLayout& part : waves) {
+    out.wave_blocks.push_back(static_cast<int32_t>(out.blocks.size() / 4));
+    for (size_t q = 0; q < part.blocks.size(); q += 4) {
+      const int32_t rec[4] = {static_cast<int32_t>(part.blocks[q] + out.n_slots / 64),
+                              part.blocks[q + 1], part.blocks[q + 2],
+                              static_cast<int32_t>(part.blocks[q + 3] + out.n_groups)};
+      out.blocks.insert(out.blocks.end(), rec, rec + 4);
+    }
+    out.rows.insert(out.rows.end(), part.rows.begin(), part.rows.end());
+    out.perm.insert(out.perm.end(), part.perm.begin(), part.perm.end());
+    out.col.insert(out.col.end(), part.col.begin(), part.col.end());
+    out.n_slots += part.n_slots;
+    out.n_groups += part.n_groups;
   }
 }
 

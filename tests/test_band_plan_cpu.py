@@ -7,10 +7,12 @@ slots contiguous, each record carrying its first step within the group; a
 group's lane takes its first row's segment of the band in CSR order and, from
 its switch step on, possibly a second row's; the group lasts as long as its
 longest first segment, and its last block is marked; each row of a block
-belongs to one wavefront and meets each band at most once; the tables end with
-the sentinel block, the sentinel group and the tail padding.  The emulation
-follows the kernel's summation order (per row: bands in order, within a band
-the segment's edges one at a time) and must reproduce the CSR product.
+meets each band in one group (of one wavefront) at most; the wavefronts' steps
+in a band differ by no more than one group's; the tables end with the sentinel
+block, the sentinel group and the tail padding.  The emulation follows the
+kernel's summation order (per row: bands in order, the workgroup passing a
+barrier after each; within a band the segment's edges one at a time) and must
+reproduce the CSR product.
 """
 
 from __future__ import annotations
@@ -95,11 +97,12 @@ def test_band_layout_invariants(n, m, seed, hubs, width, rows, steps):
     for e in range(edges):
         segments.setdefault((int(row_of_edge[e]), int(col[e]) // width), []).append(e)
     step = 0
-    owner = {}
     for q in range(n_row_blocks):
         r0 = q * rows
+        seen_bands = {}
+        band_steps = np.zeros((n_bands, WAVES), np.int64)
+        group_steps = np.zeros(n_bands, np.int64)
         for w in range(WAVES):
-            seen_bands = {}
             prev_band = -1
             b = wave_blocks[WAVES * q + w]
             while b < wave_blocks[WAVES * q + w + 1]:
@@ -123,7 +126,6 @@ def test_band_layout_invariants(n, m, seed, hubs, width, rows, steps):
                 assert len(set(members)) == len(members)
                 for r in members:
                     assert 0 <= r < min(rows, n - r0)
-                    assert owner.setdefault(r0 + r, (q, w)) == (q, w)       # one wavefront per row
                     assert (r0 + r, band) not in seen_bands                 # one group per band
                     seen_bands[(r0 + r, band)] = True
                     assert len(seg(r)) > 0
@@ -156,6 +158,10 @@ def test_band_layout_invariants(n, m, seed, hubs, width, rows, steps):
                 for first, second, switch in lanes:
                     if first != NO_ROW:
                         assert len(seg(first)) + (len(seg(second)) if second != NO_ROW else 0) <= t
+                band_steps[band, w] += t
+                group_steps[band] = max(group_steps[band], t)
+        # each group went to the wavefront with the fewest steps in its band
+        assert np.all(band_steps.max(axis=1) - band_steps.min(axis=1) <= group_steps)
     assert 64 * step + TAIL == plan.n_slots
 
 
@@ -171,10 +177,12 @@ def test_band_emulation_matches_csr_product(n, m, seed, hubs, width, rows, steps
     sums = np.zeros((n, 16), np.float32)
     for q in range(plan.n_row_blocks):
         r0 = q * rows
-        for w in range(WAVES):
+        for band_now, w in ((k, w) for k in range(plan.n_bands) for w in range(WAVES)):
             acc = np.zeros((64, 16), np.float32)
             for b in range(wave_blocks[WAVES * q + w], wave_blocks[WAVES * q + w + 1]):
                 start, band, info, group = blocks[b]
+                if band != band_now:
+                    continue
                 lanes = [lane_rows(word) for word in group_rows[group]]
                 for k in range(info & 0xFF):
                     slots = np.arange(64) + 64 * (start + k)
@@ -242,9 +250,10 @@ def test_band_plan_does_not_depend_on_thread_count(monkeypatch):
 def test_band_padding_at_scale_out_density():
     """About 3.3 edges per (row, band), as at N=1M, M=100M with bands of 32,768
     sources (the default 65,535 gives 6.6, with less padding), and 1954-row
-    blocks of 8 wavefronts (244 rows each, as there): with a second row per
-    lane where one fits the layout holds at most 1.2 slots per edge (one row
-    per lane: about 1.48)."""
+    blocks of 8 wavefronts, as there: with a block's rows pooled per band and
+    a second row per lane where one fits, the layout holds at most 1.05 slots
+    per edge (rows dealt to the wavefronts first: 1.13; one row per lane:
+    about 1.48)."""
     rng = np.random.default_rng(5)
     n, m = 100_000, 10_000_000
     dst = np.sort(rng.integers(0, n, m))
@@ -255,4 +264,4 @@ def test_band_padding_at_scale_out_density():
                            3277, 1954, 4)[0]
     ratio = (plan.n_slots - TAIL) / m
     print(f"slots per edge {ratio:.3f}")
-    assert ratio <= 1.2
+    assert ratio <= 1.05
