@@ -1,5 +1,6 @@
 // Fused dendritic matrix tick over source bands, for wide batches (16 state
-// columns per workgroup) whose state is larger than an XCD's L2.
+// columns per workgroup, or 8 when the batch is an odd multiple of 8) whose
+// state is larger than an XCD's L2.
 //
 // Semantics follow the reference's fused kernel (csrc/compartmental.cu:121-140
 // and :72-90): j = W @ s over the batch columns, then the three-state update.
@@ -12,13 +13,13 @@
 //    workgroup walks the bands in the same order: the workgroups resident on
 //    one XCD gather from about one band at a time.
 //  * One 512-lane workgroup (one per compute unit) owns a block of
-//    destination rows and one 16-column tile.  Its row sums live in LDS for
-//    the whole tick, so no partial sums leave the compute unit.  A row's
-//    edges in one band lie in one group of one wavefront, so within a band
-//    its LDS updates race with no other wavefront; its groups of different
-//    bands may lie in different wavefronts, which the barrier after each band
-//    orders.  The wavefronts finish each band before any starts the next: a
-//    compute unit's eight
+//    destination rows and one tile of C = 16 (or 8) columns.  Its row sums
+//    live in LDS for the whole tick, so no partial sums leave the compute
+//    unit.  A row's edges in one band lie in one group of one wavefront, so
+//    within a band its LDS updates race with no other wavefront; its groups
+//    of different bands may lie in different wavefronts, which the barrier
+//    after each band orders.  The wavefronts finish each band before any
+//    starts the next: a compute unit's eight
 //    wavefronts then gather from one band, and the workgroups of an XCD, which
 //    start together with equal work, stay within a band or two of each other.
 //    (Two 256-lane workgroups per compute unit drifted apart by up to a dozen
@@ -26,10 +27,12 @@
 //    gathers, against nearly nine in ten with the barrier.)
 //  * Per band the block's rows are packed 64 lanes at a time, longest
 //    segments first, and each group goes to the wavefront with the fewest
-//    steps in the band so far; lane l walks its row's segment.  The four lanes of a
-//    quad gather their four rows' 64-byte source rows together, each lane
-//    one 16-byte quarter of each, and each lane keeps the running sums of its
-//    quarter's four columns for the quad's four rows (16 registers).  A lane whose row ends early may take a
+//    steps in the band so far; lane l walks its row's segment.  The four lanes
+//    of a quad gather their four rows' 64-byte source rows together, each
+//    lane one 16-byte quarter of each, and each lane keeps the running sums
+//    of its quarter's four columns for the quad's four rows (16 registers);
+//    with 8 columns a pair of lanes does the same for its two rows' 32-byte
+//    source rows.  A lane whose row ends early may take a
 //    second, shorter row in the group's remaining steps: at the switch step it
 //    adds its sums to the first row's LDS sums and starts again from zero.
 //    At the group's end the lane adds them to its (last) row's LDS sums.
@@ -112,13 +115,14 @@ __device__ __forceinline__ void load_band_slots(const BandArgs& A, const BandBlo
 }
 
 // Adds four running sums (acc[4j .. 4j+3]: columns 4*seg .. 4*seg+3 of one
-// row) to that row's LDS sums.
-__device__ __forceinline__ void add_quarter(v4f* sums4, uint32_t row, int seg, float (&acc)[16],
-                                            int j) {
-  v4f t = sums4[row * 4 + seg];
+// row) to that row's LDS sums; a row holds G groups of four columns.
+template <int G>
+__device__ __forceinline__ void add_piece(v4f* sums4, uint32_t row, int seg,
+                                          float (&acc)[4 * G], int j) {
+  v4f t = sums4[row * G + seg];
   t.x += acc[4 * j + 0]; t.y += acc[4 * j + 1];
   t.z += acc[4 * j + 2]; t.w += acc[4 * j + 3];
-  sums4[row * 4 + seg] = t;
+  sums4[row * G + seg] = t;
 }
 
 // Source of padding slots and of steps past a block's end: 16 zeros.
@@ -141,40 +145,48 @@ __device__ __forceinline__ float decode_band(const BandSlot& x, int lane, float 
   }
 }
 
-// Value `v` of lane J of each group of four lanes (a quad), for every lane of
-// the quad: a DPP quad permutation.
-template <int J>
-__device__ __forceinline__ uint32_t from_quad_lane(uint32_t v) {
-  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v),
-                                                        J | (J << 2) | (J << 4) | (J << 6),
-                                                        0xF, 0xF, false));
+// Value `v` of lane J of each group of G lanes (G = 4: a quad; G = 2: a pair
+// within a quad), for every lane of the group: a DPP quad permutation.
+template <int G, int J>
+__device__ __forceinline__ uint32_t from_group_lane(uint32_t v) {
+  constexpr int sel = G == 4 ? J | (J << 2) | (J << 4) | (J << 6)
+                             : J | (J << 2) | ((2 + J) << 4) | ((2 + J) << 6);
+  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), sel, 0xF, 0xF, false));
 }
-__device__ __forceinline__ void quad_values(uint32_t v, uint32_t (&out)[4]) {
-  out[0] = from_quad_lane<0>(v); out[1] = from_quad_lane<1>(v);
-  out[2] = from_quad_lane<2>(v); out[3] = from_quad_lane<3>(v);
+template <int G>
+__device__ __forceinline__ void group_values(uint32_t v, uint32_t (&out)[G]) {
+  out[0] = from_group_lane<G, 0>(v);
+  out[1] = from_group_lane<G, 1>(v);
+  if constexpr (G == 4) {
+    out[2] = from_group_lane<G, 2>(v);
+    out[3] = from_group_lane<G, 3>(v);
+  }
 }
 
-template <int FMT, int D>
+// C: state columns per workgroup, 16 (a 64-byte source row, gathered by the
+// four lanes of a quad) or 8 (a 32-byte row, gathered by a pair of lanes).
+template <int FMT, int D, int C>
 __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) {
-  extern __shared__ __attribute__((aligned(16))) float sums[];   // [block_rows][16]
+  constexpr int G = C / 4;   // lanes that gather a row together, 16 bytes each
+  extern __shared__ __attribute__((aligned(16))) float sums[];   // [block_rows][C]
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * A.block_rows;
   const int nrows = static_cast<int>(min<int64_t>(A.block_rows, A.N - r0));
-  const int64_t b0 = int64_t{16} * blockIdx.y;
+  const int64_t b0 = int64_t{C} * blockIdx.y;
   const float gscale = (FMT == NS_WEIGHT_E4M3 || FMT == NS_WEIGHT_NVFP4) ? *A.gscale : 1.0f;
   v4f* const sums4 = reinterpret_cast<v4f*>(sums);
-  for (int i = tid; i < nrows * 4; i += kBandWaves * 64) sums4[i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int i = tid; i < nrows * G; i += kBandWaves * 64) sums4[i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   __syncthreads();
 
   const int32_t* wb = A.wave_blocks + static_cast<int64_t>(blockIdx.x) * kBandWaves + wave;
   const int32_t b_begin = wb[0], b_end = wb[1];
   const float* const srow = A.s_rows + b0;
   const uint64_t zero_row = reinterpret_cast<uint64_t>(&kBandZeroRow[0]);
-  float acc[16];
+  float acc[4 * G];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+  for (int j = 0; j < 4 * G; ++j) acc[j] = 0.0f;
 
   BandBlock cur{0, 0, 0, 0, 0};
   BandSlot here[D];
@@ -187,26 +199,26 @@ __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) 
   int32_t b = b_begin;
   for (int32_t band = 0; band < A.n_bands; ++band) {
   for (; b < b_end && cur.band == band; ++b) {
-    // Gathers of this block: each slot's whole 16-column source row.
+    // Gathers of this block: each slot's whole C-column source row.
     const int64_t base = static_cast<int64_t>(cur.band) * A.band_width;
-    // The four lanes of a quad gather together: at step k, instruction j loads
-    // quarter `seg` (16 bytes) of the source row of the quad's lane j, so one
-    // load instruction touches 16 rows, each in one 64-byte piece, rather than
-    // 64 rows as when each lane loads its own row in four instructions: a
-    // quarter of the cache-line accesses.  Lane l then accumulates columns
-    // 4*seg .. 4*seg+3 of the rows of its quad's four lanes (acc[4j..4j+3] for
+    // The G lanes of a group gather together: at step k, instruction j loads
+    // piece `seg` (16 bytes) of the source row of the group's lane j, so one
+    // load instruction touches 64/G rows, each in one 4G-float piece, rather
+    // than 64 rows as when each lane loads its own row in G instructions: 1/G
+    // of the cache-line accesses.  Lane l then accumulates columns
+    // 4*seg .. 4*seg+3 of the rows of its group's G lanes (acc[4j..4j+3] for
     // lane j's row), in step order, and adds them to those rows' LDS sums at
     // each row's switch or end.  A padding slot (or a step past the block's
     // end) reads the zero row: the two global addresses are blended by a mask,
     // so the choice stays a select and the loads stay global loads.
-    const int seg = lane & 3;
-    v4f g[D][4];
+    const int seg = lane & (G - 1);
+    v4f g[D][G];
 #pragma unroll
     for (int k = 0; k < D; ++k) {
-      uint32_t cq[4];
-      quad_values(here[k].c, cq);
+      uint32_t cq[G];
+      group_values<G>(here[k].c, cq);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < G; ++j) {
         const bool real = k < cur.steps && cq[j] != kBandPad;
         const uint64_t mask = 0ull - static_cast<uint64_t>(real);
         const uint64_t at = reinterpret_cast<uint64_t>(srow + (base + cq[j]) * A.s_stride + 4 * seg);
@@ -221,17 +233,17 @@ __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) 
     BandSlot ahead[D];
     uint32_t row_ahead;
     load_band_slots<FMT, D>(A, nxt, lane, ahead, row_ahead);
-    // The quad's lane words: lane j's rows and the step where it switches.
-    uint32_t rowq[4];
-    quad_values(row, rowq);
+    // The group's lane words: lane j's rows and the step where it switches.
+    uint32_t rowq[G];
+    group_values<G>(row, rowq);
 #pragma unroll
     for (int k = 0; k < D; ++k) {
       if (k < cur.steps) {
         const float w = decode_band<FMT>(here[k], lane, gscale);
-        uint32_t wq[4];
-        quad_values(__builtin_bit_cast(uint32_t, w), wq);
+        uint32_t wq[G];
+        group_values<G>(__builtin_bit_cast(uint32_t, w), wq);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < G; ++j) {
           const float wj = __builtin_bit_cast(float, wq[j]);
           acc[4 * j + 0] += wj * g[k][j].x;
           acc[4 * j + 1] += wj * g[k][j].y;
@@ -239,10 +251,10 @@ __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) 
           acc[4 * j + 3] += wj * g[k][j].w;
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < G; ++j) {
           const int turn_j = static_cast<int>(rowq[j] >> 24) - cur.t0 - 1;
           if (k == turn_j) {   // lane j moves on to its second row
-            add_quarter(sums4, rowq[j] & kBandNoRow, seg, acc, j);
+            add_piece<G>(sums4, rowq[j] & kBandNoRow, seg, acc, j);
             acc[4 * j + 0] = acc[4 * j + 1] = acc[4 * j + 2] = acc[4 * j + 3] = 0.0f;
           }
         }
@@ -250,14 +262,14 @@ __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) 
     }
     if (cur.last) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < G; ++j) {
         const uint32_t first_j = rowq[j] & kBandNoRow;
         const uint32_t second_j = (rowq[j] >> kBandRowBits) & kBandNoRow;
         const uint32_t r = second_j != kBandNoRow ? second_j : first_j;
-        if (r != kBandNoRow) add_quarter(sums4, r, seg, acc, j);
+        if (r != kBandNoRow) add_piece<G>(sums4, r, seg, acc, j);
       }
 #pragma unroll
-      for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+      for (int j = 0; j < 4 * G; ++j) acc[j] = 0.0f;
     }
     cur = nxt;
     row = row_ahead;
@@ -268,9 +280,9 @@ __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) 
   }
 
   // The update: consecutive lanes take consecutive columns of a row.
-  for (int i = tid; i < nrows * 16; i += kBandWaves * 64) {
-    const int64_t n = r0 + (i >> 4);
-    const int64_t b = b0 + (i & 15);
+  for (int i = tid; i < nrows * C; i += kBandWaves * 64) {
+    const int64_t n = r0 + i / C;
+    const int64_t b = b0 + i % C;
     const NextState x = advance_one(A.p, n, sums[i], A.s.get(b, n), A.d.get(b, n),
                                     A.a.get(b, n), A.u.get(b, n), A.v.get(b, n));
     A.os.put(b, n, x.soma);
@@ -280,27 +292,33 @@ __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) 
   }
 }
 
-template <int D>
+template <int D, int C>
 hipError_t launch_bands(const BandArgs& A, int fmt, int n_row_blocks, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(n_row_blocks), static_cast<unsigned>(A.B / 16));
+  const dim3 grid(static_cast<unsigned>(n_row_blocks), static_cast<unsigned>(A.B / C));
   const dim3 block(kBandWaves * 64);
-  const size_t lds = static_cast<size_t>(A.block_rows) * 16 * sizeof(float);
+  const size_t lds = static_cast<size_t>(A.block_rows) * C * sizeof(float);
   switch (fmt) {
-    case NS_WEIGHT_F32: band_tick_kernel<NS_WEIGHT_F32, D><<<grid, block, lds, stream>>>(A); break;
-    case NS_WEIGHT_F16: band_tick_kernel<NS_WEIGHT_F16, D><<<grid, block, lds, stream>>>(A); break;
-    case NS_WEIGHT_E4M3: band_tick_kernel<NS_WEIGHT_E4M3, D><<<grid, block, lds, stream>>>(A); break;
-    default: band_tick_kernel<NS_WEIGHT_NVFP4, D><<<grid, block, lds, stream>>>(A); break;
+    case NS_WEIGHT_F32: band_tick_kernel<NS_WEIGHT_F32, D, C><<<grid, block, lds, stream>>>(A); break;
+    case NS_WEIGHT_F16: band_tick_kernel<NS_WEIGHT_F16, D, C><<<grid, block, lds, stream>>>(A); break;
+    case NS_WEIGHT_E4M3: band_tick_kernel<NS_WEIGHT_E4M3, D, C><<<grid, block, lds, stream>>>(A); break;
+    default: band_tick_kernel<NS_WEIGHT_NVFP4, D, C><<<grid, block, lds, stream>>>(A); break;
   }
   return hipGetLastError();
 }
 
 template <int D>
+hipError_t launch_bands(const BandArgs& A, int fmt, int n_row_blocks, hipStream_t stream) {
+  return A.B % 16 == 0 ? launch_bands<D, 16>(A, fmt, n_row_blocks, stream)
+                       : launch_bands<D, 8>(A, fmt, n_row_blocks, stream);
+}
+
+template <int D, int C>
 hipError_t allow_band_lds() {
-  const int bytes = kBandMaxBlockRows * 16 * static_cast<int>(sizeof(float));
-  const void* kernels[4] = {reinterpret_cast<const void*>(&band_tick_kernel<NS_WEIGHT_F32, D>),
-                            reinterpret_cast<const void*>(&band_tick_kernel<NS_WEIGHT_F16, D>),
-                            reinterpret_cast<const void*>(&band_tick_kernel<NS_WEIGHT_E4M3, D>),
-                            reinterpret_cast<const void*>(&band_tick_kernel<NS_WEIGHT_NVFP4, D>)};
+  const int bytes = kBandMaxBlockRows * C * static_cast<int>(sizeof(float));
+  const void* kernels[4] = {reinterpret_cast<const void*>(&band_tick_kernel<NS_WEIGHT_F32, D, C>),
+                            reinterpret_cast<const void*>(&band_tick_kernel<NS_WEIGHT_F16, D, C>),
+                            reinterpret_cast<const void*>(&band_tick_kernel<NS_WEIGHT_E4M3, D, C>),
+                            reinterpret_cast<const void*>(&band_tick_kernel<NS_WEIGHT_NVFP4, D, C>)};
   for (const void* k : kernels) {
     const hipError_t err =
         hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
@@ -309,12 +327,18 @@ hipError_t allow_band_lds() {
   return hipSuccess;
 }
 
+template <int D>
+hipError_t allow_band_lds() {
+  const hipError_t e = allow_band_lds<D, 16>();
+  return e != hipSuccess ? e : allow_band_lds<D, 8>();
+}
+
 int check_step_head(const ns_step_args& a);
 int check_step_planes(const ns_step_args& a);
 
 int band_step(const ns_step_args& a, const ns_band_plan& pl, hipStream_t stream) {
-  if (a.batch % 16) return fail("the band kernel needs a batch that is a multiple of 16, not %lld",
-                                (long long)a.batch);
+  if (a.batch % 8) return fail("the band kernel needs a batch that is a multiple of 8, not %lld",
+                               (long long)a.batch);
   if (a.state.stride_b != 1 || a.state.stride_n < a.batch || a.state.stride_n % 4 ||
       reinterpret_cast<uintptr_t>(a.state.data) % 16)
     return fail("the band kernel needs a neuron-major state with 16-byte aligned rows");
@@ -340,7 +364,7 @@ int band_step(const ns_step_args& a, const ns_band_plan& pl, hipStream_t stream)
   if (reinterpret_cast<uintptr_t>(pl.col) % 2 || reinterpret_cast<uintptr_t>(pl.weight) % need ||
       reinterpret_cast<uintptr_t>(pl.rows) % 4)
     return fail("band arrays are misaligned");
-  if (static_cast<int64_t>(pl.n_row_blocks) > 0x7FFFFFFF || a.batch / 16 > 65535)
+  if (static_cast<int64_t>(pl.n_row_blocks) > 0x7FFFFFFF || a.batch / 8 > 65535)
     return fail("band grid too large");
 
   BandArgs A{};

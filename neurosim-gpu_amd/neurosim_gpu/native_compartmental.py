@@ -232,10 +232,24 @@ def panels_pay_off(topology, batch: int) -> bool:
             and topology.n_edges >= PANEL_AUTO_MIN_SEGMENT * panels * n)
 
 
-# Fewest neurons for which "auto" picks the band kernel (8 MB of 16-column
-# state): below that the whole state is a few L2s and the row kernel gathers it
-# from cache as well.
-BAND_AUTO_MIN_NEURONS = 4 * 32768
+# Fewest bytes of one workgroup's column tile of the state (16 columns when the
+# batch is a multiple of 16, else 8) for which "auto" picks the band kernel, one
+# XCD's L2.  Measured, us per tick (rows / bands), 20 edges per neuron, fp32:
+# B=8: N=50k (1.6 MB) 14.7 / 17.2, N=131k (4 MB) 36.5 / 29.5, N=262k 75.0 / 46.3,
+# N=524k 173.7 / 89.0; B=16: N=65k (4 MB) 46.4 / 29.0, N=131k 81.9 / 41.4,
+# N=262k 152.8 / 66.5; N=1M, M=100M, fp8: B=8 1603 / 658, B=16 1933 / 855.
+BAND_AUTO_MIN_TILE_BYTES = 4 << 20
+
+
+def band_tile_columns(batch: int) -> int:
+    """State columns per band workgroup: 16, or 8 for an odd multiple of 8."""
+    return 16 if batch % 16 == 0 else 8
+
+
+def bands_pay_off(n_neurons: int, batch: int) -> bool:
+    """Whether "auto" picks the band kernel for this state size."""
+    return (batch > 0 and batch % 8 == 0
+            and n_neurons * band_tile_columns(batch) * 4 >= BAND_AUTO_MIN_TILE_BYTES)
 
 
 class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
@@ -252,11 +266,12 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
     state in LDS and streams a panel-sorted copy of the graph (batch 1 or 2;
     built once, at construction), "bands" streams a band-sorted copy of the
     graph whose gathers stay within an L2-sized band of sources at a time
-    (batch a multiple of 16; built once), "rows" streams the CSR as is and
+    (batch a multiple of 8; built once), "rows" streams the CSR as is and
     gathers the state from cache.  "auto" uses panels when the batch allows
     and the graph is dense enough for them (``panels_pay_off``), bands when
-    the batch is a multiple of 16 and the graph has at least
-    ``BAND_AUTO_MIN_NEURONS`` neurons, rows otherwise.  ``panel_width`` caps
+    the batch is a multiple of 8 and a workgroup's column tile of the state
+    (16 or 8 columns) is at least ``BAND_AUTO_MIN_TILE_BYTES`` (``bands_pay_off``),
+    rows otherwise.  ``panel_width`` caps
     the neurons per panel (default: what LDS holds) and ``panel_tiles`` sets
     the workgroups per panel (default: compute units / panels).
     ``panel_pairs`` builds the pair layout (``NS_PANEL_PAIRS``: every row at least
@@ -298,14 +313,13 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         native = isinstance(self.extension, NativeExtension)
         if kernel == "panels" and (batch not in (1, 2) or not native):
             raise ValueError("the panel kernel needs batch 1 or 2 and the native extension")
-        if kernel == "bands" and (batch % 16 or batch == 0 or not native):
-            raise ValueError("the band kernel needs a batch that is a multiple of 16 and the "
+        if kernel == "bands" and (batch % 8 or batch == 0 or not native):
+            raise ValueError("the band kernel needs a batch that is a multiple of 8 and the "
                              "native extension")
         use_panels = kernel == "panels" or (kernel == "auto" and batch in (1, 2) and native
                                             and panels_pay_off(topology, batch))
         use_bands = kernel == "bands" or (
-            kernel == "auto" and native and batch > 0 and batch % 16 == 0
-            and topology.n_neurons >= BAND_AUTO_MIN_NEURONS)
+            kernel == "auto" and native and bands_pay_off(topology.n_neurons, batch))
         self.kernel = "panels" if use_panels else "bands" if use_bands else "rows"
         if panel_pairs is None:
             panel_pairs = weight_format == "nvfp4"

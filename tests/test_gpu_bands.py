@@ -1,4 +1,5 @@
-"""The source-band tick (batch a multiple of 16) on the MI355X.
+"""The source-band tick (batch a multiple of 8: workgroups of 16 state columns
+when the batch is a multiple of 16, else of 8) on the MI355X.
 
 Small band widths and row blocks force many bands, many row blocks and short
 register blocks on small graphs; hub rows give segments of hundreds to
@@ -49,7 +50,7 @@ def band_runtime(topology, model, state, **kwargs):
     return native
 
 
-@pytest.mark.parametrize("batch", [16, 32])
+@pytest.mark.parametrize("batch", [8, 16, 24, 32])
 @pytest.mark.parametrize("width,rows,steps", [(None, None, 8), (1000, 256, 8), (512, 64, 4),
                                               (4096, 2496, 8), (777, 1001, 4)])
 def test_bands_match_oracle(gpu, batch, width, rows, steps):
@@ -70,26 +71,28 @@ def test_bands_match_oracle(gpu, batch, width, rows, steps):
     assert worst <= 1e-5
 
 
-def test_bands_and_rows_agree_and_repeat(gpu):
+@pytest.mark.parametrize("batch", [8, 16])
+def test_bands_and_rows_agree_and_repeat(gpu, batch):
     case = make_case(20_000, 400_000, 5, gpu)
     runs = {}
     for kernel in ("bands", "rows", "bands"):
         native = NativeDendriticMatrixRuntime(case.topology, case.model,
-                                              torch.zeros(16, 20_000, device=gpu), kernel=kernel,
-                                              band_width=2048, band_rows=300)
+                                              torch.zeros(batch, 20_000, device=gpu),
+                                              kernel=kernel, band_width=2048, band_rows=300)
         for _ in range(25):
-            native.step(column_drive(16).to(gpu), dendritic_drive=0.1)
+            native.step(column_drive(batch).to(gpu), dendritic_drive=0.1)
         if kernel in runs:
             assert torch.equal(native.state, runs[kernel].state)      # bitwise repeatable
         runs[kernel] = native
     assert errors(runs["bands"], runs["rows"]) <= 2e-6
 
 
+@pytest.mark.parametrize("batch", [8, 16])
 @pytest.mark.parametrize("fmt", ["fp16", "fp8", "nvfp4"])
-def test_band_formats_equal_decoded_fp32(gpu, fmt):
+def test_band_formats_equal_decoded_fp32(gpu, fmt, batch):
     graph, topology, model, params = hub_case(gpu, n=6000, seed=9)
     kwargs = {"weight_dtype": torch.float16} if fmt == "fp16" else {"weight_format": fmt}
-    native = band_runtime(topology, model, torch.zeros(16, 6000, device=gpu), band_width=1024,
+    native = band_runtime(topology, model, torch.zeros(batch, 6000, device=gpu), band_width=1024,
                           band_rows=500, **kwargs)
     native._weights()
     if fmt == "fp16":
@@ -102,10 +105,10 @@ def test_band_formats_equal_decoded_fp32(gpu, fmt):
     decoded = SparseTopology.from_edges(
         6000, topology.src, topology.dst,
         torch.from_numpy(decoded_host).to(gpu)[topology.out_weight_index.long()])
-    reference = band_runtime(decoded, model, torch.zeros(16, 6000, device=gpu), band_width=1024,
-                             band_rows=500)
-    oracle = ort.MatrixOracle(graph, params, torch.zeros(16, 6000), in_weight=decoded_host)
-    drive = column_drive(16)
+    reference = band_runtime(decoded, model, torch.zeros(batch, 6000, device=gpu),
+                             band_width=1024, band_rows=500)
+    oracle = ort.MatrixOracle(graph, params, torch.zeros(batch, 6000), in_weight=decoded_host)
+    drive = column_drive(batch)
     for _ in range(10):
         native.step(drive.to(gpu), dendritic_drive=0.1)
         reference.step(drive.to(gpu), dendritic_drive=0.1)
@@ -135,12 +138,13 @@ def test_band_state_layouts_drives_and_weight_refresh(gpu):
     assert errors(native, oracle) <= 1e-5
 
 
-def test_band_rollout_graph_equals_eager_ticks(gpu):
+@pytest.mark.parametrize("batch", [8, 16])
+def test_band_rollout_graph_equals_eager_ticks(gpu, batch):
     case = make_case(5000, 100_000, 6, gpu)
-    drive = column_drive(16).to(gpu)
-    eager = band_runtime(case.topology, case.model, torch.zeros(16, 5000, device=gpu),
+    drive = column_drive(batch).to(gpu)
+    eager = band_runtime(case.topology, case.model, torch.zeros(batch, 5000, device=gpu),
                          band_width=1500, band_rows=200, weight_format="fp8")
-    rolled = band_runtime(case.topology, case.model, torch.zeros(16, 5000, device=gpu),
+    rolled = band_runtime(case.topology, case.model, torch.zeros(batch, 5000, device=gpu),
                           band_width=1500, band_rows=200, weight_format="fp8")
     rollout = MatrixRollout(rolled, 8, drive=drive, dendritic_drive=0.1)
     for replay in range(3):
