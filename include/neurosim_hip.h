@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 13
+#define NS_ABI_VERSION 14
 
 /* Return codes. */
 #define NS_OK 0
@@ -170,9 +170,9 @@ typedef struct ns_panel_plan {
  * left (longest first), and the group lasts as many steps as its longest.  A
  * lane takes its first row's segment in CSR order and, in the steps after it,
  * possibly a second row's segment (the longest left that fits, lanes with the
- * most spare steps choosing first).  Each group goes to the one of the 8
- * wavefronts with the fewest steps in the band so far, so a row's groups of
- * different bands may lie in different wavefronts.  A group's slots are
+ * most spare steps choosing first).  Each group goes to the one of the
+ * NS_BAND_WAVES wavefronts with the fewest steps in the band so far, so a
+ * row's groups of different bands may lie in different wavefronts.  A group's slots are
  * step-major (slot (step k, lane l) is 64*first_step + 64*k + l).  A group is
  * cut into register blocks of at most `block_steps` steps; a wavefront's
  * blocks are consecutive in `blocks`, in band order, and their slots
@@ -182,6 +182,10 @@ typedef struct ns_panel_plan {
  * and one register block of slots ahead, so the tables end with a sentinel
  * block record (whose group is a last group of 64 padding rows) and 8*64
  * padding slots. */
+/* Wavefronts per band workgroup: `wave_blocks` holds NS_BAND_WAVES entries per
+ * row block (plus one). */
+#define NS_BAND_WAVES 16
+
 typedef struct ns_band_plan {
   int32_t band_width;          /* source neurons per band, at most 65535 */
   int32_t n_bands;
@@ -192,8 +196,9 @@ typedef struct ns_band_plan {
   int32_t block_steps;         /* steps per register block the plan was cut for */
   int32_t reserved;
   int64_t n_slots;
-  const int32_t* wave_blocks;  /* [n_row_blocks*8 + 1]: wavefront w of row block q owns
-                                  blocks wave_blocks[8q+w] .. wave_blocks[8q+w+1]-1 */
+  const int32_t* wave_blocks;  /* [n_row_blocks*NS_BAND_WAVES + 1]: wavefront w of row
+                                  block q owns blocks wave_blocks[NS_BAND_WAVES*q + w] ..
+                                  wave_blocks[NS_BAND_WAVES*q + w + 1] - 1 */
   const int32_t* blocks;       /* [n_blocks+1][4]: first step, band,
                                   steps | last << 8 | step in group << 9 (last: the block
                                   ends its group), group */
@@ -441,7 +446,7 @@ int ns_dendritic_step(const ns_step_args* args, void* stream);
  * (1..ns_band_max_block_rows()), register blocks of at most `block_steps`
  * steps (1..8).  Call once with all output pointers NULL to get the sizes in
  * *plan (n_bands, n_row_blocks, n_blocks, n_groups, n_slots), then again with
- * wave_blocks int32[8*n_row_blocks+1], blocks int32[4*(n_blocks+1)], rows
+ * wave_blocks int32[NS_BAND_WAVES*n_row_blocks+1], blocks int32[4*(n_blocks+1)], rows
  * uint32[64*n_groups], perm int32[n_slots] (-1 for padding), col
  * uint16[n_slots].  Pointer fields of *plan are not touched.  blocks holds
  * n_blocks records plus the sentinel, rows n_groups groups including the

@@ -12,14 +12,14 @@
 //    about twice as fast.  So sources are cut into bands, and every
 //    workgroup walks the bands in the same order: the workgroups resident on
 //    one XCD gather from about one band at a time.
-//  * One 512-lane workgroup (one per compute unit) owns a block of
+//  * One 1024-lane workgroup (one per compute unit) owns a block of
 //    destination rows and one tile of C = 16 (or 8) columns.  Its row sums
 //    live in LDS for the whole tick, so no partial sums leave the compute
 //    unit.  A row's edges in one band lie in one group of one wavefront, so
 //    within a band its LDS updates race with no other wavefront; its groups
 //    of different bands may lie in different wavefronts, which the barrier
 //    after each band orders.  The wavefronts finish each band before any
-//    starts the next: a compute unit's eight
+//    starts the next: a compute unit's sixteen
 //    wavefronts then gather from one band, and the workgroups of an XCD, which
 //    start together with equal work, stay within a band or two of each other.
 //    (Two 256-lane workgroups per compute unit drifted apart by up to a dozen

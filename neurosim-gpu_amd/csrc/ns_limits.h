@@ -16,7 +16,7 @@ constexpr int kPanelWaves = 16;
 constexpr int kPanelThreads = kPanelWaves * 64;
 constexpr int kPanelMaxPrefetch = 16;                  // steps per register block, at most
 constexpr int kPanelTailSlots = 2 * kPanelMaxPrefetch * 64;
-constexpr int kBandWaves = 8;                           // wavefronts per band workgroup (one per CU)
+constexpr int kBandWaves = 16;                          // wavefronts per band workgroup (one per CU)
 constexpr int kBandMaxBlockRows = 2496;                 // 16 float row sums each in LDS (156 KB)
 constexpr int kBandMaxBlockSteps = 8;                   // steps per register block, at most
 // A band lane word: first row (bits 0-11), second row (bits 12-23) and the

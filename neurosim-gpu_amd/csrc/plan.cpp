@@ -16,6 +16,8 @@
 #include "ns_error.h"
 #include "ns_limits.h"
 
+static_assert(ns::kBandWaves == NS_BAND_WAVES, "band wavefronts match the ABI");
+
 namespace ns {
 
 char* error_buffer() {

@@ -35,7 +35,7 @@ import numpy as np
 import torch
 
 _LIB_NAME = "libneurosim_hip.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 WEIGHT_F32, WEIGHT_F16, WEIGHT_E4M3, WEIGHT_NVFP4 = 0, 1, 2, 3
 _PLAN_CACHE = 64   # row plans kept per extension (one per live topology and batch width)
@@ -589,7 +589,7 @@ class PanelLayout(_SlotLayout):
 # and flushes, and the gathers stay mostly in L2.
 BAND_WIDTH = 65535
 # Wavefronts per band workgroup (kBandWaves): one workgroup per compute unit.
-BAND_WAVES = 8
+BAND_WAVES = 16
 
 
 def default_band_rows(n: int, units: int) -> int:

@@ -104,7 +104,7 @@ BandOut plan_bands(const Csr& g, int32_t width, int32_t rows, int32_t steps) {
                          nullptr, nullptr, nullptr);
   check(rc == 0, "band size query");
   if (rc) return o;
-  o.wave_blocks.resize(8 * o.plan.n_row_blocks + 1);
+  o.wave_blocks.resize(NS_BAND_WAVES * o.plan.n_row_blocks + 1);
   o.blocks.resize(4 * (o.plan.n_blocks + 1));
   o.rows.resize(64 * o.plan.n_groups);
   o.perm.resize(o.plan.n_slots);
