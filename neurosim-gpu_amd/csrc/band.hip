@@ -61,6 +61,8 @@ struct BandArgs {
   int64_t s_stride;
   int32_t band_width, block_rows;
   int32_t n_bands, reserved;
+  uint32_t row_bytes;    // s_stride * 4
+  int32_t band_bytes;    // band_width * row_bytes: the buffer range of one band
   const int32_t* wave_blocks;
   const int32_t* blocks;
   const uint32_t* rows;   // lane words: first row, second row, switch step
@@ -125,10 +127,10 @@ __device__ __forceinline__ void add_piece(v4f* sums4, uint32_t row, int seg,
   sums4[row * G + seg] = t;
 }
 
-// Source of padding slots and of steps past a block's end: 16 zeros.
-__device__ __attribute__((aligned(16))) float kBandZeroRow[16] = {};
-
-typedef const __attribute__((address_space(1))) v4f* global_v4f_ptr;
+// Buffer resource word 3 of a raw (unswizzled, stride 0) buffer on gfx9.
+constexpr int kRawBufferWord3 = 0x00020000;
+// A byte offset beyond every band's buffer range: the load returns zeros.
+constexpr uint32_t kBandOutOfRange = 0x80000000u;
 
 // Slots start at multiples of 64, so an NVFP4 slot's nibble half is the lane's parity.
 template <int FMT>
@@ -183,7 +185,6 @@ __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) 
   const int32_t* wb = A.wave_blocks + static_cast<int64_t>(blockIdx.x) * kBandWaves + wave;
   const int32_t b_begin = wb[0], b_end = wb[1];
   const float* const srow = A.s_rows + b0;
-  const uint64_t zero_row = reinterpret_cast<uint64_t>(&kBandZeroRow[0]);
   float acc[4 * G];
 #pragma unroll
   for (int j = 0; j < 4 * G; ++j) acc[j] = 0.0f;
@@ -199,8 +200,12 @@ __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) 
   int32_t b = b_begin;
   for (int32_t band = 0; band < A.n_bands; ++band) {
   for (; b < b_end && cur.band == band; ++b) {
-    // Gathers of this block: each slot's whole C-column source row.
+    // Gathers of this block: each slot's whole C-column source row, as buffer
+    // loads over the band's rows (32-bit offsets, so no 64-bit address per
+    // load is held in registers).
     const int64_t base = static_cast<int64_t>(cur.band) * A.band_width;
+    const __amdgpu_buffer_rsrc_t band_rows = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(srow + base * A.s_stride), 0, A.band_bytes, kRawBufferWord3);
     // The G lanes of a group gather together: at step k, instruction j loads
     // piece `seg` (16 bytes) of the source row of the group's lane j, so one
     // load instruction touches 64/G rows, each in one 4G-float piece, rather
@@ -209,8 +214,7 @@ __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) 
     // 4*seg .. 4*seg+3 of the rows of its group's G lanes (acc[4j..4j+3] for
     // lane j's row), in step order, and adds them to those rows' LDS sums at
     // each row's switch or end.  A padding slot (or a step past the block's
-    // end) reads the zero row: the two global addresses are blended by a mask,
-    // so the choice stays a select and the loads stay global loads.
+    // end) loads at an offset beyond the band's range, which reads zeros.
     const int seg = lane & (G - 1);
     v4f g[D][G];
 #pragma unroll
@@ -220,10 +224,8 @@ __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) 
 #pragma unroll
       for (int j = 0; j < G; ++j) {
         const bool real = k < cur.steps && cq[j] != kBandPad;
-        const uint64_t mask = 0ull - static_cast<uint64_t>(real);
-        const uint64_t at = reinterpret_cast<uint64_t>(srow + (base + cq[j]) * A.s_stride + 4 * seg);
-        const uint64_t src = (at & mask) | ((zero_row + 16u * seg) & ~mask);
-        g[k][j] = *reinterpret_cast<global_v4f_ptr>(src);
+        const uint32_t at = real ? cq[j] * A.row_bytes + 16u * seg : kBandOutOfRange;
+        g[k][j] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(band_rows, at, 0, 0));
       }
     }
     // The next block's slots load while the gathers are in flight (past the
@@ -364,6 +366,8 @@ int band_step(const ns_step_args& a, const ns_band_plan& pl, hipStream_t stream)
   if (reinterpret_cast<uintptr_t>(pl.col) % 2 || reinterpret_cast<uintptr_t>(pl.weight) % need ||
       reinterpret_cast<uintptr_t>(pl.rows) % 4)
     return fail("band arrays are misaligned");
+  if (int64_t{pl.band_width} * a.state.stride_n * 4 >= int64_t{kBandOutOfRange})
+    return fail("a band of the state (band width x row stride) must be under 2 GiB");
   if (static_cast<int64_t>(pl.n_row_blocks) > 0x7FFFFFFF || a.batch / 8 > 65535)
     return fail("band grid too large");
 
@@ -374,6 +378,8 @@ int band_step(const ns_step_args& a, const ns_band_plan& pl, hipStream_t stream)
   A.u = plane(a.drive, a.state.data); A.v = plane(a.dendritic_drive, a.state.data);
   for (int i = 0; i < 6; ++i) A.p.v[i] = Vec{a.params[i].data, a.params[i].stride};
   A.s_rows = a.state.data; A.s_stride = a.state.stride_n;
+  A.row_bytes = static_cast<uint32_t>(a.state.stride_n * 4);
+  A.band_bytes = static_cast<int32_t>(int64_t{pl.band_width} * a.state.stride_n * 4);
   A.band_width = pl.band_width; A.block_rows = pl.block_rows; A.n_bands = pl.n_bands;
   A.wave_blocks = pl.wave_blocks; A.blocks = pl.blocks; A.rows = pl.rows; A.col = pl.col;
   A.weight = pl.weight; A.slot_scales = pl.slot_scales; A.gscale = a.matrix.global_scale;
