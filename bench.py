@@ -583,7 +583,7 @@ def main() -> None:
     cli.add_argument("--no-mall-flush", action="store_true")
     cli.add_argument("--kernel", default="auto", choices=("auto", "rows", "panels", "bands"),
                      help="headline tick kernel: LDS column panels (batch 1-2), source bands "
-                          "(batch a multiple of 8) or CSR row blocks")
+                          "(batch a multiple of 4) or CSR row blocks")
     cli.add_argument("--copy-calibration", action="store_true",
                      help="only run 256 MiB device copies (PMC byte-counter calibration)")
     cli.add_argument("--configs", default="encode,backward,weights,batched,pels,scaleout",

@@ -158,12 +158,12 @@ typedef struct ns_panel_plan {
 } ns_panel_plan;
 
 /* Source-band layout of a CSR matrix for wide batches (batch a multiple of
- * 8, neuron-major state), built by ns_plan_bands.  Sources are cut into
+ * 4, neuron-major state), built by ns_plan_bands.  Sources are cut into
  * `n_bands` bands of `band_width` neurons; a band of the state (band_width x
- * 16 or 8 floats per column tile) is sized to stay resident in one XCD's L2 while
+ * 16, 8 or 4 floats per column tile) is sized to stay resident in one XCD's L2 while
  * every workgroup on that XCD gathers from it.  Destination rows are cut into
  * `n_row_blocks` blocks of `block_rows` rows; one workgroup owns one block
- * (and one tile of 16 or 8 columns), keeps the block's row sums in LDS, walks the
+ * (and one tile of 16, 8 or 4 columns), keeps the block's row sums in LDS, walks the
  * bands in order, passing a workgroup barrier after each, and finally applies
  * the update.  Per band, the block's rows with edges in the band are packed
  * into groups of 64 lanes: a group's first rows are the 64 longest segments
@@ -459,9 +459,10 @@ int ns_plan_bands(const int32_t* rowptr_host, const int32_t* col_host, int64_t n
 /* Largest block_rows the band kernel's LDS holds. */
 int32_t ns_band_max_block_rows(void);
 
-/* Fused matrix tick over a band layout (batch a multiple of 8, state
+/* Fused matrix tick over a band layout (batch a multiple of 4, state
  * neuron-major with 16-byte aligned rows; workgroups take 16 state columns
- * when the batch is a multiple of 16, else 8).  Same semantics and arguments as
+ * when the batch is a multiple of 16, else 8 when it is a multiple of 8, else
+ * 4).  Same semantics and arguments as
  * ns_dendritic_step (it replaces the same reference entry,
  * csrc/bindings.cpp:3-7,137-142; csrc/compartmental.cu:176-236); `args->plan`
  * and `args->panels` are ignored, the CSR in `args->matrix` gives only the

@@ -1,6 +1,6 @@
 // Fused dendritic matrix tick over source bands, for wide batches (16 state
-// columns per workgroup, or 8 when the batch is an odd multiple of 8) whose
-// state is larger than an XCD's L2.
+// columns per workgroup; 8 when the batch is an odd multiple of 8, 4 when it
+// is an odd multiple of 4) whose state is larger than an XCD's L2.
 //
 // Semantics follow the reference's fused kernel (csrc/compartmental.cu:121-140
 // and :72-90): j = W @ s over the batch columns, then the three-state update.
@@ -13,7 +13,7 @@
 //    workgroup walks the bands in the same order: the workgroups resident on
 //    one XCD gather from about one band at a time.
 //  * One 1024-lane workgroup (one per compute unit) owns a block of
-//    destination rows and one tile of C = 16 (or 8) columns.  Its row sums
+//    destination rows and one tile of C = 16 (or 8, or 4) columns.  Its row sums
 //    live in LDS for the whole tick, so no partial sums leave the compute
 //    unit.  A row's edges in one band lie in one group of one wavefront, so
 //    within a band its LDS updates race with no other wavefront; its groups
@@ -32,7 +32,7 @@
 //    lane one 16-byte quarter of each, and each lane keeps the running sums
 //    of its quarter's four columns for the quad's four rows (16 registers);
 //    with 8 columns a pair of lanes does the same for its two rows' 32-byte
-//    source rows.  A lane whose row ends early may take a
+//    source rows, and with 4 each lane loads its own 16-byte row.  A lane whose row ends early may take a
 //    second, shorter row in the group's remaining steps: at the switch step it
 //    adds its sums to the first row's LDS sums and starts again from zero.
 //    At the group's end the lane adds them to its (last) row's LDS sums.
@@ -157,16 +157,21 @@ __device__ __forceinline__ uint32_t from_group_lane(uint32_t v) {
 }
 template <int G>
 __device__ __forceinline__ void group_values(uint32_t v, uint32_t (&out)[G]) {
-  out[0] = from_group_lane<G, 0>(v);
-  out[1] = from_group_lane<G, 1>(v);
-  if constexpr (G == 4) {
-    out[2] = from_group_lane<G, 2>(v);
-    out[3] = from_group_lane<G, 3>(v);
+  if constexpr (G == 1) {
+    out[0] = v;   // a lane gathers its own row
+  } else {
+    out[0] = from_group_lane<G, 0>(v);
+    out[1] = from_group_lane<G, 1>(v);
+    if constexpr (G == 4) {
+      out[2] = from_group_lane<G, 2>(v);
+      out[3] = from_group_lane<G, 3>(v);
+    }
   }
 }
 
 // C: state columns per workgroup, 16 (a 64-byte source row, gathered by the
-// four lanes of a quad) or 8 (a 32-byte row, gathered by a pair of lanes).
+// four lanes of a quad), 8 (a 32-byte row, gathered by a pair of lanes) or 4
+// (a 16-byte row, gathered by its own lane).
 template <int FMT, int D, int C>
 __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) {
   constexpr int G = C / 4;   // lanes that gather a row together, 16 bytes each
@@ -310,8 +315,9 @@ hipError_t launch_bands(const BandArgs& A, int fmt, int n_row_blocks, hipStream_
 
 template <int D>
 hipError_t launch_bands(const BandArgs& A, int fmt, int n_row_blocks, hipStream_t stream) {
-  return A.B % 16 == 0 ? launch_bands<D, 16>(A, fmt, n_row_blocks, stream)
-                       : launch_bands<D, 8>(A, fmt, n_row_blocks, stream);
+  return A.B % 16 == 0  ? launch_bands<D, 16>(A, fmt, n_row_blocks, stream)
+         : A.B % 8 == 0 ? launch_bands<D, 8>(A, fmt, n_row_blocks, stream)
+                        : launch_bands<D, 4>(A, fmt, n_row_blocks, stream);
 }
 
 template <int D, int C>
@@ -331,15 +337,16 @@ hipError_t allow_band_lds() {
 
 template <int D>
 hipError_t allow_band_lds() {
-  const hipError_t e = allow_band_lds<D, 16>();
-  return e != hipSuccess ? e : allow_band_lds<D, 8>();
+  hipError_t e = allow_band_lds<D, 16>();
+  if (e == hipSuccess) e = allow_band_lds<D, 8>();
+  return e != hipSuccess ? e : allow_band_lds<D, 4>();
 }
 
 int check_step_head(const ns_step_args& a);
 int check_step_planes(const ns_step_args& a);
 
 int band_step(const ns_step_args& a, const ns_band_plan& pl, hipStream_t stream) {
-  if (a.batch % 8) return fail("the band kernel needs a batch that is a multiple of 8, not %lld",
+  if (a.batch % 4) return fail("the band kernel needs a batch that is a multiple of 4, not %lld",
                                (long long)a.batch);
   if (a.state.stride_b != 1 || a.state.stride_n < a.batch || a.state.stride_n % 4 ||
       reinterpret_cast<uintptr_t>(a.state.data) % 16)
@@ -368,7 +375,7 @@ int band_step(const ns_step_args& a, const ns_band_plan& pl, hipStream_t stream)
     return fail("band arrays are misaligned");
   if (int64_t{pl.band_width} * a.state.stride_n * 4 >= int64_t{kBandOutOfRange})
     return fail("a band of the state (band width x row stride) must be under 2 GiB");
-  if (static_cast<int64_t>(pl.n_row_blocks) > 0x7FFFFFFF || a.batch / 8 > 65535)
+  if (static_cast<int64_t>(pl.n_row_blocks) > 0x7FFFFFFF || a.batch / 4 > 65535)
     return fail("band grid too large");
 
   BandArgs A{};

@@ -604,7 +604,7 @@ def default_band_rows(n: int, units: int) -> int:
 
 
 class BandLayout(_SlotLayout):
-    """Source-band layout of one graph for batches that are multiples of 8 (see ns_plan_bands).
+    """Source-band layout of one graph for batches that are multiples of 4 (see ns_plan_bands).
 
     Built once per graph structure on the host from copies of in_rowptr and
     in_col (a synchronisation; set-up only).  Holds the device tables, the

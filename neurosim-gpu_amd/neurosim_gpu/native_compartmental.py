@@ -233,8 +233,8 @@ def panels_pay_off(topology, batch: int) -> bool:
 
 
 # Fewest bytes of one workgroup's column tile of the state (16 columns when the
-# batch is a multiple of 16, else 8) for which "auto" picks the band kernel, one
-# XCD's L2.  Measured, us per tick (rows / bands), 20 edges per neuron, fp32:
+# batch is a multiple of 16, else 8 or 4) for which "auto" picks the band kernel,
+# one XCD's L2.  Measured, us per tick (rows / bands), 20 edges per neuron, fp32:
 # B=8: N=50k (1.6 MB) 14.7 / 17.2, N=131k (4 MB) 36.5 / 29.5, N=262k 75.0 / 46.3,
 # N=524k 173.7 / 89.0; B=16: N=65k (4 MB) 46.4 / 29.0, N=131k 81.9 / 41.4,
 # N=262k 152.8 / 66.5; N=1M, M=100M, fp8: B=8 1603 / 658, B=16 1933 / 855.
@@ -242,13 +242,22 @@ BAND_AUTO_MIN_TILE_BYTES = 4 << 20
 
 
 def band_tile_columns(batch: int) -> int:
-    """State columns per band workgroup: 16, or 8 for an odd multiple of 8."""
-    return 16 if batch % 16 == 0 else 8
+    """State columns per band workgroup: 16, or 8 for an odd multiple of 8, or 4
+    for an odd multiple of 4."""
+    return 16 if batch % 16 == 0 else 8 if batch % 8 == 0 else 4
+
+
+def default_band_steps(batch: int) -> int:
+    """Steps per register block of the band tick: 8 for 4-column tiles, whose
+    gathers need few registers (N=1M, M=100M, B=4, fp8: 551 us against 579 at
+    4 steps), else 4 (16 columns at 8 steps exceed the registers of 16
+    wavefronts per compute unit)."""
+    return 8 if band_tile_columns(batch) == 4 else 4
 
 
 def bands_pay_off(n_neurons: int, batch: int) -> bool:
     """Whether "auto" picks the band kernel for this state size."""
-    return (batch > 0 and batch % 8 == 0
+    return (batch > 0 and batch % 4 == 0
             and n_neurons * band_tile_columns(batch) * 4 >= BAND_AUTO_MIN_TILE_BYTES)
 
 
@@ -266,11 +275,11 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
     state in LDS and streams a panel-sorted copy of the graph (batch 1 or 2;
     built once, at construction), "bands" streams a band-sorted copy of the
     graph whose gathers stay within an L2-sized band of sources at a time
-    (batch a multiple of 8; built once), "rows" streams the CSR as is and
+    (batch a multiple of 4; built once), "rows" streams the CSR as is and
     gathers the state from cache.  "auto" uses panels when the batch allows
     and the graph is dense enough for them (``panels_pay_off``), bands when
-    the batch is a multiple of 8 and a workgroup's column tile of the state
-    (16 or 8 columns) is at least ``BAND_AUTO_MIN_TILE_BYTES`` (``bands_pay_off``),
+    the batch is a multiple of 4 and a workgroup's column tile of the state
+    (16, 8 or 4 columns) is at least ``BAND_AUTO_MIN_TILE_BYTES`` (``bands_pay_off``),
     rows otherwise.  ``panel_width`` caps
     the neurons per panel (default: what LDS holds) and ``panel_tiles`` sets
     the workgroups per panel (default: compute units / panels).
@@ -281,7 +290,7 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
     ``band_width`` sets the sources per band (default ``BAND_WIDTH``),
     ``band_rows`` the destination rows per band workgroup (default: one
     workgroup per compute unit, ``default_band_rows``) and ``band_steps`` the
-    register block (2, 4 or 8 steps).
+    register block (2, 4 or 8 steps; default ``default_band_steps``).
     """
 
     def __init__(self, topology: SparseTopology, dynamics: DendriticDynamics,
@@ -290,7 +299,7 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
                  weight_format: str | None = None, kernel: str = "auto",
                  panel_width: int | None = None, panel_tiles: int | None = None,
                  band_width: int | None = None, band_rows: int | None = None,
-                 band_steps: int = 4, panel_pairs: bool | None = None) -> None:
+                 band_steps: int | None = None, panel_pairs: bool | None = None) -> None:
         if kernel not in ("auto", "rows", "panels", "bands"):
             raise ValueError("kernel must be 'auto', 'rows', 'panels' or 'bands'")
         if threads_per_row not in (None, 8, 16, 32):
@@ -313,8 +322,8 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         native = isinstance(self.extension, NativeExtension)
         if kernel == "panels" and (batch not in (1, 2) or not native):
             raise ValueError("the panel kernel needs batch 1 or 2 and the native extension")
-        if kernel == "bands" and (batch % 8 or batch == 0 or not native):
-            raise ValueError("the band kernel needs a batch that is a multiple of 8 and the "
+        if kernel == "bands" and (batch % 4 or batch == 0 or not native):
+            raise ValueError("the band kernel needs a batch that is a multiple of 4 and the "
                              "native extension")
         use_panels = kernel == "panels" or (kernel == "auto" and batch in (1, 2) and native
                                             and panels_pay_off(topology, batch))
@@ -335,7 +344,7 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         self._panel_width = panel_width
         self._bands = (BandLayout(topology, initial_state.device,
                                   band_width=band_width or BAND_WIDTH, block_rows=band_rows,
-                                  block_steps=band_steps)
+                                  block_steps=band_steps or default_band_steps(batch))
                        if use_bands else None)
 
     def _invalidate_precision_cache(self) -> None:

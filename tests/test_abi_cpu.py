@@ -163,9 +163,9 @@ def test_band_step_validation_messages(lib):
         rc = lib.ns_dendritic_step_bands(ctypes.byref(args), ctypes.byref(plan), None)
         return rc, lib.ns_last_error().decode()
 
-    args, keep = fake_step_args(n=8, batch=12)
+    args, keep = fake_step_args(n=8, batch=6)
     plan, tables = fake_band_plan(8)
-    assert "multiple of 8" in band_call(args, plan)[1]
+    assert "multiple of 4" in band_call(args, plan)[1]
     args, keep = fake_step_args(n=8, batch=16)
     assert "neuron-major" in band_call(args, plan)[1]
     # neuron-major [16,8] planes from here on

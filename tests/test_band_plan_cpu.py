@@ -268,13 +268,17 @@ def test_band_padding_at_scale_out_density():
 
 
 def test_auto_picks_bands_by_tile_bytes():
-    """"auto" takes bands for batches that are multiples of 8 once a workgroup's
-    column tile of the state (16 columns, or 8 for odd multiples of 8) holds 4 MB."""
-    from neurosim_gpu.native_compartmental import band_tile_columns, bands_pay_off
+    """"auto" takes bands for batches that are multiples of 4 once a workgroup's
+    column tile of the state (16 columns, or 8 or 4 for odd multiples of 8 or 4)
+    holds 4 MB."""
+    from neurosim_gpu.native_compartmental import (band_tile_columns, bands_pay_off,
+                                                   default_band_steps)
 
-    assert [band_tile_columns(b) for b in (8, 16, 24, 32, 48)] == [8, 16, 8, 16, 16]
+    assert [band_tile_columns(b) for b in (4, 8, 12, 16, 24, 32, 48)] == [4, 8, 4, 16, 8, 16, 16]
+    assert bands_pay_off(262_144, 4) and not bands_pay_off(262_143, 4)
     assert bands_pay_off(65_536, 16) and not bands_pay_off(65_535, 16)
     assert bands_pay_off(131_072, 8) and not bands_pay_off(131_071, 8)
     assert bands_pay_off(131_072, 24) and bands_pay_off(1_000_000, 8)
     assert not bands_pay_off(50_000, 8)
-    assert not any(bands_pay_off(1_000_000, b) for b in (0, 1, 2, 4, 12))
+    assert not any(bands_pay_off(1_000_000, b) for b in (0, 1, 2, 6, 10))
+    assert [default_band_steps(b) for b in (4, 8, 12, 16)] == [8, 4, 8, 4]

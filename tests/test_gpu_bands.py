@@ -1,5 +1,5 @@
-"""The source-band tick (batch a multiple of 8: workgroups of 16 state columns
-when the batch is a multiple of 16, else of 8) on the MI355X.
+"""The source-band tick (batch a multiple of 4: workgroups of 16 state columns
+when the batch is a multiple of 16, else of 8 or 4) on the MI355X.
 
 Small band widths and row blocks force many bands, many row blocks and short
 register blocks on small graphs; hub rows give segments of hundreds to
@@ -50,7 +50,7 @@ def band_runtime(topology, model, state, **kwargs):
     return native
 
 
-@pytest.mark.parametrize("batch", [8, 16, 24, 32])
+@pytest.mark.parametrize("batch", [4, 8, 12, 16, 24, 32])
 @pytest.mark.parametrize("width,rows,steps", [(None, None, 8), (1000, 256, 8), (512, 64, 4),
                                               (4096, 2496, 8), (777, 1001, 4)])
 def test_bands_match_oracle(gpu, batch, width, rows, steps):
@@ -71,7 +71,7 @@ def test_bands_match_oracle(gpu, batch, width, rows, steps):
     assert worst <= 1e-5
 
 
-@pytest.mark.parametrize("batch", [8, 16])
+@pytest.mark.parametrize("batch", [4, 8, 16])
 def test_bands_and_rows_agree_and_repeat(gpu, batch):
     case = make_case(20_000, 400_000, 5, gpu)
     runs = {}
@@ -87,7 +87,7 @@ def test_bands_and_rows_agree_and_repeat(gpu, batch):
     assert errors(runs["bands"], runs["rows"]) <= 2e-6
 
 
-@pytest.mark.parametrize("batch", [8, 16])
+@pytest.mark.parametrize("batch", [4, 8, 16])
 @pytest.mark.parametrize("fmt", ["fp16", "fp8", "nvfp4"])
 def test_band_formats_equal_decoded_fp32(gpu, fmt, batch):
     graph, topology, model, params = hub_case(gpu, n=6000, seed=9)
@@ -138,7 +138,7 @@ def test_band_state_layouts_drives_and_weight_refresh(gpu):
     assert errors(native, oracle) <= 1e-5
 
 
-@pytest.mark.parametrize("batch", [8, 16])
+@pytest.mark.parametrize("batch", [4, 8, 16])
 def test_band_rollout_graph_equals_eager_ticks(gpu, batch):
     case = make_case(5000, 100_000, 6, gpu)
     drive = column_drive(batch).to(gpu)
