@@ -582,12 +582,13 @@ class PanelLayout(_SlotLayout):
         return plan
 
 
-# Sources per band: the most a 16-bit band-local index holds (0xFFFF marks
-# padding), 65535 neurons x 16 columns x 4 bytes = 4 MB of state, an XCD's L2.
-# Measured at N=1M, M=100M, B=16 (ms per tick): 24576 sources 1.10, 32768 1.01,
-# 45056 0.91, 53248 0.88, 65535 0.88; fewer bands mean fewer barriers, groups
-# and flushes, and the gathers stay mostly in L2.
-BAND_WIDTH = 65535
+# Sources per band (at most 65535, the most a 16-bit band-local index holds;
+# 0xFFFF marks padding): 53248 neurons x 16 columns x 4 bytes = 3.4 MB of
+# state, most of an XCD's 4 MB L2, leaving room for the slot stream.  Measured
+# at N=1M, M=100M, fp8 (us per tick), B=16: 49152 sources 725.6, 53248 710.7,
+# 57344 719.0, 61440 720.2, 65535 726.1 (32768: 736.4); B=8: 609.4, 597.4,
+# 600.5, 597.5, 598.7.  Fewer bands mean fewer barriers, groups and flushes.
+BAND_WIDTH = 53248
 # Wavefronts per band workgroup (kBandWaves): one workgroup per compute unit.
 BAND_WAVES = 16
 

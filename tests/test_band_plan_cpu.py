@@ -249,7 +249,7 @@ def test_band_plan_does_not_depend_on_thread_count(monkeypatch):
 
 def test_band_padding_at_scale_out_density():
     """About 3.3 edges per (row, band), as at N=1M, M=100M with bands of 32,768
-    sources (the default 65,535 gives 6.6, with less padding), and 1954-row
+    sources (the default 53,248 gives 5.3, with less padding), and 1954-row
     blocks of 16 wavefronts, as there: with a block's rows pooled per band and
     a second row per lane where one fits, the layout holds at most 1.05 slots
     per edge (rows dealt to the wavefronts first: 1.13; one row per lane:
