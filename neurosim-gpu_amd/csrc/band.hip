@@ -218,17 +218,24 @@ __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) 
     // of the cache-line accesses.  Lane l then accumulates columns
     // 4*seg .. 4*seg+3 of the rows of its group's G lanes (acc[4j..4j+3] for
     // lane j's row), in step order, and adds them to those rows' LDS sums at
-    // each row's switch or end.  A padding slot (or a step past the block's
-    // end) loads at an offset beyond the band's range, which reads zeros.
+    // each row's switch or end.  A padding slot loads at an offset beyond the
+    // band's range, which reads zeros.
     const int seg = lane & (G - 1);
     v4f g[D][G];
 #pragma unroll
     for (int k = 0; k < D; ++k) {
+      // Steps past the block's end issue no loads (a wave-uniform test): each
+      // load instruction costs address-unit cycles whatever its lanes read.
+      if (k >= cur.steps) {
+#pragma unroll
+        for (int j = 0; j < G; ++j) g[k][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        continue;
+      }
       uint32_t cq[G];
       group_values<G>(here[k].c, cq);
 #pragma unroll
       for (int j = 0; j < G; ++j) {
-        const bool real = k < cur.steps && cq[j] != kBandPad;
+        const bool real = cq[j] != kBandPad;
         const uint32_t at = real ? cq[j] * A.row_bytes + 16u * seg : kBandOutOfRange;
         g[k][j] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(band_rows, at, 0, 0));
       }
