@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 14
+#define NS_ABI_VERSION 15
 
 /* Return codes. */
 #define NS_OK 0
@@ -172,11 +172,12 @@ typedef struct ns_panel_plan {
  * possibly a second row's segment (the longest left that fits, lanes with the
  * most spare steps choosing first).  Each group goes to the one of the
  * NS_BAND_WAVES wavefronts with the fewest steps in the band so far, so a
- * row's groups of different bands may lie in different wavefronts.  A group's slots are
- * step-major (slot (step k, lane l) is 64*first_step + 64*k + l).  A group is
- * cut into register blocks of at most `block_steps` steps; a wavefront's
- * blocks are consecutive in `blocks`, in band order, and their slots
- * contiguous.
+ * row's groups of different bands may lie in different wavefronts.  A group is
+ * cut into register blocks of `block_steps` steps (its last block may count
+ * fewer; its slots past that count are padding).  A block's slots are
+ * lane-major: slot (lane l, step k) is 64*first_step + l*block_steps + k, so a
+ * lane's steps are consecutive.  A wavefront's blocks are consecutive in
+ * `blocks`, in band order, and their slots contiguous.
  * Padding slots have source index 0xFFFF and weight code 0.  Slot k is
  * original CSR edge perm[k] (or padding).  The kernel reads one block record
  * and one register block of slots ahead, so the tables end with a sentinel

@@ -92,25 +92,83 @@ __device__ __forceinline__ BandBlock load_band_block(const BandArgs& A, int32_t 
   return BandBlock{q[0], q[1], info & 0xFF, (info >> 8) & 1, info >> 9, q[3]};
 }
 
-// This lane's D slots from the block's first step, and its lane word in the
-// block's group.  The loads do not depend on the block's step count (the slot array
-// has D padding steps past its end, the block table a sentinel record), so
-// the compiler can count them and wait for exactly the ones it needs.
+// BYTES consecutive bytes at p (1, 2, 4, 8, 16 or 32; aligned to their size,
+// at most 16) as little-endian 32-bit words, in one or two load instructions.
+template <int BYTES>
+__device__ __forceinline__ void load_run(const void* p, uint32_t (&w)[(BYTES + 3) / 4]) {
+  if constexpr (BYTES == 1) {
+    w[0] = *static_cast<const uint8_t*>(p);
+  } else if constexpr (BYTES == 2) {
+    w[0] = *static_cast<const uint16_t*>(p);
+  } else if constexpr (BYTES == 4) {
+    w[0] = *static_cast<const uint32_t*>(p);
+  } else if constexpr (BYTES == 8) {
+    const uint2 v = *static_cast<const uint2*>(p);
+    w[0] = v.x; w[1] = v.y;
+  } else {
+    static_assert(BYTES == 16 || BYTES == 32, "runs of 1 to 32 bytes");
+#pragma unroll
+    for (int h = 0; h < BYTES / 16; ++h) {
+      const uint4 v = static_cast<const uint4*>(p)[h];
+      w[4 * h + 0] = v.x; w[4 * h + 1] = v.y; w[4 * h + 2] = v.z; w[4 * h + 3] = v.w;
+    }
+  }
+}
+
+// Field k of BITS bits (4, 8, 16 or 32) of a run of little-endian words.
+template <int BITS, int N>
+__device__ __forceinline__ uint32_t run_field(const uint32_t (&w)[N], int k) {
+  if constexpr (BITS == 32) {
+    return w[k];
+  } else {
+    constexpr int per = 32 / BITS;
+    return (w[k / per] >> (BITS * (k % per))) & ((1u << BITS) - 1u);
+  }
+}
+
+// This lane's D slots of the block and its lane word in the block's group.  A
+// block's slots are lane-major (lane l's steps at 64*first_step + l*D + k), so
+// the lane's D source indices come in one load and its D weight codes in
+// another, rather than one load per step.  The loads do not depend on the
+// block's step count (the slot array has D padding steps past its end, the
+// block table a sentinel record), so the compiler can count them and wait for
+// exactly the ones it needs.
 template <int FMT, int D>
 __device__ __forceinline__ void load_band_slots(const BandArgs& A, const BandBlock& blk, int lane,
                                                 BandSlot (&x)[D], uint32_t& row) {
-  const int64_t q0 = int64_t{64} * blk.step0 + lane;
+  const int64_t q0 = int64_t{64} * blk.step0 + int64_t{D} * lane;
+  uint32_t cw[(2 * D + 3) / 4];
+  load_run<2 * D>(A.col + q0, cw);
 #pragma unroll
   for (int k = 0; k < D; ++k) {
-    const int64_t q = q0 + 64 * k;
-    x[k].c = A.col[q];
+    x[k].c = run_field<16>(cw, k);
     x[k].sc = 0u;
-    if constexpr (FMT == NS_WEIGHT_F32) x[k].w = static_cast<const uint32_t*>(A.weight)[q];
-    else if constexpr (FMT == NS_WEIGHT_F16) x[k].w = static_cast<const uint16_t*>(A.weight)[q];
-    else if constexpr (FMT == NS_WEIGHT_E4M3) x[k].w = static_cast<const uint8_t*>(A.weight)[q];
-    else {
-      x[k].w = static_cast<const uint8_t*>(A.weight)[q >> 1];
-      x[k].sc = A.slot_scales[q];
+  }
+  if constexpr (FMT == NS_WEIGHT_F32) {
+    uint32_t ww[D];
+    load_run<4 * D>(static_cast<const uint32_t*>(A.weight) + q0, ww);
+#pragma unroll
+    for (int k = 0; k < D; ++k) x[k].w = ww[k];
+  } else if constexpr (FMT == NS_WEIGHT_F16) {
+    uint32_t ww[(2 * D + 3) / 4];
+    load_run<2 * D>(static_cast<const uint16_t*>(A.weight) + q0, ww);
+#pragma unroll
+    for (int k = 0; k < D; ++k) x[k].w = run_field<16>(ww, k);
+  } else if constexpr (FMT == NS_WEIGHT_E4M3) {
+    uint32_t ww[(D + 3) / 4];
+    load_run<D>(static_cast<const uint8_t*>(A.weight) + q0, ww);
+#pragma unroll
+    for (int k = 0; k < D; ++k) x[k].w = run_field<8>(ww, k);
+  } else {
+    // Two nibbles per byte in slot order (q0 is even): step k's nibble is
+    // nibble k of the lane's D/2 bytes; one block-scale code per slot.
+    uint32_t ww[(D / 2 + 3) / 4], sw[(D + 3) / 4];
+    load_run<D / 2>(static_cast<const uint8_t*>(A.weight) + q0 / 2, ww);
+    load_run<D>(A.slot_scales + q0, sw);
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+      x[k].w = run_field<4>(ww, k);
+      x[k].sc = run_field<8>(sw, k);
     }
   }
   row = A.rows[int64_t{64} * blk.group + lane];
@@ -132,9 +190,9 @@ constexpr int kRawBufferWord3 = 0x00020000;
 // A byte offset beyond every band's buffer range: the load returns zeros.
 constexpr uint32_t kBandOutOfRange = 0x80000000u;
 
-// Slots start at multiples of 64, so an NVFP4 slot's nibble half is the lane's parity.
+// An NVFP4 slot carries its own nibble (see load_band_slots).
 template <int FMT>
-__device__ __forceinline__ float decode_band(const BandSlot& x, int lane, float gscale) {
+__device__ __forceinline__ float decode_band(const BandSlot& x, float gscale) {
   if constexpr (FMT == NS_WEIGHT_F32) {
     return __builtin_bit_cast(float, x.w);
   } else if constexpr (FMT == NS_WEIGHT_F16) {
@@ -142,8 +200,7 @@ __device__ __forceinline__ float decode_band(const BandSlot& x, int lane, float 
   } else if constexpr (FMT == NS_WEIGHT_E4M3) {
     return e4m3_to_float(x.w) * gscale;
   } else {
-    const ns_v2f pair = e2m1_pair(x.w & 0xFFu);
-    return ((lane & 1) ? pair.y : pair.x) * (e4m3_to_float(x.sc) * gscale);
+    return e2m1_pair(x.w).x * (e4m3_to_float(x.sc) * gscale);
   }
 }
 
@@ -253,7 +310,7 @@ __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) 
 #pragma unroll
     for (int k = 0; k < D; ++k) {
       if (k < cur.steps) {
-        const float w = decode_band<FMT>(here[k], lane, gscale);
+        const float w = decode_band<FMT>(here[k], gscale);
         uint32_t wq[G];
         group_values<G>(__builtin_bit_cast(uint32_t, w), wq);
 #pragma unroll

@@ -561,18 +561,22 @@ void append_band_block(BandLayout& out, const int32_t* rowptr, const int32_t* co
           }
           part.rows.push_back(word);
         }
+      // A block spans block_steps steps (those past the group's end are
+      // padding) and its slots are lane-major: lane l's steps are the
+      // consecutive slots 64*first_step + l*block_steps + (0 .. block_steps-1),
+      // so the kernel loads each lane's columns, and its weights, at once.
       for (int32_t t0 = 0; t0 < steps; t0 += block_steps) {
         const int32_t nst = std::min(block_steps, steps - t0);
         const int32_t last = t0 + block_steps >= steps ? 1 : 0;
         const int32_t rec[4] = {static_cast<int32_t>(part.n_slots / 64), k,
                                 nst | (last << 8) | (t0 << 9), group};
         part.blocks.insert(part.blocks.end(), rec, rec + 4);
-        part.n_slots += int64_t{64} * nst;
+        part.n_slots += int64_t{64} * block_steps;
         if (!fill) continue;
-        for (int32_t t = t0; t < t0 + nst; ++t)
-          for (int l = 0; l < 64; ++l) {
+        for (int l = 0; l < 64; ++l)
+          for (int32_t t = t0; t < t0 + block_steps; ++t) {
             int32_t edge = -1;
-            if (l < gn) {
+            if (l < gn && t < t0 + nst) {
               const int32_t la = seg_len(first[l]);
               if (t < la) edge = edge_at(first[l], t);
               else if (second[l] >= 0 && t - la < seg_len(second[l])) edge = edge_at(second[l], t - la);
