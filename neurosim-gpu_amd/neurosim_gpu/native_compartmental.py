@@ -248,11 +248,11 @@ def band_tile_columns(batch: int) -> int:
 
 
 def default_band_steps(batch: int) -> int:
-    """Steps per register block of the band tick: 8 for 4-column tiles, whose
-    gathers need few registers (N=1M, M=100M, B=4, fp8: 551 us against 579 at
-    4 steps), else 4 (16 columns at 8 steps exceed the registers of 16
-    wavefronts per compute unit)."""
-    return 8 if band_tile_columns(batch) == 4 else 4
+    """Steps per register block of the band tick: 8 for 8- and 4-column tiles,
+    whose gathers need fewer registers (N=1M, M=100M, fp8, us per tick at 8 / 4
+    steps: B=8 579 / 590, B=4 515 / 537), 4 for 16 columns (8 steps exceed the
+    registers of 16 wavefronts per compute unit and spill)."""
+    return 4 if band_tile_columns(batch) == 16 else 8
 
 
 def bands_pay_off(n_neurons: int, batch: int) -> bool:

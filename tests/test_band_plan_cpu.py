@@ -289,4 +289,4 @@ def test_auto_picks_bands_by_tile_bytes():
     assert bands_pay_off(131_072, 24) and bands_pay_off(1_000_000, 8)
     assert not bands_pay_off(50_000, 8)
     assert not any(bands_pay_off(1_000_000, b) for b in (0, 1, 2, 6, 10))
-    assert [default_band_steps(b) for b in (4, 8, 12, 16)] == [8, 4, 8, 4]
+    assert [default_band_steps(b) for b in (4, 8, 12, 16, 24, 32)] == [8, 8, 8, 4, 8, 4]
