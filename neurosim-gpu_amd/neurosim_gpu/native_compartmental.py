@@ -290,7 +290,8 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
     ``band_width`` sets the sources per band (default ``BAND_WIDTH``),
     ``band_rows`` the destination rows per band workgroup (default: one
     workgroup per compute unit, ``default_band_rows``) and ``band_steps`` the
-    register block (2, 4 or 8 steps; default ``default_band_steps``).
+    register block (2, 4 or 8 steps; default ``default_band_steps``; 8 steps
+    with 16 columns per workgroup spill registers and run about 3x slower).
     """
 
     def __init__(self, topology: SparseTopology, dynamics: DendriticDynamics,
