@@ -662,11 +662,12 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
 
 // Several panels, NS_PANEL_COMBINE_LAUNCH: add each row's panel partial sums
 // in panel order, then update; one neuron (all BT columns) per thread.  Every
-// load (state, parameters, the first kCombineBatch panels' sums) is issued
-// before the first add, so the kernel waits on memory about once rather than
-// once per panel.
+// load (state, parameters, the first CB panels' sums) is issued before the
+// first add, so the kernel waits on memory about once rather than once per
+// panel.  CB is the number of panels, up to kCombineBatch, so that no load
+// rereads a panel's sum: each load instruction costs address-unit cycles.
 
-template <int BT>
+template <int BT, int CB>
 __global__ __launch_bounds__(kThreads) void panel_combine_kernel(PanelArgs A) {
   const int64_t n = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (n >= A.N) return;
@@ -691,10 +692,10 @@ __global__ __launch_bounds__(kThreads) void panel_combine_kernel(PanelArgs A) {
   float sum[BT];
 #pragma unroll
   for (int j = 0; j < BT; ++j) sum[j] = 0.0f;
-  for (int p0 = 0; p0 < A.n_panels; p0 += kCombineBatch) {
-    float part[kCombineBatch][BT];
+  for (int p0 = 0; p0 < A.n_panels; p0 += CB) {
+    float part[CB][BT];
 #pragma unroll
-    for (int q = 0; q < kCombineBatch; ++q) {
+    for (int q = 0; q < CB; ++q) {
       // Past the last panel, reread the last panel's sum (not added) so that
       // no load waits behind a branch.
       const int p = min(p0 + q, A.n_panels - 1);
@@ -702,7 +703,7 @@ __global__ __launch_bounds__(kThreads) void panel_combine_kernel(PanelArgs A) {
       for (int j = 0; j < BT; ++j) part[q][j] = A.partials[p * plane + n * BT + j];
     }
 #pragma unroll
-    for (int q = 0; q < kCombineBatch; ++q)
+    for (int q = 0; q < CB; ++q)
 #pragma unroll
       for (int j = 0; j < BT; ++j)
         if (p0 + q < A.n_panels) sum[j] += part[q][j];
@@ -729,8 +730,16 @@ hipError_t launch_panels(const PanelArgs& A, int fmt, int n_tiles, hipStream_t s
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || A.n_panels == 1 || A.counters) return err;
-  const int64_t blocks = (A.N + kThreads - 1) / kThreads;
-  panel_combine_kernel<BT><<<dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, stream>>>(A);
+  const dim3 cgrid(static_cast<unsigned>((A.N + kThreads - 1) / kThreads)), cblock(kThreads);
+  switch (std::min(A.n_panels, kCombineBatch)) {
+    case 2: panel_combine_kernel<BT, 2><<<cgrid, cblock, 0, stream>>>(A); break;
+    case 3: panel_combine_kernel<BT, 3><<<cgrid, cblock, 0, stream>>>(A); break;
+    case 4: panel_combine_kernel<BT, 4><<<cgrid, cblock, 0, stream>>>(A); break;
+    case 5: panel_combine_kernel<BT, 5><<<cgrid, cblock, 0, stream>>>(A); break;
+    case 6: panel_combine_kernel<BT, 6><<<cgrid, cblock, 0, stream>>>(A); break;
+    case 7: panel_combine_kernel<BT, 7><<<cgrid, cblock, 0, stream>>>(A); break;
+    default: panel_combine_kernel<BT, kCombineBatch><<<cgrid, cblock, 0, stream>>>(A); break;
+  }
   return hipGetLastError();
 }
 
