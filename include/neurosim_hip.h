@@ -207,7 +207,8 @@ typedef struct ns_band_plan {
                                   0-11) and second row (bits 12-23), 0xFFF none, and the
                                   step in the group where the second row starts (bits
                                   24-31; 0 without a second row) */
-  const uint16_t* col;         /* [n_slots] source index minus the band's first neuron */
+  const uint16_t* col;         /* [n_slots] source index minus the band's first neuron;
+                                  16-byte aligned, as are weight and slot_scales */
   const void* weight;          /* [n_slots] weights in slot order, encoding of the matrix */
   const uint8_t* slot_scales;  /* NVFP4: e4m3 block-scale code of each slot's edge */
 } ns_band_plan;

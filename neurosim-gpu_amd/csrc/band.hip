@@ -433,10 +433,12 @@ int band_step(const ns_step_args& a, const ns_band_plan& pl, hipStream_t stream)
     return fail("band plan tables are required");
   if (a.matrix.format == NS_WEIGHT_NVFP4 && !pl.slot_scales)
     return fail("NVFP4 bands require per-slot block scales");
-  const uintptr_t need = a.matrix.format == NS_WEIGHT_F32 ? 4 : a.matrix.format == NS_WEIGHT_F16 ? 2 : 1;
-  if (reinterpret_cast<uintptr_t>(pl.col) % 2 || reinterpret_cast<uintptr_t>(pl.weight) % need ||
-      reinterpret_cast<uintptr_t>(pl.rows) % 4)
-    return fail("band arrays are misaligned");
+  // A lane loads its block's source indices, weight codes and block scales
+  // as runs of up to 16 bytes (lane-major slots).
+  if (reinterpret_cast<uintptr_t>(pl.col) % 16 || reinterpret_cast<uintptr_t>(pl.weight) % 16 ||
+      reinterpret_cast<uintptr_t>(pl.rows) % 4 ||
+      (pl.slot_scales && reinterpret_cast<uintptr_t>(pl.slot_scales) % 16))
+    return fail("band arrays are misaligned (col, weight and slot_scales need 16-byte alignment)");
   if (int64_t{pl.band_width} * a.state.stride_n * 4 >= int64_t{kBandOutOfRange})
     return fail("a band of the state (band width x row stride) must be under 2 GiB");
   if (static_cast<int64_t>(pl.n_row_blocks) > 0x7FFFFFFF || a.batch / 4 > 65535)

@@ -180,6 +180,9 @@ def test_band_step_validation_messages(lib):
         rc, text = band_call(args, plan)
         assert rc != 0 and message in text, (bad, text)
     plan, tables = fake_band_plan(8)
+    plan.col = tables[3].ctypes.data + 2          # lane runs need 16-byte alignment
+    assert "misaligned" in band_call(args, plan)[1]
+    plan, tables = fake_band_plan(8)
     args.matrix.format = native.WEIGHT_E4M3
     assert "global scale" in band_call(args, plan)[1]
     args, keep = fake_step_args(n=8, batch=0)
