@@ -32,12 +32,18 @@
 //    lane one 16-byte quarter of each, and each lane keeps the running sums
 //    of its quarter's four columns for the quad's four rows (16 registers);
 //    with 8 columns a pair of lanes does the same for its two rows' 32-byte
-//    source rows, and with 4 each lane loads its own 16-byte row.  A lane whose row ends early may take a
-//    second, shorter row in the group's remaining steps: at the switch step it
-//    adds its sums to the first row's LDS sums and starts again from zero.
-//    At the group's end the lane adds them to its (last) row's LDS sums.
-//  * Register blocks of up to D steps are software-pipelined: the slots of
-//    block b+1 are loaded while block b's gathers are in flight.
+//    source rows, and with 4 each lane loads its own 16-byte row.  A lane
+//    whose row ends early may take a second, shorter row in the group's
+//    remaining steps: at the switch step it adds its sums to the first row's
+//    LDS sums and starts again from zero.  At the group's end the lane adds
+//    them to its (last) row's LDS sums.
+//  * A group is cut into register blocks of D steps whose slots are
+//    lane-major, so a lane loads its D source indices and its D weight codes
+//    in one load each.  Blocks are software-pipelined: the slots of block b+1
+//    are loaded while block b's gathers are in flight, and steps past a
+//    block's count issue no gathers.  Every vector-memory instruction costs
+//    the address units cycles whatever its lanes read, so the loop is built
+//    to issue few of them.
 //  * After the last band the workgroup applies the update to its rows.
 //
 // Summation order: per row, bands in order; within a band, the row's edges in
