@@ -187,3 +187,23 @@ def test_band_empty_graph_and_isolated_rows(gpu):
         native.step(0.2, dendritic_drive=0.1)
         oracle.step(0.2, 0.1)
     assert errors(native, oracle) <= 1e-5
+
+
+@pytest.mark.parametrize("batch,n", [(8, 140_000), (4, 270_000), (16, 70_000)])
+def test_auto_takes_bands_past_the_tile_threshold(gpu, batch, n):
+    """kernel="auto" picks bands once a workgroup's column tile of the state (16, 8 or
+    4 columns) holds 4 MB, with the default band width, rows and register depth."""
+    print(f"case auto bands batch={batch} n={n}", flush=True)
+    case = make_case(n, 10 * n, 12, gpu)
+    native = NativeDendriticMatrixRuntime(case.topology, case.model,
+                                          torch.zeros(batch, n, device=gpu))
+    assert native.kernel == "bands"
+    oracle = ort.MatrixOracle(case.graph, case.params, torch.zeros(batch, n))
+    drive = column_drive(batch)
+    worst = 0.0
+    for _ in range(5):
+        native.step(drive.to(gpu), dendritic_drive=0.1)
+        oracle.step(drive, 0.1)
+        worst = max(worst, errors(native, oracle))
+    print(f"auto bands batch={batch} n={n}: {worst:.3e} over 5 ticks")
+    assert worst <= 1e-5
