@@ -52,7 +52,7 @@ def band_runtime(topology, model, state, **kwargs):
 
 @pytest.mark.parametrize("batch", [4, 8, 12, 16, 24, 32])
 @pytest.mark.parametrize("width,rows,steps", [(None, None, 8), (1000, 256, 8), (512, 64, 4),
-                                              (4096, 2496, 8), (777, 1001, 4)])
+                                              (4096, 2496, 8), (777, 1001, 4), (640, 128, 2)])
 def test_bands_match_oracle(gpu, batch, width, rows, steps):
     print(f"case bands batch={batch} width={width} rows={rows} steps={steps}", flush=True)
     graph, topology, model, params = hub_case(gpu)
@@ -87,13 +87,15 @@ def test_bands_and_rows_agree_and_repeat(gpu, batch):
     assert errors(runs["bands"], runs["rows"]) <= 2e-6
 
 
-@pytest.mark.parametrize("batch", [4, 8, 16])
+@pytest.mark.parametrize("batch,steps", [(4, None), (8, None), (16, None), (4, 2), (16, 2)])
 @pytest.mark.parametrize("fmt", ["fp16", "fp8", "nvfp4"])
-def test_band_formats_equal_decoded_fp32(gpu, fmt, batch):
+def test_band_formats_equal_decoded_fp32(gpu, fmt, batch, steps):
+    """Each format's lane runs (source indices, weight codes, NVFP4 nibbles and block
+    scales) at the default register depth and at 2 steps (runs of 1 to 4 bytes)."""
     graph, topology, model, params = hub_case(gpu, n=6000, seed=9)
     kwargs = {"weight_dtype": torch.float16} if fmt == "fp16" else {"weight_format": fmt}
     native = band_runtime(topology, model, torch.zeros(batch, 6000, device=gpu), band_width=1024,
-                          band_rows=500, **kwargs)
+                          band_rows=500, band_steps=steps, **kwargs)
     native._weights()
     if fmt == "fp16":
         decoded_host = topology.in_weight.half().float().cpu().numpy()
@@ -106,7 +108,7 @@ def test_band_formats_equal_decoded_fp32(gpu, fmt, batch):
         6000, topology.src, topology.dst,
         torch.from_numpy(decoded_host).to(gpu)[topology.out_weight_index.long()])
     reference = band_runtime(decoded, model, torch.zeros(batch, 6000, device=gpu),
-                             band_width=1024, band_rows=500)
+                             band_width=1024, band_rows=500, band_steps=steps)
     oracle = ort.MatrixOracle(graph, params, torch.zeros(batch, 6000), in_weight=decoded_host)
     drive = column_drive(batch)
     for _ in range(10):
