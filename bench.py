@@ -526,7 +526,9 @@ def measure_pels(device, theta: float = 0.02) -> dict:
 
 def measure_scaleout(device, cpu_sample: bool) -> dict:
     """N=1000000, M~100M, B=16, drive [16,1] U(0,.4) (seed 1), fp8 e4m3 weights,
-    200 graph-captured ticks; CPU oracle (fp32, decoded weights) on 10 ticks."""
+    200 graph-captured ticks; CPU oracle (fp32, decoded weights) on 10 ticks.  The
+    same graph is also timed at B=8 and B=4 (100 ticks each, auto kernel and row
+    blocks) under `narrow_batches`."""
     n, candidates, batch = 1_000_000, 100_000_000, 16
     log("scale-out: drawing N=1000000 M=100M candidates on the host, coalescing on the GPU")
     torch.cuda.synchronize()
@@ -559,6 +561,23 @@ def measure_scaleout(device, cpu_sample: bool) -> dict:
                                             weight_format="fp8", kernel="rows")
         result["rows_kernel_ms_per_tick"] = round(rollout_ms(rows, 100, 2, drive.to(device), 0.1), 5)
         runtime = rows
+    # The same graph at batches 8 and 4 (band tiles of 8 and 4 columns), auto kernel
+    # and row blocks, 100 graph-replayed ticks each.
+    del runtime
+    runtime = None
+    narrow = {}
+    for b in (8, 4):
+        entry = {}
+        for kernel in ("auto", "rows"):
+            rt = NativeDendriticMatrixRuntime(topology, model, torch.zeros(b, n, device=device),
+                                              weight_format="fp8", kernel=kernel)
+            key = "ms_per_tick" if kernel == "auto" else "rows_kernel_ms_per_tick"
+            if kernel == "auto":
+                entry["kernel"] = rt.kernel
+            entry[key] = round(rollout_ms(rt, 50, 2, column_drive(b).to(device), 0.1), 5)
+            del rt
+        narrow[str(b)] = entry
+    result["narrow_batches"] = narrow
     if cpu_sample:
         log("scale-out: timing the CPU oracle on 10 ticks")
         from neurosim_gpu.precision import quantize_dequantize
@@ -568,7 +587,6 @@ def measure_scaleout(device, cpu_sample: bool) -> dict:
         result["cpu_baseline"] = {"value": round(cpu_ms, 1), "unit": "ms/tick", "cores": threads,
                                   "kind": "port", "sample": "10 fp32 ticks on the decoded fp8 "
                                   "weights, torch CPU CSR product + elementwise update"}
-    del runtime
     torch.cuda.empty_cache()
     return result
 
