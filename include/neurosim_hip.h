@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 15
+#define NS_ABI_VERSION 16
 
 /* Return codes. */
 #define NS_OK 0
@@ -445,7 +445,8 @@ int ns_dendritic_step(const ns_step_args* args, void* stream);
 
 /* Host-side band planner for a host copy of (rowptr, col): `band_width`
  * sources per band (1..65535), `block_rows` destination rows per workgroup
- * (1..ns_band_max_block_rows()), register blocks of at most `block_steps`
+ * (1..4095; the tick takes at most ns_band_max_block_rows(batch)), register
+ * blocks of at most `block_steps`
  * steps (1..8).  Call once with all output pointers NULL to get the sizes in
  * *plan (n_bands, n_row_blocks, n_blocks, n_groups, n_slots), then again with
  * wave_blocks int32[NS_BAND_WAVES*n_row_blocks+1], blocks int32[4*(n_blocks+1)], rows
@@ -458,8 +459,10 @@ int ns_plan_bands(const int32_t* rowptr_host, const int32_t* col_host, int64_t n
                   ns_band_plan* plan, int32_t* wave_blocks, int32_t* blocks, uint32_t* rows,
                   int32_t* perm, uint16_t* col);
 
-/* Largest block_rows the band kernel's LDS holds. */
-int32_t ns_band_max_block_rows(void);
+/* Largest block_rows the band tick takes at this batch: its LDS holds each
+ * row's sums over the workgroup's column tile, 2496 rows of 16 columns, 4095
+ * (the lane word's limit) of 8 or 4. */
+int32_t ns_band_max_block_rows(int64_t batch);
 
 /* Fused matrix tick over a band layout (batch a multiple of 4, state
  * neuron-major with 16-byte aligned rows; workgroups take 16 state columns

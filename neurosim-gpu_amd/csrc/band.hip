@@ -392,7 +392,7 @@ hipError_t launch_bands(const BandArgs& A, int fmt, int n_row_blocks, hipStream_
 
 template <int D, int C>
 hipError_t allow_band_lds() {
-  const int bytes = kBandMaxBlockRows * C * static_cast<int>(sizeof(float));
+  const int bytes = band_max_rows(C) * C * static_cast<int>(sizeof(float));
   const void* kernels[4] = {reinterpret_cast<const void*>(&band_tick_kernel<NS_WEIGHT_F32, D, C>),
                             reinterpret_cast<const void*>(&band_tick_kernel<NS_WEIGHT_F16, D, C>),
                             reinterpret_cast<const void*>(&band_tick_kernel<NS_WEIGHT_E4M3, D, C>),
@@ -425,8 +425,9 @@ int band_step(const ns_step_args& a, const ns_band_plan& pl, hipStream_t stream)
   if (pl.n_bands != (a.n_neurons + pl.band_width - 1) / pl.band_width)
     return fail("%d bands of width %d do not cover N=%lld", pl.n_bands, pl.band_width,
                 (long long)a.n_neurons);
-  if (pl.block_rows < 1 || pl.block_rows > kBandMaxBlockRows)
-    return fail("block_rows must be in [1, %d]", kBandMaxBlockRows);
+  if (pl.block_rows < 1 || pl.block_rows > band_max_rows(a.batch))
+    return fail("block_rows must be in [1, %d] at batch %lld", band_max_rows(a.batch),
+                (long long)a.batch);
   if (pl.n_row_blocks != (a.n_neurons + pl.block_rows - 1) / pl.block_rows)
     return fail("%d row blocks of %d rows do not cover N=%lld", pl.n_row_blocks, pl.block_rows,
                 (long long)a.n_neurons);

@@ -2,6 +2,8 @@
 // C++: the planners compile without the HIP headers).
 #pragma once
 
+#include <cstdint>
+
 namespace ns {
 
 constexpr int kThreads = 256;   // 4 wavefronts of 64 lanes
@@ -18,6 +20,7 @@ constexpr int kPanelMaxPrefetch = 16;                  // steps per register blo
 constexpr int kPanelTailSlots = 2 * kPanelMaxPrefetch * 64;
 constexpr int kBandWaves = 16;                          // wavefronts per band workgroup (one per CU)
 constexpr int kBandMaxBlockRows = 2496;                 // 16 float row sums each in LDS (156 KB)
+constexpr int kBandMaxNarrowRows = 4095;                // 8 or 4 sums each (128 KB at 8), the lane word's limit
 constexpr int kBandMaxBlockSteps = 8;                   // steps per register block, at most
 // A band lane word: first row (bits 0-11), second row (bits 12-23) and the
 // step at which the lane moves on to its second row (bits 24-31).
@@ -25,5 +28,12 @@ constexpr unsigned kBandNoRow = 0xFFF;
 constexpr int kBandRowBits = 12;
 constexpr int kBandMaxSwitch = 255;
 static_assert(kBandMaxBlockRows <= static_cast<int>(kBandNoRow), "block rows fit a lane word");
+static_assert(kBandMaxNarrowRows <= static_cast<int>(kBandNoRow), "block rows fit a lane word");
+
+// Most destination rows per band workgroup for a batch: its LDS holds each
+// row's sums over the workgroup's column tile (16 columns, or 8 or 4).
+constexpr int band_max_rows(int64_t batch) {
+  return batch % 16 == 0 ? kBandMaxBlockRows : kBandMaxNarrowRows;
+}
 
 }  // namespace ns

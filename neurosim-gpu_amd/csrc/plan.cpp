@@ -607,7 +607,7 @@ void append_band_block(BandLayout& out, const int32_t* rowptr, const int32_t* co
 
 }  // namespace
 
-extern "C" int32_t ns_band_max_block_rows(void) { return kBandMaxBlockRows; }
+extern "C" int32_t ns_band_max_block_rows(int64_t batch) { return band_max_rows(batch); }
 
 extern "C" int ns_plan_bands(const int32_t* rowptr, const int32_t* col, int64_t n_rows,
                              int32_t band_width, int32_t block_rows, int32_t block_steps,
@@ -621,8 +621,8 @@ extern "C" int ns_plan_bands(const int32_t* rowptr, const int32_t* col, int64_t 
     if (rowptr[r + 1] < rowptr[r]) return fail("rowptr must be non-decreasing");
   if (rowptr[n_rows] > 0 && !col) return fail("col is required");
   if (band_width < 1 || band_width > 65535) return fail("band_width must be in [1, 65535]");
-  if (block_rows < 1 || block_rows > kBandMaxBlockRows)
-    return fail("block_rows must be in [1, %d]", kBandMaxBlockRows);
+  if (block_rows < 1 || block_rows > kBandMaxNarrowRows)
+    return fail("block_rows must be in [1, %d]", kBandMaxNarrowRows);
   if (block_steps < 1 || block_steps > kBandMaxBlockSteps)
     return fail("block_steps must be in [1, %d]", kBandMaxBlockSteps);
   for (int64_t e = 0; e < rowptr[n_rows]; ++e)

@@ -35,7 +35,7 @@ import numpy as np
 import torch
 
 _LIB_NAME = "libneurosim_hip.so"
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 WEIGHT_F32, WEIGHT_F16, WEIGHT_E4M3, WEIGHT_NVFP4 = 0, 1, 2, 3
 _PLAN_CACHE = 64   # row plans kept per extension (one per live topology and batch width)
@@ -187,7 +187,7 @@ def load_library() -> ctypes.CDLL:
     lib.ns_plan_bands.argtypes = [_c_ptr, _c_ptr, _c_i64, ctypes.c_int32, ctypes.c_int32,
                                   ctypes.c_int32, ctypes.POINTER(_BandPlan)] + [_c_ptr] * 5
     lib.ns_band_max_block_rows.restype = ctypes.c_int32
-    lib.ns_band_max_block_rows.argtypes = []
+    lib.ns_band_max_block_rows.argtypes = [_c_i64]
     lib.ns_dendritic_step_bands.restype = ctypes.c_int
     lib.ns_dendritic_step_bands.argtypes = [ctypes.POINTER(_StepArgs), ctypes.POINTER(_BandPlan),
                                             _c_ptr]
@@ -447,8 +447,10 @@ def plan_bands_host(rowptr: torch.Tensor, col: torch.Tensor, band_width: int, bl
     return plan, wave_blocks, blocks, rows, perm, cols
 
 
-def band_max_block_rows() -> int:
-    return int(load_library().ns_band_max_block_rows())
+def band_max_block_rows(batch: int = 16) -> int:
+    """Most destination rows per band workgroup at this batch (its LDS holds the
+    rows' sums over a tile of 16, 8 or 4 columns)."""
+    return int(load_library().ns_band_max_block_rows(batch))
 
 
 def _device_tensor(array: np.ndarray, device) -> torch.Tensor:
@@ -593,11 +595,13 @@ BAND_WIDTH = 53248
 BAND_WAVES = 16
 
 
-def default_band_rows(n: int, units: int) -> int:
+def default_band_rows(n: int, units: int, batch: int = 16) -> int:
     """Destination rows per band workgroup: one workgroup per compute unit, in
     whole rounds (the grid is a multiple of ``units``), as few rounds as fit LDS.
-    Workgroups of one round start together and so walk the bands together."""
-    limit = band_max_block_rows()
+    Workgroups of one round start together and so walk the bands together, and
+    each round reads the bands into L2 once more: at N=1M, 8-column tiles fit one
+    round of 3907 rows (560 us per tick against 579 for two rounds of 1954)."""
+    limit = band_max_block_rows(batch)
     rounds = 1
     while -(-n // (units * rounds)) > limit:
         rounds += 1
@@ -611,15 +615,16 @@ class BandLayout(_SlotLayout):
     in_col (a synchronisation; set-up only).  Holds the device tables, the
     slot permutation and, per weight version and encoding, the weights
     rearranged into slot order on the device.  ``block_rows`` defaults to
-    ``default_band_rows``.
+    ``default_band_rows`` for ``batch``.
     """
 
     def __init__(self, topology, device, *, band_width: int = BAND_WIDTH,
-                 block_rows: int | None = None, block_steps: int = 4) -> None:
+                 block_rows: int | None = None, block_steps: int = 4,
+                 batch: int = 16) -> None:
         n = topology.n_neurons
         if block_rows is None:
             units = torch.cuda.get_device_properties(device).multi_processor_count
-            block_rows = default_band_rows(n, units)
+            block_rows = default_band_rows(n, units, batch)
         plan, wave_blocks, blocks, rows, perm, cols = plan_bands_host(
             topology.in_rowptr, topology.in_col, band_width, block_rows, block_steps)
         self.n = n

@@ -345,7 +345,8 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         self._panel_width = panel_width
         self._bands = (BandLayout(topology, initial_state.device,
                                   band_width=band_width or BAND_WIDTH, block_rows=band_rows,
-                                  block_steps=band_steps or default_band_steps(batch))
+                                  block_steps=band_steps or default_band_steps(batch),
+                                  batch=batch)
                        if use_bands else None)
 
     def _invalidate_precision_cache(self) -> None:

@@ -187,7 +187,7 @@ def test_band_step_validation_messages(lib):
     assert "global scale" in band_call(args, plan)[1]
     args, keep = fake_step_args(n=8, batch=0)
     assert band_call(args, plan) == (0, "")
-    assert lib.ns_band_max_block_rows() == 2496
+    assert [lib.ns_band_max_block_rows(b) for b in (16, 32, 8, 4, 12)] == [2496, 2496] + [4095] * 3
 
 
 def test_empty_batch_is_a_no_op(lib):

@@ -226,7 +226,7 @@ def test_band_planner_rejects_bad_arguments():
     assert rc()[0] == 0
     assert "band_width" in rc(width=0)[1] and "band_width" in rc(width=65536)[1]
     assert "block_rows" in rc(rows=0)[1]
-    assert "block_rows" in rc(rows=band_max_block_rows() + 1)[1]
+    assert "block_rows" in rc(rows=band_max_block_rows(8) + 1)[1]
     assert "block_steps" in rc(steps=0)[1] and "block_steps" in rc(steps=9)[1]
     bad = rowptr.copy()
     bad[5] = bad[6] + 1
