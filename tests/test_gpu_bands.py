@@ -52,7 +52,8 @@ def band_runtime(topology, model, state, **kwargs):
 
 @pytest.mark.parametrize("batch", [4, 8, 12, 16, 24, 32])
 @pytest.mark.parametrize("width,rows,steps", [(None, None, 8), (1000, 256, 8), (512, 64, 4),
-                                              (4096, 2496, 8), (777, 1001, 4), (640, 128, 2)])
+                                              (4096, 2496, 8), (777, 1001, 4), (640, 128, 2),
+                                              (333, 32, 4)])   # 375 row blocks, two rounds
 def test_bands_match_oracle(gpu, batch, width, rows, steps):
     print(f"case bands batch={batch} width={width} rows={rows} steps={steps}", flush=True)
     graph, topology, model, params = hub_case(gpu)
