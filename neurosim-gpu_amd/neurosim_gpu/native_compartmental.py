@@ -23,6 +23,7 @@ library raises at construction, nothing falls back silently.
 
 from __future__ import annotations
 
+import warnings
 from types import SimpleNamespace
 
 import torch
@@ -338,6 +339,7 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
                                     pairs=panel_pairs)
                         if use_panels else None)
         self.source_major_weights = SourceMajorWeights()
+        self._unversioned_warned = False
         self._recorded_key, self._recorded_source, self._recorded_seen = None, None, 0
         # The backward's transposed product on panels (False: the out-edge walk).
         self.transposed_panels_enabled = True
@@ -390,6 +392,7 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
 
     def _band_plan(self, weight: torch.Tensor, scales: tuple):
         """ctypes band plan for this tick's weights (rebuilt when the weights change)."""
+        self._warn_if_unversioned(weight)
         key = (self.topology.weight_version, self.checkpoint_precision) + _weight_key(weight)
         return self._slot_plan(self._bands, key, weight, scales)
 
@@ -397,8 +400,26 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         """ctypes panel plan for this tick's weights (rebuilt when the weights
         change: a new topology weight version, or the payload replaced or
         modified in place)."""
+        self._warn_if_unversioned(weight)
         key = (self.topology.weight_version, self.checkpoint_precision) + _weight_key(weight)
         return self._slot_plan(self._panels, key, weight, scales)
+
+    def _warn_if_unversioned(self, weight: torch.Tensor) -> None:
+        """Warn once per runtime when float32 panel or band ticks run over an
+        ``in_weight`` made under torch.inference_mode: PyTorch keeps no version
+        counter for such a tensor, so an in-place edit of it is not seen by the
+        slot-order copy these kernels read, while the reference's float32 tick
+        reads ``in_weight`` afresh every tick.  (Reduced encodings follow the
+        topology's weight version, as the reference's do.)"""
+        if (self._unversioned_warned or self.checkpoint_precision != "fp32"
+                or not torch.is_inference(weight)):
+            return
+        self._unversioned_warned = True
+        warnings.warn(
+            "in_weight was created under torch.inference_mode and has no version counter: "
+            f"the {self.kernel} tick reads a slot-order copy of it, so after editing "
+            "in_weight in place call topology.mark_weights_mutated_() (or "
+            "apply_source_weights_) before the next step", RuntimeWarning, stacklevel=4)
 
     @property
     def checkpoint_precision(self) -> str:

@@ -130,3 +130,44 @@ def with_weights(graph: Graph, canonical_weight: np.ndarray) -> Graph:
     in_weight[graph.out_weight_index] = canonical_weight
     return Graph(graph.n, graph.src, graph.dst, canonical_weight.copy(), graph.out_rowptr,
                  graph.in_rowptr, graph.in_col, in_weight, graph.out_weight_index)
+
+
+def with_in_weight(graph: Graph, in_weight: np.ndarray) -> Graph:
+    """The same structure with new destination-major weights (e.g. decoded ones)."""
+    in_weight = np.asarray(in_weight)
+    return Graph(graph.n, graph.src, graph.dst, in_weight[graph.out_weight_index].copy(),
+                 graph.out_rowptr, graph.in_rowptr, graph.in_col, in_weight.copy(),
+                 graph.out_weight_index)
+
+
+def block_diagonal(graphs: list[Graph]) -> Graph:
+    """The disjoint union of graphs: graph k's neurons are numbered after those
+    of graphs 0..k-1, so W is block diagonal and both CSR views keep every
+    row's edges in their original order.  A CSR product's row sum reads only
+    its own row, so each block of a tick over the union evolves exactly as its
+    graph would alone (tests/test_oracle_runtime.py checks this bitwise)."""
+    offsets = np.cumsum([0] + [g.n for g in graphs])
+    edge_offsets = np.cumsum([0] + [g.n_edges for g in graphs])
+
+    def cat(name, shift=None):
+        if shift is None:
+            return np.concatenate([getattr(g, name) for g in graphs])
+        return np.concatenate([getattr(g, name).astype(np.int64) + shift[k]
+                               for k, g in enumerate(graphs)])
+
+    def rowptr(name):
+        parts = [np.zeros(1, np.int64)] + [getattr(g, name)[1:].astype(np.int64) + edge_offsets[k]
+                                           for k, g in enumerate(graphs)]
+        return np.concatenate(parts).astype(np.int32)
+
+    return Graph(
+        n=int(offsets[-1]),
+        src=cat("src", offsets).astype(np.int32),
+        dst=cat("dst", offsets).astype(np.int32),
+        weight=cat("weight"),
+        out_rowptr=rowptr("out_rowptr"),
+        in_rowptr=rowptr("in_rowptr"),
+        in_col=cat("in_col", offsets).astype(np.int32),
+        in_weight=cat("in_weight"),
+        out_weight_index=cat("out_weight_index", edge_offsets).astype(np.int32),
+    )

@@ -67,6 +67,7 @@ CASES = [
     (2000, 30000, 5, ((0, 4000),), 2000, 2000, 8),      # one band, one block
     (1000, 0, 6, (), 100, 64, 8),                       # no edges
     (4000, 20000, 7, (), 50, 1, 8),                     # one row per block
+    (12000, 96000, 8, ((0, 9000), (3, 6000)), 2000, 4095, 8),  # 12-bit row limit
 ]
 
 

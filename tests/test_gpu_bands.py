@@ -20,6 +20,7 @@ from oracle import precision as op
 from oracle import runtime as ort
 from oracle import topology as otop
 from neurosim_gpu import NativeDendriticMatrixRuntime, SparseTopology, topology_to
+from neurosim_gpu.native import band_max_block_rows as native_band_limit
 from neurosim_gpu.rollout import MatrixRollout
 
 pytestmark = pytest.mark.gpu
@@ -69,6 +70,31 @@ def test_bands_match_oracle(gpu, batch, width, rows, steps):
     layout = native._bands
     print(f"bands batch={batch} width={width}: {worst:.3e} over 30 ticks ({layout.n_bands} bands, "
           f"{layout.n_row_blocks} row blocks, {layout.n_blocks} register blocks)")
+    assert worst <= 1e-5
+
+
+@pytest.mark.parametrize("batch", [4, 8, 12, 24])
+@pytest.mark.parametrize("width", [None, 2000])
+def test_bands_at_the_largest_row_block(gpu, batch, width):
+    """8- and 4-column tiles (batch 24 and 8, 12 and 4) at 4095 rows per block, the
+    most a lane word's 12-bit row index holds next to the 0xFFF no-row sentinel:
+    the hub graph's first two blocks use row indices up to 4094, and its short
+    rows take second rows in their lanes."""
+    rows = 4095
+    assert native_band_limit(batch) >= rows
+    print(f"case bands batch={batch} width={width} rows={rows}", flush=True)
+    graph, topology, model, params = hub_case(gpu)
+    drive = column_drive(batch)
+    native = band_runtime(topology, model, torch.zeros(batch, graph.n, device=gpu),
+                          band_width=width, band_rows=rows)
+    assert native._bands.block_rows == rows and native._bands.n_row_blocks == 3
+    oracle = ort.MatrixOracle(graph, params, torch.zeros(batch, graph.n))
+    worst = 0.0
+    for _ in range(30):
+        native.step(drive.to(gpu), dendritic_drive=0.1)
+        oracle.step(drive, 0.1)
+        worst = max(worst, errors(native, oracle))
+    print(f"bands batch={batch} width={width} rows={rows}: {worst:.3e} over 30 ticks")
     assert worst <= 1e-5
 
 

@@ -197,6 +197,42 @@ def test_panel_fp32_follows_in_place_edits_of_in_weight(gpu):
     assert errors(native, oracle) <= 1e-5
 
 
+def test_panel_fp32_warns_once_about_inference_mode_weights(gpu):
+    """An in_weight made under torch.inference_mode has no version counter, so the
+    slot-order copy cannot see an in-place edit: the runtime says so, once; after
+    mark_weights_mutated_() the edit takes effect.  Versioned weights do not warn."""
+    import dataclasses
+    import warnings
+
+    case = make_case(3000, 60_000, 4, gpu)
+    with torch.inference_mode():
+        frozen = case.topology.in_weight.clone()
+    topology = dataclasses.replace(case.topology, in_weight=frozen)
+    native = NativeDendriticMatrixRuntime(topology, case.model, torch.zeros(1, 3000, device=gpu),
+                                          kernel="panels", panel_width=512, panel_tiles=4)
+    oracle = ort.MatrixOracle(case.graph, case.params, torch.zeros(1, 3000))
+    with warnings.catch_warnings(record=True) as caught:
+        warnings.simplefilter("always")
+        for tick in range(8):
+            if tick == 4:
+                with torch.inference_mode():
+                    frozen.mul_(0.5)
+                topology.mark_weights_mutated_()
+                oracle.matrix = ort.csr_matrix(case.graph, torch.float32, frozen.cpu().numpy())
+            native.step(0.2, dendritic_drive=0.1)
+            oracle.step(0.2, 0.1)
+    notes = [w for w in caught if "inference_mode" in str(w.message)]
+    assert len(notes) == 1 and issubclass(notes[0].category, RuntimeWarning)
+    assert errors(native, oracle) <= 1e-5
+    versioned = NativeDendriticMatrixRuntime(case.topology, case.model,
+                                             torch.zeros(1, 3000, device=gpu), kernel="panels",
+                                             panel_width=512, panel_tiles=4)
+    with warnings.catch_warnings(record=True) as caught:
+        warnings.simplefilter("always")
+        versioned.step(0.2, dendritic_drive=0.1)
+    assert not [w for w in caught if "inference_mode" in str(w.message)]
+
+
 def test_panel_weight_refresh_after_mutation(gpu):
     case = make_case(3000, 60_000, 4, gpu)
     native = NativeDendriticMatrixRuntime(case.topology, case.model, torch.zeros(1, 3000, device=gpu),

@@ -112,3 +112,61 @@ def test_brainwaves_trajectory_fp32():
     assert np.abs(driven - gold["driven_mean"]).max() < 5e-7
     assert np.abs(zero - gold["zero_mean"]).max() < 5e-7
     assert zero[-512:].mean() == meta["mean_last_512_ticks"]["zero_input"] == 0.0
+
+
+def test_block_diagonal_union_evolves_each_block_exactly_as_alone():
+    """The long-horizon drift tests run several graphs (seeds, and each weight
+    mode's decoded weights) as one oracle over their block-diagonal union.  Each
+    block must follow its own graph's run bit for bit, at the drift tests' shape."""
+    from oracle import precision as op
+    n, edges, batch, ticks = 1024, 16_384, 4, 60
+    base = [otop.random_graph(n, edges, seed=seed, weight_scale=0.15) for seed in (11, 23)]
+    graphs = [otop.with_in_weight(g, op.quantize_dequantize(g.in_weight, mode))
+              for g in base for mode in ("fp32", "fp16", "fp8", "nvfp4")]
+    union = otop.block_diagonal(graphs)
+    assert union.n == n * len(graphs) and union.n_edges == sum(g.n_edges for g in graphs)
+    key = union.src.astype(np.int64) * union.n + union.dst
+    assert (np.diff(key) > 0).all()
+    assert np.array_equal(union.in_weight[union.out_weight_index], union.weight)
+
+    def params(count):
+        full = lambda value: torch.full((n * count,), value)
+        return od.from_time_constants(full(0.72), full(0.8), dt=1.0, tau_dendrite=4.0,
+                                      tau_adaptation=20.0, coupling=0.45,
+                                      adaptation_strength=0.15)
+
+    gen = torch.Generator().manual_seed(3)
+    drives = torch.rand((ticks, batch, n), generator=gen) * 0.4
+    joint = ort.MatrixOracle(union, params(len(graphs)), torch.full((batch, union.n), 0.25))
+    alone = [ort.MatrixOracle(g, params(1), torch.full((batch, n), 0.25)) for g in graphs]
+    for t in range(ticks):
+        joint.step(drives[t].repeat(1, len(graphs)), 0.05)
+        for run in alone:
+            run.step(drives[t], 0.05)
+    for name in ("state", "dendritic_state", "adaptation_state"):
+        expected = torch.cat([getattr(run, name) for run in alone], dim=1)
+        assert torch.equal(getattr(joint, name), expected), name
+    # The blocks are really different runs (decoded weights change the states).
+    assert not torch.equal(alone[0].state, alone[2].state)
+
+
+def test_block_diagonal_catches_a_shifted_column():
+    # Plant a mistake: the second block's sources not shifted.  Its rows then
+    # read the first block's states, which must show.
+    graphs = [otop.random_graph(40, 200, seed=s) for s in (1, 2)]
+    union = otop.block_diagonal(graphs)
+    wrong_col = union.in_col.copy()
+    start = union.in_rowptr[40]
+    wrong_col[start:] -= 40
+    wrong = otop.Graph(union.n, union.src, union.dst, union.weight, union.out_rowptr,
+                       union.in_rowptr, wrong_col, union.in_weight, union.out_weight_index)
+    full = lambda value: torch.full((80,), value)
+    p = od.from_time_constants(full(0.72), full(0.8), dt=1.0, tau_dendrite=4.0,
+                               tau_adaptation=20.0)
+    initial = torch.cat([torch.full((1, 40), 0.1), torch.full((1, 40), 0.6)], dim=1)
+    right = ort.MatrixOracle(union, p, initial)
+    bad = ort.MatrixOracle(wrong, p, initial)
+    for _ in range(3):
+        right.step(0.1)
+        bad.step(0.1)
+    assert float((right.state[:, 40:] - bad.state[:, 40:]).abs().max()) > 1e-4

@@ -48,9 +48,11 @@ def encode(lib, weight: torch.Tensor, fmt: str, no_alloc: bool):
 def test_no_alloc_encoder_equals_the_workspace_encoder(gpu, fmt):
     lib = native.load_library()
     rng = np.random.default_rng(17)
-    # First a large call (1024 partials), then a smaller one with a larger
-    # amax: stale partials of the first call must not leak into the second.
-    for m, sigma in ((3_000_001, 0.05), (1_003, 3.0)):
+    # First a large call with a large amax (1024 partials), then a smaller one
+    # with a small amax: the encoder takes the max over its partials, so a
+    # stale partial of the first call read by the second would raise the
+    # second call's global scale and change every code.
+    for m, sigma in ((3_000_001, 3.0), (1_003, 0.05)):
         print(f"case no-alloc encode fmt={fmt} M={m}", flush=True)
         host = (rng.standard_normal(m) * sigma).astype(np.float32)
         weight = torch.from_numpy(host).to(gpu)
