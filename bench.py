@@ -512,6 +512,14 @@ def measure_pels(device, theta: float = 0.02) -> dict:
                                                theta=0.0, propagation=propagation)
             result[name] = phase(0.2, 0.1, exact)
             del exact
+    # propagation="auto": the eager ticks that count each regime's activity also
+    # let the policy sample it; the captured ticks keep the path it chose.
+    for name, value in (("driven_onset_auto", theta), ("theta0_driven_onset_auto", 0.0)):
+        chooser = NativeDendriticPELSRuntime(topology, model, torch.zeros(1, n, device=device),
+                                             theta=value, propagation="auto")
+        result[name] = phase(0.2, 0.1, chooser)
+        result[name]["path"] = chooser.selected_path
+        del chooser
     del two_launch
     with torch.inference_mode():
         for _ in range(512):

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 16
+#define NS_ABI_VERSION 17
 
 /* Return codes. */
 #define NS_OK 0
@@ -261,7 +261,9 @@ typedef struct ns_event_args {
      stores j into `current` and zeroes pending_in; the emitters' out-edges are
      added into pending_out, which must be zero on entry.  The caller swaps the
      two buffers between ticks, or adds pending_out into `current` and zeroes
-     it.  `delta` is not used. */
+     it.  `delta` is not used.  With NS_EVENT_ADVANCE_ONLY, pending_in alone
+     may be given (pending_out NULL): the launch folds it into `current` the
+     same way and writes the deltas to `delta`. */
   float* pending_in;
   float* pending_out;
   /* Optional: the weights in source-major order, out_weight[e] ==
@@ -270,7 +272,18 @@ typedef struct ns_event_args {
   const float* out_weight;
   int32_t flags;               /* NS_EVENT_* */
   int32_t reserved;
+  /* Optional, one-launch forms only (pending_in given): counters of
+     int64[NS_EVENT_ACTIVITY_SLOTS * NS_EVENT_ACTIVITY_STRIDE].  The tick adds
+     the out-degree of every active (neuron, column) pair, |s' - emitted| >=
+     theta, to counter k * NS_EVENT_ACTIVITY_STRIDE for some k below
+     NS_EVENT_ACTIVITY_SLOTS; the sum of those counters grows by the tick's
+     active out-edges, the reference's PELS policy measure (runtime.py:129-165).
+     The caller zeroes and reads them (NULL: not counted). */
+  int64_t* activity;
 } ns_event_args;
+
+#define NS_EVENT_ACTIVITY_SLOTS 32
+#define NS_EVENT_ACTIVITY_STRIDE 16
 
 /* ns_event_args flag: run the advance and emission only (the two-launch
  * tick's first kernel; `delta` required, one-launch buffers not allowed) and

@@ -48,6 +48,7 @@ struct EventArgs {
   const float* out_weight;
   float* pending_in;
   float* pending_out;
+  unsigned long long* activity;
 };
 
 // Everything pair (n, b) reads besides its current.
@@ -62,15 +63,18 @@ __device__ __forceinline__ PairInputs load_pair(const EventArgs& A, int64_t n, i
 }
 
 // Advances pair (n, b) on current j, stores the three states and the
-// emitted state, and returns the pair's delta.
+// emitted state, and returns the pair's delta; `active` tells whether the
+// residual reached the threshold (the reference's emission mask, which at
+// theta = 0 includes pairs whose residual is zero).
 __device__ __forceinline__ float advance_loaded_pair(const EventArgs& A, int64_t n, int64_t b,
-                                                     float j, const PairInputs& in) {
+                                                     float j, const PairInputs& in,
+                                                     bool& active) {
   const NextState x = advance_loaded(in.p, j, in.s, in.d, in.a, in.u, in.v);
   float dl;
   {
 #pragma clang fp contract(off)
     const float residual = x.soma - in.emitted;
-    const bool active = fabsf(residual) >= in.theta;
+    active = fabsf(residual) >= in.theta;
     dl = active ? residual : 0.0f;
     A.oe.put(b, n, in.emitted + dl);
   }
@@ -82,7 +86,8 @@ __device__ __forceinline__ float advance_loaded_pair(const EventArgs& A, int64_t
 
 __device__ __forceinline__ float advance_pair(const EventArgs& A, int64_t n, int64_t b,
                                               float j) {
-  return advance_loaded_pair(A, n, b, j, load_pair(A, n, b));
+  bool active;
+  return advance_loaded_pair(A, n, b, j, load_pair(A, n, b), active);
 }
 
 __global__ __launch_bounds__(kThreads) void event_advance_kernel(EventArgs A) {
@@ -174,12 +179,41 @@ __global__ __launch_bounds__(kThreads) void event_scatter_kernel(EventArgs A) {
   scatter_chunk(A, chunk, lane, mine, start, end, A.current, A.csb, A.csn);
 }
 
-// The one-launch tick: one lane per pair, one wavefront per 64 pairs.
+// Adds the out-degrees of a workgroup's active pairs (`edges` per lane) to
+// one of NS_EVENT_ACTIVITY_SLOTS counters, NS_EVENT_ACTIVITY_STRIDE apart
+// (workgroup w uses slot w mod the slot count): a wavefront sum by
+// shuffles, then one atomic per workgroup, so that few workgroups meet on one
+// address.  Every lane of the workgroup must call it.
+__device__ __forceinline__ void count_activity(const EventArgs& A, int64_t edges) {
+  __shared__ unsigned long long wave_sum[kThreads / 64];
+  unsigned long long v = static_cast<unsigned long long>(edges);
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
+  if ((threadIdx.x & 63) == 0) wave_sum[threadIdx.x >> 6] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long total = 0;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) total += wave_sum[w];
+    if (total)
+      __hip_atomic_fetch_add(A.activity + (blockIdx.x % NS_EVENT_ACTIVITY_SLOTS) *
+                                              NS_EVENT_ACTIVITY_STRIDE,
+                             total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// The one-launch tick: one lane per pair, one wavefront per 64 pairs.  It
+// reads j = current + pending_in and folds it into the current.  kScatter:
+// the wavefront scatters its deltas into pending_out; else (the fused
+// advance-only tick) the deltas go to `delta` for the caller to propagate.
+// kCount: the out-degrees of the active pairs are added to `activity`.
+template <bool kScatter, bool kCount>
 __global__ __launch_bounds__(kThreads) void event_tick_kernel(EventArgs A) {
   const int lane = threadIdx.x & 63;
   const int64_t chunk = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) >> 6;
   const int64_t i = chunk * 64 + lane;
   float dl = 0.0f;
+  bool active = false;
   int64_t start = 0, end = 0;
   if (i < A.count) {
     const int64_t n = i / A.B;
@@ -194,9 +228,11 @@ __global__ __launch_bounds__(kThreads) void event_tick_kernel(EventArgs A) {
     const float j = current + pending;
     *at = j;
     A.pending_in[i] = 0.0f;
-    dl = advance_loaded_pair(A, n, b, j, in);
+    dl = advance_loaded_pair(A, n, b, j, in, active);
+    if constexpr (!kScatter) A.delta[i] = dl;
   }
-  scatter_chunk(A, chunk, lane, dl, start, end, A.pending_out, 1, A.B);
+  if constexpr (kCount) count_activity(A, active ? end - start : 0);
+  if constexpr (kScatter) scatter_chunk(A, chunk, lane, dl, start, end, A.pending_out, 1, A.B);
 }
 
 }  // namespace ns
@@ -234,24 +270,30 @@ extern "C" int ns_dendritic_event(const ns_event_args* args, void* stream) {
     return fail("four output planes are required");
   if (a.flags & ~NS_EVENT_ADVANCE_ONLY) return fail("unknown event flags %d", a.flags);
   const bool advance_only = (a.flags & NS_EVENT_ADVANCE_ONLY) != 0;
-  const bool fused = a.pending_in || a.pending_out;
-  if (fused && !(a.pending_in && a.pending_out))
-    return fail("pending_in and pending_out go together");
-  if (fused && advance_only) return fail("the advance-only tick takes no pending buffers");
-  if (!fused && !a.delta) return fail("a delta workspace is required");
-  const int64_t B = a.batch, N = a.n_neurons;
-  // Written memory: the four planes, then the delta workspace or the two
-  // pending buffers (entry n*B + b).
-  Extent outs[6] = {extent(a.out_state, B, N), extent(a.out_dendrite, B, N),
-                    extent(a.out_adaptation, B, N), extent(a.out_emitted, B, N)};
-  int n_outs = 5;
-  if (fused) {
-    outs[4] = extent_of(a.pending_in, 1, B, B, N);
-    outs[5] = extent_of(a.pending_out, 1, B, B, N);
-    n_outs = 6;
+  // The one-launch forms read j = current + pending_in; the scattering one
+  // also needs pending_out, the advance-only one writes `delta` instead.
+  const bool fused = a.pending_in != nullptr;
+  if (advance_only) {
+    if (a.pending_out) return fail("the advance-only tick scatters nothing: pending_out must be NULL");
+    if (!a.delta) return fail("a delta workspace is required");
   } else {
-    outs[4] = extent_of(a.delta, N, 1, B, N);
+    if (fused != (a.pending_out != nullptr)) return fail("pending_in and pending_out go together");
+    if (!fused && !a.delta) return fail("a delta workspace is required");
   }
+  if (a.activity && !fused)
+    return fail("activity counts need the one-launch tick (pending_in)");
+  const int64_t B = a.batch, N = a.n_neurons;
+  // Written memory: the four planes, then the workspaces (pending buffers and
+  // delta, entry n*B + b) and the activity counters.
+  Extent outs[8] = {extent(a.out_state, B, N), extent(a.out_dendrite, B, N),
+                    extent(a.out_adaptation, B, N), extent(a.out_emitted, B, N)};
+  int n_outs = 4;
+  if (a.pending_in) outs[n_outs++] = extent_of(a.pending_in, 1, B, B, N);
+  if (a.pending_out) outs[n_outs++] = extent_of(a.pending_out, 1, B, B, N);
+  if (a.delta && (advance_only || !fused)) outs[n_outs++] = extent_of(a.delta, N, 1, B, N);
+  if (a.activity)
+    outs[n_outs++] = extent_of(a.activity, 0, 1, 1,
+                               2 * NS_EVENT_ACTIVITY_SLOTS * NS_EVENT_ACTIVITY_STRIDE);
   const Extent ins[8] = {extent(a.state, B, N), extent(a.dendrite, B, N),
                          extent(a.adaptation, B, N), extent(a.drive, B, N),
                          extent(a.dendritic_drive, B, N), extent(a.emitted, B, N),
@@ -286,11 +328,18 @@ extern "C" int ns_dendritic_event(const ns_event_args* args, void* stream) {
   A.weight = a.weight;
   A.out_weight = a.out_weight;
   A.pending_in = a.pending_in; A.pending_out = a.pending_out;
+  A.activity = reinterpret_cast<unsigned long long*>(a.activity);
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (fused) {
-    const int64_t blocks = (A.count + kThreads - 1) / kThreads;
-    event_tick_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, s>>>(A);
+    const dim3 grid(static_cast<unsigned>((A.count + kThreads - 1) / kThreads));
+    if (advance_only) {
+      if (A.activity) event_tick_kernel<false, true><<<grid, dim3(kThreads), 0, s>>>(A);
+      else event_tick_kernel<false, false><<<grid, dim3(kThreads), 0, s>>>(A);
+    } else {
+      if (A.activity) event_tick_kernel<true, true><<<grid, dim3(kThreads), 0, s>>>(A);
+      else event_tick_kernel<true, false><<<grid, dim3(kThreads), 0, s>>>(A);
+    }
     const hipError_t err = hipGetLastError();
     return err == hipSuccess ? NS_OK : fail_launch("event tick", err);
   }

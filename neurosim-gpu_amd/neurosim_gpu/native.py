@@ -35,7 +35,7 @@ import numpy as np
 import torch
 
 _LIB_NAME = "libneurosim_hip.so"
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 WEIGHT_F32, WEIGHT_F16, WEIGHT_E4M3, WEIGHT_NVFP4 = 0, 1, 2, 3
 _PLAN_CACHE = 64   # row plans kept per extension (one per live topology and batch width)
@@ -111,9 +111,12 @@ class _EventArgs(ctypes.Structure):
                 ("out_state", _OutPlane), ("out_dendrite", _OutPlane),
                 ("out_adaptation", _OutPlane), ("out_emitted", _OutPlane),
                 ("delta", _c_ptr), ("pending_in", _c_ptr), ("pending_out", _c_ptr),
-                ("out_weight", _c_ptr), ("flags", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+                ("out_weight", _c_ptr), ("flags", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("activity", _c_ptr)]
 
 EVENT_ADVANCE_ONLY = 1   # NS_EVENT_ADVANCE_ONLY
+EVENT_ACTIVITY_SLOTS = 32   # NS_EVENT_ACTIVITY_SLOTS
+EVENT_ACTIVITY_STRIDE = 16  # NS_EVENT_ACTIVITY_STRIDE
 
 
 class _SpmmArgs(ctypes.Structure):
@@ -774,7 +777,7 @@ class NativeExtension:
     def dendritic_event(self, state, dendrite, adaptation, params, current, emitted, theta,
                         rowptr, dst, weight_index, weight, input, input_scalar,
                         dendritic_input, dendritic_scalar, delta=None, pending=None,
-                        out_weight=None, advance_only=False):
+                        out_weight=None, advance_only=False, activity=None):
         """One PELS tick (ns_dendritic_event); returns the four new planes.
 
         Without ``pending`` the tick is two launches and ``current`` is updated
@@ -786,8 +789,11 @@ class NativeExtension:
         the weights in source-major order (``weight[weight_index]``), which the
         scatter then streams instead of gathering.  ``advance_only`` runs the
         advance and emission only (NS_EVENT_ADVANCE_ONLY): ``delta`` (entry
-        n*B + b) receives the emitted deltas and ``current`` is left as it was,
-        for the caller to propagate."""
+        n*B + b) receives the emitted deltas, for the caller to propagate, and
+        ``current`` is left as it was, or, with ``pending=(pending_in, None)``,
+        receives current + pending_in in one launch.  ``activity``, an int64
+        tensor of EVENT_ACTIVITY_SLOTS * EVENT_ACTIVITY_STRIDE counters (one-launch
+        forms only), has the tick's active out-edges added to it."""
         _check_state(state)
         args = _EventArgs()
         args.state = _plane(state, state, "state")
@@ -828,18 +834,28 @@ class NativeExtension:
                 raise RuntimeError("out_weight must be M contiguous float32 on the state's device")
             args.out_weight = out_weight.data_ptr()
         if advance_only:
-            if pending is not None:
-                raise RuntimeError("the advance-only tick takes no pending buffers")
             args.flags = EVENT_ADVANCE_ONLY
         if pending is not None:
             pending_in, pending_out = pending
+            if advance_only and pending_out is not None:
+                raise RuntimeError("the advance-only tick scatters nothing: no pending_out")
             for buffer in (pending_in, pending_out):
+                if buffer is None:
+                    continue
                 if (buffer.numel() < batch * n or buffer.dtype != torch.float32
                         or not buffer.is_contiguous() or buffer.device != state.device):
                     raise RuntimeError("pending buffers must hold B*N float32 on the state's device")
-            args.pending_in, args.pending_out = pending_in.data_ptr(), pending_out.data_ptr()
-        elif delta is None:
+            args.pending_in = pending_in.data_ptr()
+            args.pending_out = None if pending_out is None else pending_out.data_ptr()
+        if delta is None and (pending is None or advance_only):
             delta = torch.empty(batch * n, dtype=torch.float32, device=state.device)
+        if activity is not None:
+            if (activity.dtype != torch.int64 or not activity.is_contiguous()
+                    or activity.numel() < EVENT_ACTIVITY_SLOTS * EVENT_ACTIVITY_STRIDE
+                    or activity.device != state.device):
+                raise RuntimeError("activity must hold EVENT_ACTIVITY_SLOTS * "
+                                   "EVENT_ACTIVITY_STRIDE int64 counters on the state's device")
+            args.activity = activity.data_ptr()
         if delta is not None:
             if (delta.numel() < batch * n or delta.dtype != torch.float32
                     or not delta.is_contiguous()):

@@ -29,7 +29,8 @@ from types import SimpleNamespace
 import torch
 
 from .compartmental import DendriticDynamics, DendriticMatrixRuntime, DendriticPELSRuntime
-from .native import (BAND_WIDTH, BandLayout, NativeExtension, PanelLayout, encode_weights,
+from .native import (BAND_WIDTH, EVENT_ACTIVITY_SLOTS, EVENT_ACTIVITY_STRIDE, BandLayout,
+                     NativeExtension, PanelLayout, encode_weights,
                      load_native_extension, new_planes, panel_geometry)
 from .topology import SparseTopology
 
@@ -535,13 +536,24 @@ class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
     are, after an odd number read ``persistent_current`` (which folds) before
     the next replay.  ``one_launch=False`` runs
     the two-launch tick (advance, then scatter into the current).
+
     ``propagation="matrix"`` propagates the emitted deltas as the reference's
     matrix path does (runtime.py:233-235), current += W @ delta over the
     destination-major CSR, after an advance-only launch: no atomics, so it is
-    the faster choice when many sources emit (theta = 0, driven onsets).  Float32
-    atomics make the scatter's summation order, and therefore the last bits
-    of the current, run-dependent.  Statistics and autograd requests use the
-    reference step.
+    the faster choice when many sources emit (theta = 0, driven onsets).
+    ``propagation="auto"`` chooses between the two as the reference's PELS
+    policy does (runtime.py:129-165): at every ``policy_interval``-th tick it
+    compares the active out-edges (those of pairs with |s' - emitted| >= theta)
+    with ``event_edge_fraction`` of all B*M edges, scattering below it and
+    multiplying at or above it.  The count is taken on the device by the tick
+    itself and read back without waiting for the GPU: a sampled tick's counters
+    are copied to pinned host memory behind it on the stream, and a later policy
+    tick whose copy has completed by then applies the decision (the reference
+    counts on the host at the policy tick itself).  Until a first sample is in,
+    the tick scatters; inside a HIP graph capture the path in force is kept.
+    Float32 atomics make the scatter's summation order, and therefore the last
+    bits of the current, run-dependent.  Statistics and autograd requests use
+    the reference step.
     """
 
     @property
@@ -550,24 +562,59 @@ class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
 
     def __init__(self, topology: SparseTopology, dynamics: DendriticDynamics,
                  initial_state: torch.Tensor, *, theta: float | torch.Tensor,
-                 extension=None, one_launch: bool = True, propagation: str = "event") -> None:
+                 extension=None, one_launch: bool = True, propagation: str = "event",
+                 event_edge_fraction: float = 0.12, policy_interval: int = 16) -> None:
         _require_gpu_float32(initial_state)
-        if propagation not in ("event", "matrix"):
-            raise ValueError("native PELS propagation must be 'event' or 'matrix'")
+        if propagation not in ("event", "matrix", "auto"):
+            raise ValueError("native PELS propagation must be 'event', 'matrix' or 'auto'")
         self._pending = None
         self.extension = extension if extension is not None else load_native_extension()
-        super().__init__(topology, dynamics, initial_state, theta=theta, propagation=propagation)
+        native = isinstance(self.extension, NativeExtension)
+        if propagation == "auto" and not (native and one_launch):
+            raise ValueError("propagation='auto' needs the native extension and the "
+                             "one-launch tick")
+        super().__init__(topology, dynamics, initial_state, theta=theta, propagation=propagation,
+                         event_edge_fraction=event_edge_fraction,
+                         policy_interval=policy_interval)
         self._init_native(initial_state, self.extension)
         batch, n = initial_state.shape
+        device = initial_state.device
         self.source_major_weights = SourceMajorWeights(build_after=1)
-        if propagation == "matrix" or not isinstance(self.extension, NativeExtension):
-            one_launch = False
-        if one_launch:
-            self._pending = torch.zeros(2, batch * n, dtype=torch.float32,
-                                        device=initial_state.device)
+        self._delta = None
+        if native and one_launch:
+            self._pending = torch.zeros(2, batch * n, dtype=torch.float32, device=device)
             self._parity = 0
-        else:
-            self._delta = torch.empty(batch * n, dtype=torch.float32, device=initial_state.device)
+        if not (native and one_launch) or propagation != "event":
+            self._delta = torch.empty(batch * n, dtype=torch.float32, device=device)
+        # The path the next tick takes; "auto" changes it from sampled activity.
+        self._path = "matrix" if propagation == "matrix" else "event"
+        self._activity = self._activity_host = self._sample = None
+        if propagation == "auto":
+            slots = EVENT_ACTIVITY_SLOTS * EVENT_ACTIVITY_STRIDE
+            self._activity = torch.zeros(slots, dtype=torch.int64, device=device)
+            self._activity_host = torch.zeros(slots, dtype=torch.int64, pin_memory=True)
+
+    @property
+    def selected_path(self) -> str:
+        """The propagation the next native tick takes ("event" or "matrix")."""
+        return self._path
+
+    def _policy_tick(self) -> bool:
+        """For "auto": apply a finished sample at a policy tick and say whether
+        this tick samples (counts its active out-edges)."""
+        if self.propagation != "auto" or self._tick % self.policy_interval:
+            return False
+        if torch.cuda.is_current_stream_capturing():
+            return False
+        if self._sample is not None:
+            if not self._sample.query():
+                return False                 # the last sample is still on its way
+            counts = self._activity_host.view(EVENT_ACTIVITY_SLOTS, EVENT_ACTIVITY_STRIDE)
+            edges = int(counts[:, 0].sum())
+            slots = max(self.topology.n_edges * self.state.shape[0], 1)
+            self._path = "event" if edges / slots < self.event_edge_fraction else "matrix"
+            self._sample = None
+        return True
 
     @property
     def persistent_current(self) -> torch.Tensor:
@@ -631,17 +678,26 @@ class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
         # pending buffers are separate, so nothing outstanding is lost.
         if not self._current.is_contiguous():
             self._current = self._current.contiguous()
-        matrix = self.propagation == "matrix" and isinstance(self.extension, NativeExtension)
+        native = isinstance(self.extension, NativeExtension)
+        sample = self._policy_tick()
+        matrix = native and self._path == "matrix"
         if self._pending is not None:
             # pending[parity] holds the last tick's scatter (or zeros); the other is zero.
-            extra = {"pending": (self._pending[self._parity], self._pending[1 - self._parity])}
+            pending_in, pending_out = self._pending[self._parity], self._pending[1 - self._parity]
+            if matrix:
+                extra = {"pending": (pending_in, None), "delta": self._delta,
+                         "advance_only": True}
+            else:
+                extra = {"pending": (pending_in, pending_out)}
+            if sample:
+                extra["activity"] = self._activity
         elif matrix:
             extra = {"delta": self._delta, "advance_only": True}
-        elif isinstance(self.extension, NativeExtension):
+        elif native:
             extra = {"delta": self._delta}
         else:
             extra = {}
-        out_weight = self._source_major()
+        out_weight = self._source_major() if not matrix else None
         if out_weight is not None:
             extra["out_weight"] = out_weight
         self.state, self.dendritic_state, self.adaptation_state, self.emitted_state = (
@@ -658,6 +714,13 @@ class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
             topology = self.topology
             self.extension.csr_spmm(delta, topology.in_rowptr, topology.in_col,
                                     topology.in_weight, accumulate_into=self._current)
+        if sample:
+            # The counters reach the host behind this tick; a later policy tick
+            # reads them once the copy is done, then they start again from zero.
+            self._activity_host.copy_(self._activity, non_blocking=True)
+            self._sample = torch.cuda.Event()
+            self._sample.record()
+            self._activity.zero_()
         if self._pending is not None:
             self._parity ^= 1
         self._tick += 1

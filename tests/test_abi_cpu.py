@@ -486,7 +486,31 @@ def test_event_flags_are_checked(lib):
     assert call(args) == (1, "unknown event flags 2")
     args.flags = native.EVENT_ADVANCE_ONLY
     args.pending_in, args.pending_out = keep[0][10].ctypes.data, keep[0][11].ctypes.data
-    assert call(args) == (1, "the advance-only tick takes no pending buffers")
+    assert call(args) == (1, "the advance-only tick scatters nothing: pending_out must be NULL")
+    # The fused advance-only tick: pending_in folds into the current, deltas go to `delta`.
+    args.pending_out = None
+    args.delta = None
+    assert call(args) == (1, "a delta workspace is required")
+    args.delta = args.pending_in
+    assert "must not overlap outputs or each other" in call(args)[1]
+
+
+def test_event_activity_counters_are_checked(lib):
+    def call(args):
+        rc = lib.ns_dendritic_event(ctypes.byref(args), None)
+        return rc, lib.ns_last_error().decode()
+
+    counters = np.zeros(native.EVENT_ACTIVITY_SLOTS * native.EVENT_ACTIVITY_STRIDE, np.int64)
+    args, keep = fake_event_args()
+    args.activity = counters.ctypes.data
+    assert call(args) == (1, "activity counts need the one-launch tick (pending_in)")
+    args, keep = fake_event_args()
+    args.delta = None
+    args.pending_in, args.pending_out = keep[0][10].ctypes.data, keep[0][11].ctypes.data
+    args.activity = keep[0][11].ctypes.data          # overlaps pending_out
+    assert "must not overlap outputs or each other" in call(args)[1]
+    args.activity = args.current                     # overlaps an input
+    assert "must not overlap" in call(args)[1]
 
 
 def test_accumulated_spmm_output_must_not_overlap_itself(lib):

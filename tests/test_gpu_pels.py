@@ -15,6 +15,7 @@ import torch
 from cases import make_case, max_err
 from oracle import runtime as ort
 from neurosim_gpu import NativeDendriticPELSRuntime
+from neurosim_gpu import native as native_mod
 
 pytestmark = pytest.mark.gpu
 FIELDS = ("state", "dendritic_state", "adaptation_state")
@@ -27,7 +28,9 @@ def state_error(native, oracle) -> float:
 # one launch (scatter into pending buffers), two launches (advance, scatter),
 # or matrix propagation (advance only, then current += W @ delta)
 MODES = {"one_launch": dict(one_launch=True), "two_launch": dict(one_launch=False),
-         "matrix": dict(propagation="matrix")}
+         "matrix": dict(propagation="matrix"),
+         "matrix_two_launch": dict(propagation="matrix", one_launch=False),
+         "auto": dict(propagation="auto", policy_interval=2)}
 
 
 @pytest.mark.parametrize("mode", list(MODES))
@@ -73,9 +76,13 @@ def test_nonzero_theta_emission_and_weight_mutation(gpu, mode):
     _, stats = native.step(0.3, collect_stats=True)
     oracle.step(0.3)
     assert native.last_backend == "reference-stats" and stats.active_edges >= 0
+    path = native.selected_path
     native.step(0.3)
     oracle.step(0.3)
-    assert native.last_backend == ("native-matrix" if mode == "matrix" else "native")
+    expected = "native-matrix" if MODES[mode].get("propagation") == "matrix" else "native"
+    if mode == "auto":
+        expected = "native-matrix" if path == "matrix" else "native"
+    assert native.last_backend == expected
     assert state_error(native, oracle) <= 1e-3
 
 
@@ -95,7 +102,7 @@ def test_idle_updates_traces_and_retains_returned_state(gpu):
     assert not torch.equal(first_adaptation, native.adaptation_state)
 
 
-@pytest.mark.parametrize("propagation", ["event", "matrix"])
+@pytest.mark.parametrize("propagation", ["event", "matrix", "auto"])
 @pytest.mark.parametrize("theta", [0.0, 0.02])
 def test_cfg4_event_path_warmup_then_withdrawn(gpu, theta, propagation):
     """N=50000, M~1M, B=1: 512 ticks drive .2/.1, then 4096 ticks with inputs withdrawn."""
@@ -108,9 +115,11 @@ def test_cfg4_event_path_warmup_then_withdrawn(gpu, theta, propagation):
     bar = 1e-5 if theta == 0 else 1e-3
     worst = worst_current = 0.0
     mismatches = checked = 0
+    paths = {"event": 0, "matrix": 0}
     for tick in range(512 + 4096):
         drive, ddrive = (0.2, 0.1) if tick < 512 else (0.0, 0.0)
         before_native, before_oracle = native.emitted_state, oracle.emitted_state
+        paths[native.selected_path] += 1
         native.step(drive, dendritic_drive=ddrive)
         oracle.step(drive, ddrive)
         if tick % 64 == 63 or tick == 511:
@@ -126,7 +135,15 @@ def test_cfg4_event_path_warmup_then_withdrawn(gpu, theta, propagation):
                 # theta = 0: every pair is active, so emitted tracks the state itself
                 assert max_err(native.emitted_state, native.state) <= 1e-6
     print(f"cfg4 theta={theta} {propagation}: state {worst:.3e} current {worst_current:.3e} "
-          f"emit-mask mismatches {mismatches}/{checked}")
+          f"emit-mask mismatches {mismatches}/{checked}; ticks by path {paths}")
+    if propagation == "auto":
+        # theta = 0: every pair is active (|0| >= 0), so after the first sample every
+        # tick multiplies; theta = .02: only the onset from the zero state is that
+        # active, and the withdrawn phase scatters.
+        if theta == 0:
+            assert paths["matrix"] >= 512 + 4096 - 4 * native.policy_interval
+        else:
+            assert paths["event"] >= 4096
     assert worst <= bar
     assert worst_current <= bar
     assert max_err(native.emitted_state, oracle.emitted_state) <= bar
@@ -240,11 +257,81 @@ def test_hub_sources_scatter_many_rounds(gpu, one_launch, theta):
     assert state_error(native, oracle) <= bar
 
 
-def test_matrix_propagation_rejects_unknown_modes(gpu):
+def test_propagation_modes_are_checked(gpu):
     case = make_case(97, 600, 83, gpu, kind="reference")
-    with pytest.raises(ValueError, match="'event' or 'matrix'"):
+    with pytest.raises(ValueError, match="'event', 'matrix' or 'auto'"):
         NativeDendriticPELSRuntime(case.topology, case.model, torch.zeros(1, 97, device=gpu),
-                                   theta=0.0, propagation="auto")
+                                   theta=0.0, propagation="dense")
+    with pytest.raises(ValueError, match="one-launch"):
+        NativeDendriticPELSRuntime(case.topology, case.model, torch.zeros(1, 97, device=gpu),
+                                   theta=0.0, propagation="auto", one_launch=False)
+    with pytest.raises(ValueError, match="event_edge_fraction"):
+        NativeDendriticPELSRuntime(case.topology, case.model, torch.zeros(1, 97, device=gpu),
+                                   theta=0.0, propagation="auto", event_edge_fraction=1.5)
+
+
+@pytest.mark.parametrize("batch,theta", [(1, 0.0), (1, 0.02), (3, 0.01), (2, 2.0)])
+def test_activity_counters_count_the_active_out_edges(gpu, batch, theta):
+    """The tick's activity counters sum to the out-degrees of the pairs with
+    |s' - emitted| >= theta: the reference policy's active_edges (runtime.py:150-155),
+    in the scattering and in the fused advance-only launch."""
+    case = make_case(3000, 60_000, 8, gpu)
+    native = NativeDendriticPELSRuntime(case.topology, case.model,
+                                        torch.zeros(batch, 3000, device=gpu), theta=theta)
+    for _ in range(5):
+        native.step(0.3, dendritic_drive=0.1)
+    degree = (case.topology.out_rowptr[1:] - case.topology.out_rowptr[:-1]).long()
+    ext, t = native.extension, case.topology
+    for advance_only in (False, True):
+        emitted = native.emitted_state.clone()
+        current = native.persistent_current.contiguous().clone()
+        before = current.clone()
+        folded = torch.rand(batch * 3000, generator=torch.Generator().manual_seed(batch)) * 1e-3
+        pending = (folded.to(gpu),
+                   None if advance_only else torch.zeros(batch * 3000, device=gpu))
+        counters = torch.zeros(native_mod.EVENT_ACTIVITY_SLOTS * native_mod.EVENT_ACTIVITY_STRIDE,
+                               dtype=torch.int64, device=gpu)
+        counters[1::native_mod.EVENT_ACTIVITY_STRIDE] = 7      # between slots: untouched
+        extra = {"delta": torch.empty(batch * 3000, device=gpu)} if advance_only else {}
+        s, _, _, _ = ext.dendritic_event(
+            native.state, native.dendritic_state, native.adaptation_state, native._parameters(),
+            current, emitted, native.theta, t.out_rowptr, t.dst, t.out_weight_index,
+            t.in_weight, None, 0.3, None, 0.1, pending=pending, activity=counters,
+            advance_only=advance_only, **extra)
+        active = (s - emitted).abs() >= native.theta
+        expected = int((active.long() * degree).sum())
+        slots = counters.view(native_mod.EVENT_ACTIVITY_SLOTS, native_mod.EVENT_ACTIVITY_STRIDE)
+        print(f"activity batch={batch} theta={theta} advance_only={advance_only}: "
+              f"{int(slots[:, 0].sum())} counted, {expected} expected", flush=True)
+        assert int(slots[:, 0].sum()) == expected
+        assert bool((slots[:, 1] == 7).all()) and int(slots[:, 2:].abs().sum()) == 0
+        # Both forms fold pending_in into the current and zero it.
+        assert torch.equal(current, before + folded.to(gpu).view(3000, batch).t())
+        assert int(torch.count_nonzero(pending[0])) == 0
+
+
+def test_auto_switches_with_activity(gpu):
+    """theta = 0 makes every pair active: "auto" turns to the matrix product after its
+    first sample; quiescent (theta above every residual) it scatters; both stay on the
+    oracle."""
+    case = make_case(4000, 80_000, 9, gpu)
+    for theta, want in ((0.0, "matrix"), (2.0, "event")):
+        native = NativeDendriticPELSRuntime(case.topology, case.model,
+                                            torch.zeros(2, 4000, device=gpu), theta=theta,
+                                            propagation="auto", policy_interval=4)
+        oracle = ort.PelsOracle(case.graph, case.params, torch.zeros(2, 4000), theta=theta)
+        seen = []
+        for _ in range(40):
+            seen.append(native.selected_path)
+            native.step(0.25, dendritic_drive=0.1)
+            oracle.step(0.25, 0.1)
+            torch.cuda.synchronize()
+        print(f"auto theta={theta}: paths {''.join(p[0] for p in seen)}", flush=True)
+        assert seen[0] == "event" and seen[-1] == want
+        assert set(seen[8:]) == {want}
+        assert state_error(native, oracle) <= (1e-5 if theta == 0 else 1e-3)
+        assert max_err(native.persistent_current,
+                       ort.propagate(ort.csr_matrix(case.graph), native.emitted_state.cpu())) <= 1e-5
 
 
 @pytest.mark.parametrize("batch", [1, 3])
