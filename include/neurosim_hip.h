@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 17
+#define NS_ABI_VERSION 18
 
 /* Return codes. */
 #define NS_OK 0
@@ -115,6 +115,12 @@ typedef struct ns_row_plan {
  * instead of letting the last tile of each row range do it in the same launch.
  * The results are bitwise the same. */
 #define NS_PANEL_COMBINE_LAUNCH 2
+/* ns_panel_plan flag: `weight` holds each slot's CSR edge number (int32, -1 for
+ * padding: the plan's perm) instead of its weight, and the tick reads the
+ * float32 weight of that edge from the matrix's CSR-order weights
+ * (NS_WEIGHT_F32 only).  Ticks on a weight version used once then need no
+ * slot-order copy (ns_gather_slot_weights). */
+#define NS_PANEL_INDEXED 4
 
 typedef struct ns_panel_plan {
   int32_t panel_width;
@@ -140,7 +146,8 @@ typedef struct ns_panel_plan {
   const void* weight;          /* [n_slots] weights in slot order, encoding of the matrix:
                                   F32/F16 values, E4M3 codes, NVFP4 nibbles (two per byte;
                                   pair layouts: one uint16 word per slot pair, see
-                                  NS_PANEL_PAIRS) */
+                                  NS_PANEL_PAIRS); with NS_PANEL_INDEXED, int32 CSR edge
+                                  numbers (-1: padding) */
   const uint8_t* slot_scales;  /* NVFP4 without NS_PANEL_PAIRS: e4m3 block-scale code of
                                   each slot's edge (unused with NS_PANEL_PAIRS) */
   float* partials;             /* workspace float[2][n_panels*N*batch]: the second half

@@ -61,6 +61,11 @@ constexpr int panel_capacity_neurons() {
 // pair, the two nibbles in the low byte and the pair's block-scale code in the
 // high byte.  A kernel template format of its own, next to the NS_WEIGHT_* ones.
 constexpr int kNvfp4Pairs = 4;
+// Float32 weights read in place (NS_PANEL_INDEXED): the slot stream carries each
+// slot's CSR edge number (int32, -1 for padding) and the tick gathers the
+// weight from the CSR-order array.  A weight version ticked once then needs no
+// slot-order copy; a row's lanes read consecutive edges, which stay in L1.
+constexpr int kIndexedF32 = 5;
 
 // Wave priority follows each wave's remaining stream.
 constexpr bool kPacedWaves = true;
@@ -76,6 +81,7 @@ constexpr int block_steps() {
   else if constexpr (FMT == NS_WEIGHT_F16) return BT == 1 ? 10 : 8;
   else if constexpr (FMT == NS_WEIGHT_E4M3) return BT == 1 ? 10 : 12;
   else if constexpr (FMT == kNvfp4Pairs) return 12;
+  else if constexpr (FMT == kIndexedF32) return BT == 1 ? 10 : 8;
   else return BT == 1 ? 12 : 8;
 }
 
@@ -95,6 +101,7 @@ struct PanelArgs {
   const void* weight;
   const uint8_t* slot_scales;
   const float* gscale;
+  const float* csr_weight;  // kIndexedF32: the float32 weights in CSR order
   float* sorted;     // [rows-table entries][BT]: row sums in row-table order
   float* partials;   // [n_panels][N][BT]: row sums by row (several panels)
   OutPlane os, od, oa;
@@ -164,7 +171,7 @@ __device__ __forceinline__ const __attribute__((address_space(1))) T* scalar_bas
 template <int FMT, int D>
 __device__ __forceinline__ void load_block(const PanelArgs& A, int64_t block0, int lane,
                                            uint32_t lane32, Slot (&dst)[D]) {
-  if constexpr (FMT == NS_WEIGHT_F32) {
+  if constexpr (FMT == NS_WEIGHT_F32 || FMT == kIndexedF32) {
     const auto col = scalar_base(A.col + block0);
     const auto weight = scalar_base(static_cast<const uint32_t*>(A.weight) + block0);
 #pragma unroll
@@ -192,7 +199,8 @@ __device__ __forceinline__ void load_block(const PanelArgs& A, int64_t block0, i
 // Slots of a group start at multiples of 64, so a slot's nibble half is the lane's parity.
 template <int FMT>
 __device__ __forceinline__ float decode_slot(const Slot& x, int lane, float gscale) {
-  if constexpr (FMT == NS_WEIGHT_F32) {
+  if constexpr (FMT == NS_WEIGHT_F32 || FMT == kIndexedF32) {
+    // kIndexedF32: `w` was replaced by the gathered weight (gather_block).
     return __builtin_bit_cast(float, x.w);
   } else if constexpr (FMT == NS_WEIGHT_F16) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x.w)));
@@ -204,6 +212,24 @@ __device__ __forceinline__ float decode_slot(const Slot& x, int lane, float gsca
   } else {
     const ns_v2f pair = e2m1_pair(x.w & 0xFFu);
     return ((lane & 1) ? pair.y : pair.x) * (e4m3_to_float(x.sc) * gscale);
+  }
+}
+
+// kIndexedF32: replaces each slot's edge number by its float32 weight, all D
+// gathers issued before the first is used.  Padding (-1) reads edge 0 and
+// contributes +0.0 (its source is the slice's zero, and the weight is zeroed).
+template <int FMT, int D>
+__device__ __forceinline__ void gather_block(const PanelArgs& A, Slot (&x)[D]) {
+  if constexpr (FMT == kIndexedF32) {
+    const auto w = scalar_base(A.csr_weight);
+    uint32_t got[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+      const int32_t e = static_cast<int32_t>(x[k].w);
+      got[k] = __builtin_bit_cast(uint32_t, w[e < 0 ? 0u : static_cast<uint32_t>(e)]);
+    }
+#pragma unroll
+    for (int k = 0; k < D; ++k) x[k].w = static_cast<int32_t>(x[k].w) < 0 ? 0u : got[k];
   }
 }
 
@@ -508,9 +534,13 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
   // then close the groups that ended.  A closed group's row sums go to the
   // row-table-ordered buffer at the group's row-table entries (an address
   // made of scalars and the lane id, so closing waits on no vector load).
+  // kIndexedF32: the block's weights are gathered once its edge numbers are
+  // in (a pipeline that gathers one block ahead measured slower: 82 against
+  // 77 us for a headline tick on new weights).
   auto block = [&](Slot (&here)[D], Slot (&ahead)[D], int b) {
     const int64_t ahead0 = first + static_cast<int64_t>(b + 1) * D * 64;
     load_block<FMT, D>(A, ahead0, lane, lane32, ahead);
+    gather_block<FMT, D>(A, here);
     const int rem = total - b * D;
     uint32_t ends = rem < D ? bits & ((1u << rem) - 1u) : bits;
     bits = boundary_bits<D>(A, ahead0 / 64);
@@ -726,6 +756,7 @@ hipError_t launch_panels(const PanelArgs& A, int fmt, int n_tiles, hipStream_t s
     case NS_WEIGHT_F16: panel_tick_kernel<BT, NS_WEIGHT_F16><<<grid, block, 0, stream>>>(A); break;
     case NS_WEIGHT_E4M3: panel_tick_kernel<BT, NS_WEIGHT_E4M3><<<grid, block, 0, stream>>>(A); break;
     case kNvfp4Pairs: panel_tick_kernel<BT, kNvfp4Pairs><<<grid, block, 0, stream>>>(A); break;
+    case kIndexedF32: panel_tick_kernel<BT, kIndexedF32><<<grid, block, 0, stream>>>(A); break;
     default: panel_tick_kernel<BT, NS_WEIGHT_NVFP4><<<grid, block, 0, stream>>>(A); break;
   }
   hipError_t err = hipGetLastError();
@@ -774,9 +805,12 @@ int panel_step(const ns_step_args& a, hipStream_t stream, int product, bool laun
       !pl.weight)
     return fail("panel plan tables are required");
   if (pl.n_step_words < pl.n_slots / 64 / 32 + 2) return fail("panel plan's step bitmap is short");
-  if (pl.flags & ~(NS_PANEL_PAIRS | NS_PANEL_COMBINE_LAUNCH))
+  if (pl.flags & ~(NS_PANEL_PAIRS | NS_PANEL_COMBINE_LAUNCH | NS_PANEL_INDEXED))
     return fail("unknown panel plan flags %d", pl.flags);
   const bool pairs = (pl.flags & NS_PANEL_PAIRS) != 0;
+  const bool indexed = (pl.flags & NS_PANEL_INDEXED) != 0;
+  if (indexed && a.matrix.format != NS_WEIGHT_F32)
+    return fail("an indexed panel plan reads float32 CSR weights");
   // The products always finish in the second kernel.
   const bool one_launch = !product && pl.n_panels > 1 && !(pl.flags & NS_PANEL_COMBINE_LAUNCH);
   if (one_launch) {
@@ -797,7 +831,7 @@ int panel_step(const ns_step_args& a, hipStream_t stream, int product, bool laun
                   (long long)a.out_state.stride_b, (long long)a.out_state.stride_n);
   }
   if (!pl.partials) return fail("the panel path needs its partials workspace");
-  const uintptr_t need = a.matrix.format == NS_WEIGHT_F32 ? 4
+  const uintptr_t need = (a.matrix.format == NS_WEIGHT_F32 || indexed) ? 4
                          : (a.matrix.format == NS_WEIGHT_F16 ||
                             (a.matrix.format == NS_WEIGHT_NVFP4 && pairs)) ? 2 : 1;
   if (reinterpret_cast<uintptr_t>(pl.col) % 2 || reinterpret_cast<uintptr_t>(pl.weight) % need)
@@ -839,6 +873,11 @@ int panel_step(const ns_step_args& a, hipStream_t stream, int product, bool laun
   A.last_steps = pl.last_steps;
   A.col = pl.col; A.weight = pl.weight; A.slot_scales = pl.slot_scales;
   A.gscale = a.matrix.global_scale;
+  // An indexed plan gathers from the CSR weights; with no edges every slot is
+  // padding, which reads element 0 of the (then non-null) slot array instead.
+  A.csr_weight = indexed ? (a.matrix.n_edges > 0 ? static_cast<const float*>(a.matrix.weight)
+                                                 : static_cast<const float*>(pl.weight))
+                         : nullptr;
   A.partials = pl.partials;
   A.sorted = pl.partials + int64_t{pl.n_panels} * a.n_neurons * a.batch;
   A.os = out_plane(a.out_state); A.od = out_plane(a.out_dendrite);
@@ -866,7 +905,8 @@ int panel_step(const ns_step_args& a, hipStream_t stream, int product, bool laun
     if (!ok) { A.tile_ranges = nullptr; A.counters = nullptr; }
   }
   if (!launch) return NS_OK;
-  const int fmt = a.matrix.format == NS_WEIGHT_NVFP4 && pairs ? kNvfp4Pairs : a.matrix.format;
+  const int fmt = indexed ? kIndexedF32
+                 : a.matrix.format == NS_WEIGHT_NVFP4 && pairs ? kNvfp4Pairs : a.matrix.format;
   const hipError_t err = a.batch == 1 ? launch_panels<1>(A, fmt, pl.n_tiles, stream)
                                       : launch_panels<2>(A, fmt, pl.n_tiles, stream);
   if (err != hipSuccess) return fail_launch("panel tick", err);

@@ -35,7 +35,7 @@ import numpy as np
 import torch
 
 _LIB_NAME = "libneurosim_hip.so"
-ABI_VERSION = 17
+ABI_VERSION = 18
 
 WEIGHT_F32, WEIGHT_F16, WEIGHT_E4M3, WEIGHT_NVFP4 = 0, 1, 2, 3
 _PLAN_CACHE = 64   # row plans kept per extension (one per live topology and batch width)
@@ -388,6 +388,7 @@ LANE_TARGET = 24   # at most this many edges per lane before a row gets more lan
 
 PANEL_PAIRS = 1   # NS_PANEL_PAIRS
 PANEL_COMBINE_LAUNCH = 2   # NS_PANEL_COMBINE_LAUNCH
+PANEL_INDEXED = 4   # NS_PANEL_INDEXED
 # Largest row range the tick kernel's last tile finishes by itself when the
 # caller leaves the choice to the layout.  The last tile updates its whole
 # range on one compute unit, and in every measurement so far the combine
@@ -584,6 +585,14 @@ class PanelLayout(_SlotLayout):
         # launch captured with it (a rollout's graph) stays valid after the
         # layout has moved on to other weights.
         plan._tensors = (self, slot_weight, slot_scales)
+        return plan
+
+    def indexed_plan_struct(self) -> _PanelPlan:
+        """A plan whose slots carry CSR edge numbers (NS_PANEL_INDEXED): the tick
+        reads float32 weights from the CSR-order array itself, so it needs no
+        slot-order copy of them."""
+        plan = self.plan_struct(self.perm, None)
+        plan.flags |= PANEL_INDEXED
         return plan
 
 

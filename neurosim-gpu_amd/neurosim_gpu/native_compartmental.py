@@ -341,6 +341,9 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
                         if use_panels else None)
         self.source_major_weights = SourceMajorWeights()
         self._unversioned_warned = False
+        # The first panel tick of a float32 weight version reads in_weight in place.
+        self.indexed_first_tick = True
+        self._indexed_key = self._indexed_source = self._indexed_struct = None
         self._recorded_key, self._recorded_source, self._recorded_seen = None, None, 0
         # The backward's transposed product on panels (False: the out-edge walk).
         self.transposed_panels_enabled = True
@@ -362,12 +365,13 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
     def _recorded_panel_plan(self, weight: torch.Tensor):
         """Panel plan for a tick recorded for autograd, or None for the row kernel.
 
-        The row kernel reads ``weight`` (CSR order) itself, so a weight version
-        seen once (an optimizer step every tick) costs no slot-order copy.  From
-        the second recorded tick of one version on (backpropagation through
-        time, repeated evaluation) the panel kernel runs on a slot-order copy of
-        that version, built once.  A version is (tensor, in-place version
-        counter), so an update of the weights is never missed.
+        The first recorded tick of a weight version runs the indexed panel plan,
+        which reads ``weight`` (CSR order) itself, so a weight version seen once
+        (an optimizer step every tick) costs no slot-order copy.  From the
+        second recorded tick of one version on (backpropagation through time,
+        repeated evaluation) the panel kernel runs on a slot-order copy of that
+        version, built once.  A version is (tensor, in-place version counter),
+        so an update of the weights is never missed.
         """
         if self._panels is None:
             return None
@@ -376,7 +380,7 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
             self._recorded_key, self._recorded_source, self._recorded_seen = key, weight, 0
         self._recorded_seen += 1
         if self._recorded_seen < 2:
-            return None
+            return self._panels.indexed_plan_struct()
         return self._slot_plan(self._panels, key, weight.detach(), ())
 
     def _slot_plan(self, layout, key: tuple, weight: torch.Tensor, scales: tuple):
@@ -397,12 +401,27 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         key = (self.topology.weight_version, self.checkpoint_precision) + _weight_key(weight)
         return self._slot_plan(self._bands, key, weight, scales)
 
-    def _panel_plan(self, weight: torch.Tensor, scales: tuple):
+    def _panel_plan(self, weight: torch.Tensor, scales: tuple, *, reuse: bool = False):
         """ctypes panel plan for this tick's weights (rebuilt when the weights
         change: a new topology weight version, or the payload replaced or
-        modified in place)."""
+        modified in place).
+
+        Float32 weights: the first tick of a weight version runs the indexed
+        plan (NS_PANEL_INDEXED), which reads ``in_weight`` in CSR order, and the
+        slot-order copy is built when the same version ticks again, so weights
+        that change every tick (plasticity, training) never pay for a copy.
+        ``reuse=True`` (a captured rollout, which replays one version many
+        times) builds the copy at once.  ``indexed_first_tick = False`` turns
+        the indexed first tick off."""
         self._warn_if_unversioned(weight)
         key = (self.topology.weight_version, self.checkpoint_precision) + _weight_key(weight)
+        if (not reuse and self.indexed_first_tick and self.checkpoint_precision == "fp32"
+                and self._panel_struct_key != key
+                and (key != self._indexed_key or self._indexed_source is not weight)):
+            self._indexed_key, self._indexed_source = key, weight
+            if self._indexed_struct is None:
+                self._indexed_struct = self._panels.indexed_plan_struct()
+            return self._indexed_struct
         return self._slot_plan(self._panels, key, weight, scales)
 
     def _warn_if_unversioned(self, weight: torch.Tensor) -> None:

@@ -72,7 +72,8 @@ class MatrixRollout:
         fixed = [0.0 if s is not None else v for s, v in zip(staged, (drive, dendritic_drive))]
         weight, scales, self.backend = runtime._weights()
         topology = runtime.topology
-        panels = runtime._panel_plan(weight, scales) if runtime._panels is not None else None
+        panels = (runtime._panel_plan(weight, scales, reuse=True)
+                  if runtime._panels is not None else None)
         bands = runtime._band_plan(weight, scales) if runtime._bands is not None else None
         self._launch = TickLauncher(extension, state, runtime._parameters(),
                                     topology.in_rowptr, topology.in_col, weight, fixed[0],

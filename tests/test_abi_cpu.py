@@ -443,9 +443,13 @@ def test_panel_range_counters_are_checked(lib):
     plan.range_counters = args.out_state.data
     rc, text = call(lib, args)
     assert rc != 0 and "range counters overlap an output" in text, text
-    plan.flags = 4
+    plan.flags = 8
     rc, text = call(lib, args)
-    assert rc != 0 and "unknown panel plan flags 4" in text, text
+    assert rc != 0 and "unknown panel plan flags 8" in text, text
+    plan.flags = native.PANEL_INDEXED
+    args.matrix.format = native.WEIGHT_F16
+    rc, text = call(lib, args)
+    assert rc != 0 and "an indexed panel plan reads float32 CSR weights" in text, text
 
 
 def test_slot_gather_validation(lib):

@@ -233,6 +233,42 @@ def test_panel_fp32_warns_once_about_inference_mode_weights(gpu):
     assert not [w for w in caught if "inference_mode" in str(w.message)]
 
 
+@pytest.mark.parametrize("batch", [1, 2])
+@pytest.mark.parametrize("width,tiles,pairs", [(None, None, False), (1000, 7, False),
+                                               (256, 2, True)])
+def test_indexed_first_tick_equals_the_slot_copy(gpu, batch, width, tiles, pairs):
+    """The first panel tick of a float32 weight version reads in_weight in CSR order
+    through the slots' edge numbers (NS_PANEL_INDEXED); the ticks after it read the
+    slot-order copy.  Same layout, same sums: bitwise equal every tick, through
+    several weight changes, and within 1e-5 of the oracle."""
+    print(f"case indexed panels batch={batch} width={width} tiles={tiles} pairs={pairs}",
+          flush=True)
+    graph, topology, model, params = hub_case(gpu)
+    drive = column_drive(batch)
+    runs = []
+    for indexed in (True, False):
+        native = NativeDendriticMatrixRuntime(topology, model,
+                                              torch.zeros(batch, graph.n, device=gpu),
+                                              kernel="panels", panel_width=width,
+                                              panel_tiles=tiles, panel_pairs=pairs)
+        native.indexed_first_tick = indexed
+        runs.append(native)
+    oracle = ort.MatrixOracle(graph, params, torch.zeros(batch, graph.n))
+    indexed_ticks = 0
+    for tick in range(15):
+        if tick in (4, 5, 9):
+            topology.apply_source_weights_(topology.weight * 0.9)
+            oracle.matrix = ort.csr_matrix(otop.with_weights(graph, topology.weight.cpu().numpy()))
+        for native in runs:
+            native.step(drive.to(gpu), dendritic_drive=0.1)
+        oracle.step(drive, 0.1)
+        indexed_ticks += runs[0]._panel_struct_key != runs[0]._indexed_key
+        for field in FIELDS:
+            assert torch.equal(getattr(runs[0], field), getattr(runs[1], field)), (tick, field)
+    assert indexed_ticks == 4        # ticks 0, 4, 5 and 9 began a weight version
+    assert errors(runs[0], oracle) <= 1e-5
+
+
 def test_panel_weight_refresh_after_mutation(gpu):
     case = make_case(3000, 60_000, 4, gpu)
     native = NativeDendriticMatrixRuntime(case.topology, case.model, torch.zeros(1, 3000, device=gpu),
