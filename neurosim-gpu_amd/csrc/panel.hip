@@ -34,10 +34,10 @@
 //    stored, and the tile that completes the count adds the range's sums in
 //    panel order and applies the update: one launch per tick.  The sums are
 //    written through to, and read back from, the device-coherent level
-//    (agent-scope atomic stores and loads), and a tile's stores have completed
-//    before it counts itself in, so they need no cache write-back.  A second
-//    kernel that does the same adds after the tick kernel
-//    (NS_PANEL_COMBINE_LAUNCH) gives bitwise the same results.
+//    (agent-scope atomic stores and loads), ordered by the count (a release
+//    by every tile, an acquire by the last).  A second kernel that does the
+//    same adds after the tick kernel (NS_PANEL_COMBINE_LAUNCH, the default)
+//    gives bitwise the same results.
 //
 // Results are bitwise repeatable and, on one layout, identical across weight
 // encodings that decode to the same float32 values.
@@ -435,16 +435,19 @@ __device__ __forceinline__ void finish_rows(const PanelArgs& A, uint32_t r0, uin
 // row's sums in panel order and applies the update.  Each round issues every
 // load of its rows (parameters, states, drives, the first kCombineBatch
 // panels' sums) before the first add, so it waits on memory once.
+//
+// Ordering: the workgroup barrier makes every lane's sums part of the counting
+// thread's history; the count is a release at agent scope (every tile) and the
+// last tile's is also an acquire, so the sums of all the range's tiles happen
+// before its reads.  The counter goes back to zero in the launch that completes
+// it; after a failed launch the caller must zero the counters again.
 template <int BT>
 __device__ __forceinline__ void finish_range(const PanelArgs& A, int64_t r0, int64_t r1) {
   __shared__ int last;
-  // Each lane's sums have reached the device-coherent level before the
-  // barrier, so before the count below.
-  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
     uint32_t* const counter = A.counters + A.tile_ranges[blockIdx.x];
-    const uint32_t before = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED,
+    const uint32_t before = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL,
                                                    __HIP_MEMORY_SCOPE_AGENT);
     const bool done = before == static_cast<uint32_t>(A.n_panels - 1);
     if (done) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
