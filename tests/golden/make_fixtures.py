@@ -11,12 +11,18 @@ compact fixtures next to this script:
   shared state means after 512 warm-up ticks, the post-warm-up group inputs,
   and the 4096-tick population-mean soma traces of both rows (row 0 keeps
   its inputs, row 1 has both drives withdrawn).
+* drift.npz + drift_summary.json <- results/precision_drift.json.gz: the
+  100,000-tick schedule of 429 sample ticks, and for seed 11 of each scenario
+  (native backend) the per-sample RMSE and max-abs curves of fp16/fp8/NVFP4
+  against FP32 for the three states, with the summary figures the reference
+  computed from them.
 
 Usage: python tests/golden/make_fixtures.py [/root/reference]
 """
 
 from __future__ import annotations
 
+import gzip
 import json
 import sys
 from pathlib import Path
@@ -53,6 +59,25 @@ def main(reference: Path) -> None:
         dendritic=np.asarray(inputs["dendritic"], dtype=np.float32),
         driven_mean=np.asarray(waves["measurements"]["driven"]["population_mean_trace"]),
         zero_mean=np.asarray(waves["measurements"]["zero_input"]["population_mean_trace"]))
+
+    with gzip.open(reference / "results/precision_drift.json.gz", "rt") as handle:
+        drift = json.load(handle)
+    modes, fields = ("fp16", "fp8", "nvfp4"), ("state", "dendritic_state", "adaptation_state")
+    kept = [case for case in drift["cases"] if case["seed"] == 11 and case["backend"] == "native"]
+    arrays = {"ticks": np.asarray([s["tick"] for s in kept[0]["samples"]], dtype=np.int64)}
+    summary = {"steps": drift["protocol"]["steps"],
+               "sample_interval": drift["protocol"]["sample_interval"], "cases": {}}
+    for case in kept:
+        assert [s["tick"] for s in case["samples"]] == arrays["ticks"].tolist()
+        for stat in ("rmse", "max_abs"):
+            arrays[f"{case['scenario']}_{stat}"] = np.asarray(
+                [[[s["precisions"][m][f][stat] for s in case["samples"]] for f in fields]
+                 for m in modes], dtype=np.float64)
+        summary["cases"][case["scenario"]] = {
+            m: {f: {k: v for k, v in case["summary"][m][f].items() if k != "final"}
+                for f in fields} for m in modes}
+    np.savez_compressed(HERE / "drift.npz", **arrays)
+    (HERE / "drift_summary.json").write_text(json.dumps(summary, indent=1) + "\n")
 
 
 if __name__ == "__main__":
