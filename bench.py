@@ -19,7 +19,9 @@ B=1, theta 0.02, driven and with inputs withdrawn), the scale-out tick
 CPU oracle on a 10-tick sample), the fp8/NVFP4 device encoding of the
 headline graph's weights, one recorded tick plus its native backward on
 the headline graph next to autograd through the torch step, and headline
-ticks with a new weight version before each.  ``host`` names the CPU model,
+ticks with a new weight version before each, and the reference's own benchmark
+protocol (five shapes, eager ticks, its published RTX 5070 figures beside each
+row, kernels per tick counted in a captured graph).  ``host`` names the CPU model,
 torch and HIP versions; ``cpu_baseline`` also gives the one-thread figure.
 
     python bench.py [--gpus 1] [--steps 1000] [--warmup 50]
@@ -479,6 +481,88 @@ def measure_batched(device) -> dict:
             "pct_hbm_peak": round(100 * alg / ms / 1e6 / HBM_PEAK_GBPS, 1)}
 
 
+def _hip_runtime():
+    """The HIP runtime library this process already uses (None if it cannot be found)."""
+    import ctypes
+    try:
+        maps = Path("/proc/self/maps").read_text().splitlines()
+    except OSError:
+        return None
+    for line in maps:
+        path = line.split()[-1]
+        if "libamdhip64.so" in path:
+            try:
+                hip = ctypes.CDLL(path, mode=os.RTLD_NOLOAD | os.RTLD_NOW)
+            except OSError:
+                return None
+            hip.hipGraphGetNodes.argtypes = (ctypes.c_void_p, ctypes.c_void_p,
+                                             ctypes.POINTER(ctypes.c_size_t))
+            hip.hipGraphNodeGetType.argtypes = (ctypes.c_void_p, ctypes.POINTER(ctypes.c_int))
+            return hip
+    return None
+
+
+def graph_nodes(graph) -> dict | None:
+    """Kernel nodes and other nodes of a graph captured with ``keep_graph=True``."""
+    import ctypes
+    hip = _hip_runtime()
+    if hip is None:
+        return None
+    handle = ctypes.c_void_p(graph.raw_cuda_graph())
+    count = ctypes.c_size_t(0)
+    if hip.hipGraphGetNodes(handle, None, ctypes.byref(count)) != 0:
+        return None
+    nodes = (ctypes.c_void_p * max(count.value, 1))()
+    if hip.hipGraphGetNodes(handle, nodes, ctypes.byref(count)) != 0:
+        return None
+    kernels = 0
+    for k in range(count.value):
+        kind = ctypes.c_int(-1)
+        if hip.hipGraphNodeGetType(ctypes.c_void_p(nodes[k]), ctypes.byref(kind)) != 0:
+            return None
+        kernels += kind.value == 0          # hipGraphNodeTypeKernel
+    return {"kernels": kernels, "other_nodes": count.value - kernels}
+
+
+def captured_steps(runtime, inputs: list, fields: tuple, *, keep_graph: bool = False):
+    """A graph of ``runtime.step(drive, dendritic_drive=...)`` over ``inputs``
+    ((drive, dendritic drive) per tick), captured after one warm-up tick on a side
+    stream.  The runtime's ``fields`` are restored afterwards, so its own state is
+    as before.  Every replay starts from the states it held at capture; a
+    persistent current (updated in place) must be reset by the caller."""
+    saved = [getattr(runtime, f).clone() for f in fields]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        runtime.step(inputs[0][0], dendritic_drive=inputs[0][1])
+    torch.cuda.current_stream().wait_stream(side)
+    for f, value in zip(fields, saved):
+        setattr(runtime, f, value.clone())
+    graph = torch.cuda.CUDAGraph(keep_graph=keep_graph)
+    with torch.cuda.graph(graph):
+        for drive, dendritic in inputs:
+            runtime.step(drive, dendritic_drive=dendritic)
+    return graph, saved
+
+
+def replayed_ms(runtime, graph, saved: list, fields: tuple, ticks: int, replays: int = 8) -> float:
+    """Median ms per tick over ``replays`` replays of a ``captured_steps`` graph;
+    the runtime's ``fields`` are restored to ``saved`` afterwards."""
+    timings = []
+    for _ in range(replays):
+        if "persistent_current" in fields:
+            runtime.persistent_current.copy_(saved[fields.index("persistent_current")])
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        graph.replay()
+        end.record()
+        end.synchronize()
+        timings.append(start.elapsed_time(end) / ticks)
+    for f, value in zip(fields, saved):
+        setattr(runtime, f, value)
+    return sorted(timings)[len(timings) // 2]
+
+
 def measure_pels(device, theta: float = 0.02) -> dict:
     """N=50000, M~1M, B=1: ms/tick of the one-launch event tick in graphs of 64
     ticks, for three activity regimes: drive .2/.1 switched on at a zero state,
@@ -512,34 +596,12 @@ def measure_pels(device, theta: float = 0.02) -> dict:
                 edges += int(out_degree[changed].sum())
             for f, value in zip(fields, saved):
                 setattr(runtime, f, value.clone())
-            side = torch.cuda.Stream()
-            side.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(side):
-                runtime.step(drive, dendritic_drive=dendritic)
-            torch.cuda.current_stream().wait_stream(side)
-            for f, value in zip(fields, saved):
-                setattr(runtime, f, value.clone())
             # The graph's first tick reads these input tensors again on every replay;
             # only the persistent current (with the pending buffer of the one-launch
             # tick) is updated in place, so it is reset each time: reading the
             # attribute folds the outstanding buffer, then the copy overwrites.
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph):
-                for _ in range(chunk):
-                    runtime.step(drive, dendritic_drive=dendritic)
-            timings = []
-            for _ in range(8):
-                runtime.persistent_current.copy_(saved[-1])
-                start = torch.cuda.Event(enable_timing=True)
-                end = torch.cuda.Event(enable_timing=True)
-                start.record()
-                graph.replay()
-                end.record()
-                end.synchronize()
-                timings.append(start.elapsed_time(end) / chunk)
-            for f, value in zip(fields, saved):
-                setattr(runtime, f, value)
-        ms = sorted(timings)[len(timings) // 2]
+            graph, saved = captured_steps(runtime, [(drive, dendritic)] * chunk, fields)
+            ms = replayed_ms(runtime, graph, saved, fields, chunk)
         per_tick_sources, per_tick_edges = sources / chunk, edges / chunk
         alg = int(44 * n + 28 * n + 8 * per_tick_sources + 20 * per_tick_edges)
         return {"ms_per_tick": round(ms, 5), "emitting_sources_per_tick": round(per_tick_sources, 1),
@@ -649,6 +711,158 @@ def measure_scaleout(device, cpu_sample: bool) -> dict:
     return result
 
 
+# The reference's benchmark protocol (benchmarks/compartmental.py:38-150) and the
+# figures it published for it (results/compartmental_performance.json: NVIDIA GeForce
+# RTX 5070 Laptop GPU, CUDA 13.2): median ms per eager tick over 7 repeats of 100,
+# CUDA-event time, per runtime; "edges" is its graph's coalesced edge count.
+PROTOCOL_CASES = ((4096, 65_536, 1), (50_000, 1_000_000, 1), (50_000, 1_000_000, 8),
+                  (166_000, 10_000_000, 1), (166_000, 25_000_000, 1))
+PROTOCOL_PUBLISHED = {
+    (4096, 65_536, 1): dict(edges=65_416, native_matrix=0.01169, native_pels=0.02032,
+                            reference_matrix=0.28415, reference_pels_matrix=0.3546),
+    (50_000, 1_000_000, 1): dict(edges=999_787, native_matrix=0.06237, native_pels=0.04069,
+                                 reference_matrix=0.32694, reference_pels_matrix=0.42247),
+    (50_000, 1_000_000, 8): dict(edges=999_787, native_matrix=0.3956, native_pels=0.18265,
+                                 reference_matrix=0.66927, reference_pels_matrix=0.74575),
+    (166_000, 10_000_000, 1): dict(edges=9_998_214, native_matrix=0.4875, native_pels=0.34573,
+                                   reference_matrix=0.76716, reference_pels_matrix=0.84686),
+    (166_000, 25_000_000, 1): dict(edges=24_988_704, native_matrix=1.09299, native_pels=0.96258,
+                                   reference_matrix=1.44299, reference_pels_matrix=1.53931),
+}
+# Kernels per tick the reference counted for its native runtimes (first case's profile).
+PROTOCOL_PUBLISHED_KERNELS = {"native_matrix": 1, "native_pels": 2}
+STATE_FIELDS = ("state", "dendritic_state", "adaptation_state")
+PELS_FIELDS = STATE_FIELDS + ("emitted_state", "persistent_current")
+
+
+def measure_protocol(device, iterations: int = 100, repeats: int = 7) -> dict:
+    """The reference's benchmark protocol on this GPU, its published figures beside.
+
+    Per case: random_topology(n, candidates, seed=23) drawn on the GPU, alpha .72,
+    gain .8, tau_d 4, tau_a 25 (coupling .5, strength .2), initial state .2, drive
+    .2 + .1 sin(0.11 t), dendritic drive .1, theta .02.  Four runtimes: the torch
+    matrix runtime, the native matrix runtime, the torch PELS runtime with matrix
+    propagation and the native PELS runtime (one launch, scatter).  After 30
+    warm-up ticks each runs ``repeats`` blocks of ``iterations`` eager ticks,
+    interleaved in an order shuffled per repeat (seed 19); each block is timed with
+    HIP events and the host clock, and the medians are kept.  As in the reference,
+    every runtime sees the same inputs, so the native states are compared with the
+    torch ones at the end (its tolerances: rtol 2e-4 and atol 2e-5 for the matrix
+    tick, atol 2e-3 for PELS).  Added here: the native PELS runtime with
+    propagation="auto" (a fifth runtime in the same rotation), each native
+    runtime's kernels per tick, counted in a captured graph of one tick, and its
+    ms per tick when the same inputs run as graph replays of ``iterations`` ticks."""
+    import math
+    import random
+    from neurosim_gpu import DendriticMatrixRuntime, DendriticPELSRuntime
+
+    def drive_at(tick: int) -> float:
+        return 0.2 + 0.1 * math.sin(tick * 0.11)
+
+    order = random.Random(19)
+    cases = []
+    with torch.inference_mode():
+        for n, candidates, batch in PROTOCOL_CASES:
+            log(f"protocol: N={n} candidates={candidates} B={batch}")
+            graph = random_topology(n, candidates, device=device, seed=23)
+            soma = Dynamics(torch.full((n,), .72, device=device), torch.full((n,), .8, device=device))
+            model = DendriticDynamics.from_time_constants(soma, dt=1., tau_dendrite=4.,
+                                                          tau_adaptation=25.)
+            initial = torch.full((batch, n), .2, device=device)
+            runtimes = {
+                "reference_matrix": DendriticMatrixRuntime(graph, model, initial.clone()),
+                "native_matrix": NativeDendriticMatrixRuntime(graph, model, initial.clone()),
+                "reference_pels_matrix": DendriticPELSRuntime(graph, model, initial.clone(),
+                                                              theta=.02, propagation="matrix"),
+                "native_pels": NativeDendriticPELSRuntime(graph, model, initial.clone(), theta=.02),
+                # Not in the reference's protocol: the same tick with the propagation
+                # chosen from sampled activity (event scatter or matrix product).
+                "native_pels_auto": NativeDendriticPELSRuntime(graph, model, initial.clone(),
+                                                               theta=.02, propagation="auto"),
+            }
+            for runtime in runtimes.values():
+                for t in range(30):
+                    runtime.step(drive_at(t), dendritic_drive=.1)
+            torch.cuda.synchronize()
+            samples = {name: {"gpu_ms": [], "wall_ms": []} for name in runtimes}
+            for repeat in range(repeats):
+                names = list(runtimes)
+                order.shuffle(names)
+                for name in names:
+                    runtime = runtimes[name]
+                    start = torch.cuda.Event(enable_timing=True)
+                    end = torch.cuda.Event(enable_timing=True)
+                    torch.cuda.synchronize()
+                    wall = time.perf_counter()
+                    start.record()
+                    for t in range(iterations):
+                        runtime.step(drive_at(30 + repeat * iterations + t), dendritic_drive=.1)
+                    end.record()
+                    end.synchronize()
+                    samples[name]["wall_ms"].append((time.perf_counter() - wall) * 1000 / iterations)
+                    samples[name]["gpu_ms"].append(start.elapsed_time(end) / iterations)
+            published = PROTOCOL_PUBLISHED[(n, candidates, batch)]
+            row = {"n": n, "candidate_edges": candidates, "edges": graph.n_edges,
+                   "published_edges": published["edges"], "batch": batch,
+                   "native_matrix_kernel": runtimes["native_matrix"].kernel, "runtimes": {}}
+            for name, data in samples.items():
+                gpu = sorted(data["gpu_ms"])[len(data["gpu_ms"]) // 2]
+                wall = sorted(data["wall_ms"])[len(data["wall_ms"]) // 2]
+                row["runtimes"][name] = {"median_gpu_ms": round(gpu, 5),
+                                         "median_wall_ms": round(wall, 5),
+                                         "published_rtx5070_gpu_ms": published.get(name)}
+            # The reference's memory-probe tick (drive .2), every runtime.
+            for name, runtime in runtimes.items():
+                torch.cuda.synchronize()
+                before = torch.cuda.memory_allocated()
+                torch.cuda.reset_peak_memory_stats()
+                runtime.step(.2, dendritic_drive=.1)
+                torch.cuda.synchronize()
+                row["runtimes"][name]["tick_peak_extra_bytes"] = (torch.cuda.max_memory_allocated()
+                                                                  - before)
+            for native, reference, rtol, atol in (
+                    ("native_matrix", "reference_matrix", 2e-4, 2e-5),
+                    ("native_pels", "reference_pels_matrix", 0.0, 2e-3),
+                    ("native_pels_auto", "reference_pels_matrix", 0.0, 2e-3)):
+                a, b = runtimes[native], runtimes[reference]
+                errors = [(getattr(a, f) - getattr(b, f)).abs() for f in STATE_FIELDS]
+                within = all(bool((e <= atol + rtol * getattr(b, f).abs()).all())
+                             for e, f in zip(errors, STATE_FIELDS))
+                row["runtimes"][native]["state_max_abs_error"] = float(errors[0].max())
+                row["runtimes"][native]["within_reference_tolerance"] = within
+                if not within:
+                    log(f"protocol: {native} left the reference's tolerance at N={n} B={batch}")
+            inputs = [(drive_at(30 + repeats * iterations + 1 + t), .1) for t in range(iterations)]
+            row["runtimes"]["native_pels_auto"]["path"] = runtimes["native_pels_auto"].selected_path
+            for name, fields in (("native_matrix", STATE_FIELDS), ("native_pels", PELS_FIELDS),
+                                 ("native_pels_auto", PELS_FIELDS)):
+                runtime = runtimes[name]
+                one, saved = captured_steps(runtime, inputs[:1], fields, keep_graph=True)
+                row["runtimes"][name]["kernels_per_tick"] = graph_nodes(one)
+                for f, value in zip(fields, saved):
+                    setattr(runtime, f, value)
+                del one
+                graph_of_ticks, saved = captured_steps(runtime, inputs, fields)
+                row["runtimes"][name]["graph_replay_ms"] = round(
+                    replayed_ms(runtime, graph_of_ticks, saved, fields, iterations), 5)
+                del graph_of_ticks
+            for name in ("native_matrix", "native_pels"):
+                entry = row["runtimes"][name]
+                entry["rtx5070_over_this_gpu"] = round(published[name] / entry["median_gpu_ms"], 2)
+            log(f"protocol: {row}")
+            cases.append(row)
+            del runtimes, runtime, graph, model, initial
+            gc.collect()
+            torch.cuda.empty_cache()
+    return {"protocol": "benchmarks/compartmental.py: seed 23 (GPU generator), initial .2, "
+                        "drive .2+.1*sin(0.11 t), dendritic .1, theta .02, 30 warm-up ticks, "
+                        f"{repeats} x {iterations} eager ticks interleaved (shuffle seed 19), "
+                        "medians; float32",
+            "published": "results/compartmental_performance.json, NVIDIA GeForce RTX 5070 "
+                         "Laptop GPU",
+            "published_kernels_per_tick": PROTOCOL_PUBLISHED_KERNELS, "cases": cases}
+
+
 def main() -> None:
     cli = argparse.ArgumentParser(description=__doc__)
     cli.add_argument("--gpus", type=int, default=1)
@@ -662,7 +876,8 @@ def main() -> None:
                           "(batch a multiple of 4) or CSR row blocks")
     cli.add_argument("--copy-calibration", action="store_true",
                      help="only run 256 MiB device copies (PMC byte-counter calibration)")
-    cli.add_argument("--configs", default="encode,backward,weights,batched,pels,scaleout",
+    cli.add_argument("--configs",
+                     default="encode,backward,weights,batched,pels,scaleout,protocol",
                      help="other workloads to time after the headline one ('none' for none)")
     args = cli.parse_args()
     if args.gpus != 1:
@@ -761,6 +976,8 @@ def main() -> None:
             extra[name] = measure_pels(device)
         elif name == "scaleout":
             extra[name] = measure_scaleout(device, not args.no_cpu_baseline)
+        elif name == "protocol":
+            extra[name] = measure_protocol(device)
         else:
             cli.error(f"unknown config {name}")
         log(f"{name}: {extra[name]}")

@@ -25,6 +25,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import struct
 import threading
 import weakref
 from collections import OrderedDict
@@ -668,7 +669,9 @@ class NativeExtension:
 
     def __init__(self) -> None:
         self.lib = load_library()
-        # id(rowptr) -> (weakref, _version, {capacity: plan}); identity is re-checked on lookup.
+        # id(rowptr) -> (weakref, version, {capacity: plan}); identity is re-checked on
+        # lookup.  A rowptr made under torch.inference_mode has no version counter
+        # (PyTorch tracks none for such tensors): its plans follow its identity alone.
         self._plans: "OrderedDict[int, tuple]" = OrderedDict()
         self._lock = threading.Lock()
 
@@ -679,8 +682,9 @@ class NativeExtension:
         key = id(rowptr)
         with self._lock:
             entry = self._plans.get(key)
-            if entry is None or entry[0]() is not rowptr or entry[1] != rowptr._version:
-                entry = (weakref.ref(rowptr), rowptr._version, {})
+            version = None if torch.is_inference(rowptr) else rowptr._version
+            if entry is None or entry[0]() is not rowptr or entry[1] != version:
+                entry = (weakref.ref(rowptr), version, {})
                 self._plans[key] = entry
             self._plans.move_to_end(key)
             while len(self._plans) > _PLAN_CACHE:
@@ -1049,6 +1053,309 @@ class TickLauncher:
                                                        stream), self.lib)
         else:
             _raise_on(self.lib.ns_dendritic_step(ctypes.byref(args), stream), self.lib)
+
+
+def current_stream(device: torch.device) -> int:
+    """torch's current HIP stream on ``device`` (an index-carrying CUDA device), as
+    the integer handle the C-ABI takes."""
+    return _RAW_STREAM(device.index)
+
+
+def _public_raw_stream(index: int) -> int:
+    return torch.cuda.current_stream(index).cuda_stream
+
+
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", _public_raw_stream)
+
+
+def _consecutive(struct_type, names: tuple, size: int) -> int:
+    """Byte offset of the first of ``names``, checked to be laid out back to back."""
+    offsets = [getattr(struct_type, name).offset for name in names]
+    if any(b - a != size for a, b in zip(offsets, offsets[1:])):
+        raise RuntimeError(f"{struct_type.__name__}: fields {names} are not consecutive")
+    return offsets[0]
+
+
+# Per-tick words of the step and event argument structs, written with one
+# struct.pack_into each: five input planes (data, two strides, scalar), and
+# three or four output planes (data, two strides).
+_PLANES5 = struct.Struct("<" + "Qqqf4x" * 5)
+_OUTS3 = struct.Struct("<" + "Qqq" * 3)
+_OUTS4 = struct.Struct("<" + "Qqq" * 4)
+_CURRENT_EMITTED = struct.Struct("<Qqq" + "Qqqf4x")
+_EVENT_TAIL = struct.Struct("<QQQQiiQ")
+assert ctypes.sizeof(_Plane) == 32 and ctypes.sizeof(_OutPlane) == 24
+_IN_NAMES = ("state", "dendrite", "adaptation", "drive", "dendritic_drive")
+_STEP_IN = _consecutive(_StepArgs, _IN_NAMES, 32)
+_STEP_OUT = _consecutive(_StepArgs, ("out_state", "out_dendrite", "out_adaptation"), 24)
+_EVENT_IN = _consecutive(_EventArgs, _IN_NAMES, 32)
+_EVENT_OUT = _consecutive(_EventArgs, ("out_state", "out_dendrite", "out_adaptation",
+                                       "out_emitted"), 24)
+_EVENT_CURRENT = _consecutive(_EventArgs, ("current", "current_stride_b", "current_stride_n",
+                                           "emitted"), 8)
+_EVENT_TAIL_AT = _consecutive(_EventArgs, ("delta", "pending_in", "pending_out", "out_weight"), 8)
+if (_EventArgs.flags.offset != _EVENT_TAIL_AT + 32
+        or _EventArgs.activity.offset != _EVENT_TAIL_AT + 40):
+    raise RuntimeError("_EventArgs: flags and activity must follow out_weight")
+
+
+def _plane_words(value: torch.Tensor, state: torch.Tensor, what: str) -> tuple:
+    """(data, stride_b, stride_n) of a validated [B,N] float32 plane."""
+    _check_float(value, state, what)
+    if value.shape != state.shape:
+        raise RuntimeError("state/current/drive shape mismatch")
+    return value.data_ptr(), value.stride(0), value.stride(1)
+
+
+def _drive_words(value: torch.Tensor | None, scalar: float, state: torch.Tensor) -> tuple:
+    if value is None:
+        return 0, 0, 0, float(scalar)
+    return _plane_words(value, state, "drive") + (0.0,)
+
+
+class PreparedTick:
+    """An eager matrix tick with its fixed arguments validated once: the
+    parameter vectors, the CSR matrix and its row plan, panel or band layout.
+
+    Each call validates the three state planes unless they are this object's own
+    previous outputs, allocates three fresh neuron-major output planes (one
+    allocation, as ``new_planes``), writes the per-tick words of the argument
+    struct in two packed writes and launches on torch's current stream.  The
+    results equal ``NativeExtension.dendritic_step`` on the same inputs.
+    ``matches`` says whether the prepared arguments are still the ones given
+    (the same tensor objects at the same addresses); the caller builds a new one
+    otherwise.  Every fixed tensor is kept alive here."""
+
+    def __init__(self, extension: "NativeExtension", state: torch.Tensor, params, rowptr, col,
+                 weight, block_scales=None, global_scale=None, panels=None, bands=None):
+        _check_state(state)
+        if panels is not None and bands is not None:
+            raise RuntimeError("pass a panel or a band layout, not both")
+        self.lib = extension.lib
+        args = _StepArgs()
+        args.params = _params(params, state)
+        args.matrix = extension._csr(state, rowptr, col, weight, block_scales, global_scale)
+        batch, n = state.shape
+        args.n_neurons, args.batch = n, batch
+        bounds = None
+        if panels is not None:
+            args.panels = ctypes.addressof(panels)
+        elif bands is None:
+            bounds, blocks, capacity = extension.plan_tensors(rowptr, batch)
+            args.plan = _RowPlan(bounds.data_ptr(), blocks, capacity, 0)
+        self.args, self._ref = args, ctypes.byref(args)
+        self.bands, self._bands_ref = bands, (ctypes.byref(bands) if bands is not None else None)
+        self.batch, self.n, self.shape, self.device = batch, n, state.shape, state.device
+        self.params = tuple(params)
+        self._fixed = (rowptr, col, weight, block_scales, global_scale, panels, bands)
+        self._pointers = self._addresses(self.params, rowptr, col, weight)
+        self._bounds = bounds
+        self._last = None     # (s', d', a', their nine words)
+
+    @staticmethod
+    def _addresses(params, rowptr, col, weight) -> tuple:
+        return tuple(p.data_ptr() for p in params) + (rowptr.data_ptr(), col.data_ptr(),
+                                                      weight.data_ptr())
+
+    def matches(self, state, params, rowptr, col, weight, block_scales=None, global_scale=None,
+                panels=None, bands=None) -> bool:
+        fixed = self._fixed
+        if not (rowptr is fixed[0] and col is fixed[1] and weight is fixed[2]
+                and block_scales is fixed[3] and global_scale is fixed[4] and panels is fixed[5]
+                and bands is fixed[6] and len(params) == 6):
+            return False
+        if any(a is not b for a, b in zip(params, self.params)):
+            return False
+        last = self._last
+        if (last is None or state is not last[0]) and state.shape != self.shape:
+            return False
+        return self._addresses(params, rowptr, col, weight) == self._pointers
+
+    def __call__(self, state, dendrite, adaptation, drive, drive_scalar, dendritic_drive,
+                 dendritic_scalar) -> tuple:
+        """One tick; drives are validated [B,N] views or None with a scalar."""
+        last = self._last
+        if (last is not None and state is last[0] and dendrite is last[1]
+                and adaptation is last[2] and state.data_ptr() == last[3][0]
+                and dendrite.data_ptr() == last[3][4] and adaptation.data_ptr() == last[3][8]):
+            words = last[3]
+        else:
+            _check_state(state)
+            if state.shape != self.shape:
+                raise RuntimeError("state/current/drive shape mismatch")
+            if self.bands is not None and not (
+                    state.stride(0) == 1 and state.stride(1) >= self.batch
+                    and state.stride(1) % 4 == 0 and state.data_ptr() % 16 == 0):
+                # The band kernel gathers whole neuron rows of s: a neuron-major copy.
+                state = new_planes(1, self.batch, self.n, state)[0].copy_(state)
+            words = (_plane_words(state, state, "state") + (0.0,)
+                     + _plane_words(dendrite, state, "dendrite") + (0.0,)
+                     + _plane_words(adaptation, state, "adaptation") + (0.0,))
+        args = self.args
+        _PLANES5.pack_into(args, _STEP_IN, *words,
+                           *_drive_words(drive, drive_scalar, state),
+                           *_drive_words(dendritic_drive, dendritic_scalar, state))
+        batch, n = self.batch, self.n
+        storage = torch.empty((3, n, batch), dtype=torch.float32, device=self.device)
+        base, size = storage.data_ptr(), 4 * n * batch
+        out = (base, 1, batch, base + size, 1, batch, base + 2 * size, 1, batch)
+        _OUTS3.pack_into(args, _STEP_OUT, *out)
+        stream = current_stream(self.device)
+        if self.bands is not None:
+            code = self.lib.ns_dendritic_step_bands(self._ref, self._bands_ref, stream)
+        else:
+            code = self.lib.ns_dendritic_step(self._ref, stream)
+        _raise_on(code, self.lib)
+        outs = storage.transpose(1, 2).unbind(0)
+        self._last = (outs[0], outs[1], outs[2],
+                      (out[0], 1, batch, 0.0, out[3], 1, batch, 0.0, out[6], 1, batch, 0.0))
+        return outs
+
+
+class PreparedEvent:
+    """An eager PELS tick with its fixed arguments validated once: parameter
+    vectors, thresholds, the source-major topology, the delta workspace (made
+    here on first need when none is given), the two pending buffers (n*B + b
+    entries each) and the activity counters.
+
+    Per call it validates the state, emitted and current planes unless they are
+    the ones it saw (or wrote) last, allocates four fresh neuron-major output
+    planes and writes the per-tick words: planes, the pending buffers of
+    ``parity`` (0 or 1; None without pending buffers), the source-major weight
+    copy, the advance-only flag and the activity counters of a sampled tick.
+    The results equal ``NativeExtension.dendritic_event`` on the same inputs."""
+
+    def __init__(self, extension: "NativeExtension", state: torch.Tensor, params, theta, rowptr,
+                 dst, weight_index, weight, delta=None, pending=None, activity=None):
+        _check_state(state)
+        self.lib = extension.lib
+        args = _EventArgs()
+        args.params = _params(params, state)
+        _check_float(theta, state, "theta")
+        if theta.dim() != 1 or theta.numel() != state.size(1):
+            raise RuntimeError("theta must have N values")
+        args.theta = _Vector(theta.data_ptr(), theta.stride(0))
+        for index in (rowptr, dst, weight_index):
+            _index(index, state)
+        _check_float(weight, state, "weight")
+        if (rowptr.numel() != state.size(1) + 1 or dst.numel() != weight.numel()
+                or dst.numel() != weight_index.numel() or not weight.is_contiguous()
+                or weight.dim() != 1):
+            raise RuntimeError("invalid event topology geometry")
+        args.out_rowptr, args.dst = rowptr.data_ptr(), dst.data_ptr()
+        args.weight_index, args.weight = weight_index.data_ptr(), weight.data_ptr()
+        args.n_edges = weight.numel()
+        batch, n = state.shape
+        args.n_neurons, args.batch = n, batch
+        if delta is not None and (delta.numel() < batch * n or delta.dtype != torch.float32
+                                  or not delta.is_contiguous() or delta.device != state.device):
+            raise RuntimeError("delta workspace must hold B*N float32")
+        if pending is not None and (
+                pending.dim() != 2 or pending.size(0) != 2 or pending.size(1) < batch * n
+                or pending.dtype != torch.float32 or not pending.is_contiguous()
+                or pending.device != state.device):
+            raise RuntimeError("pending buffers must hold B*N float32 on the state's device")
+        if activity is not None and (
+                activity.dtype != torch.int64 or not activity.is_contiguous()
+                or activity.numel() < EVENT_ACTIVITY_SLOTS * EVENT_ACTIVITY_STRIDE
+                or activity.device != state.device):
+            raise RuntimeError("activity must hold EVENT_ACTIVITY_SLOTS * "
+                               "EVENT_ACTIVITY_STRIDE int64 counters on the state's device")
+        self.args, self._ref = args, ctypes.byref(args)
+        self.batch, self.n, self.shape, self.device = batch, n, state.shape, state.device
+        self.params = tuple(params)
+        self._fixed = (theta, rowptr, dst, weight_index, weight, pending, activity)
+        self._pointers = tuple(t.data_ptr() for t in self.params + self._fixed[:5])
+        self._delta = delta
+        self._pending = ((pending[0].data_ptr(), pending[1].data_ptr())
+                         if pending is not None else None)
+        self._activity = activity.data_ptr() if activity is not None else 0
+        self._out_weight = (None, 0)
+        self._current = (None, None)
+        self._last = None     # (s', d', a', e', their words)
+
+    def matches(self, state, params, theta, rowptr, dst, weight_index, weight, pending=None,
+                activity=None) -> bool:
+        fixed = self._fixed
+        if not (theta is fixed[0] and rowptr is fixed[1] and dst is fixed[2]
+                and weight_index is fixed[3] and weight is fixed[4] and pending is fixed[5]
+                and activity is fixed[6] and len(params) == 6):
+            return False
+        if any(a is not b for a, b in zip(params, self.params)):
+            return False
+        last = self._last
+        if (last is None or state is not last[0]) and state.shape != self.shape:
+            return False
+        return tuple(t.data_ptr() for t in self.params + fixed[:5]) == self._pointers
+
+    def __call__(self, state, dendrite, adaptation, emitted, current, drive, drive_scalar,
+                 dendritic_drive, dendritic_scalar, *, parity=None, advance_only=False,
+                 sample=False, out_weight=None) -> tuple:
+        """One tick; drives are validated [B,N] views or None with a scalar."""
+        last = self._last
+        if (last is not None and state is last[0] and dendrite is last[1]
+                and adaptation is last[2] and state.data_ptr() == last[4][0]
+                and dendrite.data_ptr() == last[4][4] and adaptation.data_ptr() == last[4][8]):
+            words = last[4]
+        else:
+            _check_state(state)
+            if state.shape != self.shape:
+                raise RuntimeError("state/current/drive shape mismatch")
+            words = (_plane_words(state, state, "state") + (0.0,)
+                     + _plane_words(dendrite, state, "dendrite") + (0.0,)
+                     + _plane_words(adaptation, state, "adaptation") + (0.0,))
+        if last is not None and emitted is last[3] and emitted.data_ptr() == last[5][0]:
+            emitted_words = last[5]
+        else:
+            emitted_words = _plane_words(emitted, state, "emitted") + (0.0,)
+        if current is not self._current[0] or current.data_ptr() != self._current[1][0]:
+            _check_float(current, state, "current")
+            if current.shape != state.shape:
+                raise RuntimeError("state/current/drive shape mismatch")
+            self._current = (current, (current.data_ptr(), current.stride(0), current.stride(1)))
+        if out_weight is not self._out_weight[0]:
+            if out_weight is not None and (
+                    out_weight.dtype != torch.float32 or not out_weight.is_contiguous()
+                    or out_weight.numel() != self.args.n_edges
+                    or out_weight.device != state.device):
+                raise RuntimeError("out_weight must be M contiguous float32 on the state's device")
+            self._out_weight = (out_weight, out_weight.data_ptr() if out_weight is not None else 0)
+        args = self.args
+        _PLANES5.pack_into(args, _EVENT_IN, *words,
+                           *_drive_words(drive, drive_scalar, state),
+                           *_drive_words(dendritic_drive, dendritic_scalar, state))
+        _CURRENT_EMITTED.pack_into(args, _EVENT_CURRENT, *self._current[1], *emitted_words)
+        if parity is None:
+            pending_in = pending_out = 0
+        else:
+            if self._pending is None:
+                raise RuntimeError("this tick was prepared without pending buffers")
+            pending_in, pending_out = self._pending[parity], self._pending[1 - parity]
+            if advance_only:
+                pending_out = 0
+        if sample and not self._activity:
+            raise RuntimeError("this tick was prepared without activity counters")
+        delta = 0
+        if parity is None or advance_only:
+            if self._delta is None:       # a workspace of its own, made on first need
+                self._delta = torch.empty(self.batch * self.n, dtype=torch.float32,
+                                          device=self.device)
+            delta = self._delta.data_ptr()
+        _EVENT_TAIL.pack_into(args, _EVENT_TAIL_AT, delta, pending_in, pending_out,
+                              self._out_weight[1], EVENT_ADVANCE_ONLY if advance_only else 0,
+                              0, self._activity if sample else 0)
+        batch, n = self.batch, self.n
+        storage = torch.empty((4, n, batch), dtype=torch.float32, device=self.device)
+        base, size = storage.data_ptr(), 4 * n * batch
+        out = (base, 1, batch, base + size, 1, batch, base + 2 * size, 1, batch,
+               base + 3 * size, 1, batch)
+        _OUTS4.pack_into(args, _EVENT_OUT, *out)
+        _raise_on(self.lib.ns_dendritic_event(self._ref, current_stream(self.device)), self.lib)
+        outs = storage.transpose(1, 2).unbind(0)
+        self._last = (outs[0], outs[1], outs[2], outs[3],
+                      (out[0], 1, batch, 0.0, out[3], 1, batch, 0.0, out[6], 1, batch, 0.0),
+                      (out[9], 1, batch, 0.0))
+        return outs
 
 
 @lru_cache(maxsize=1)

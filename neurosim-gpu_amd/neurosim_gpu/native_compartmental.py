@@ -30,7 +30,7 @@ import torch
 
 from .compartmental import DendriticDynamics, DendriticMatrixRuntime, DendriticPELSRuntime
 from .native import (BAND_WIDTH, EVENT_ACTIVITY_SLOTS, EVENT_ACTIVITY_STRIDE, BandLayout,
-                     NativeExtension, PanelLayout, encode_weights,
+                     NativeExtension, PanelLayout, PreparedEvent, PreparedTick, encode_weights,
                      load_native_extension, new_planes, panel_geometry)
 from .topology import SparseTopology
 
@@ -45,6 +45,10 @@ class _NativeCompartments:
         _require_gpu_float32(initial_state)
         self.extension = extension if extension is not None else load_native_extension()
         self.last_backend = "unstepped"
+        # The eager tick's launch arguments, validated once and reused while the
+        # parameters, weights and layout stay the same objects (PreparedTick,
+        # PreparedEvent).
+        self._prepared = None
 
     def _parameters(self) -> list[torch.Tensor]:
         model = self.compartment_dynamics
@@ -498,10 +502,21 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
             extra["panels"] = self._panel_plan(weight, scales)
         elif self._bands is not None:
             extra["bands"] = self._band_plan(weight, scales)
-        self.state, self.dendritic_state, self.adaptation_state = self.extension.dendritic_step(
-            self.state, self.dendritic_state, self.adaptation_state, self._parameters(),
-            self.topology.in_rowptr, self.topology.in_col, weight,
-            u, us, v, vs, self.threads_per_row, *scales, **extra)
+        topology, params = self.topology, self._parameters()
+        if isinstance(self.extension, NativeExtension):
+            tick = self._prepared
+            if tick is None or not tick.matches(self.state, params, topology.in_rowptr,
+                                                topology.in_col, weight, *scales, **extra):
+                tick = self._prepared = PreparedTick(self.extension, self.state, params,
+                                                     topology.in_rowptr, topology.in_col,
+                                                     weight, *scales, **extra)
+            outs = tick(self.state, self.dendritic_state, self.adaptation_state, u, us, v, vs)
+        else:
+            outs = self.extension.dendritic_step(
+                self.state, self.dendritic_state, self.adaptation_state, params,
+                topology.in_rowptr, topology.in_col, weight, u, us, v, vs,
+                self.threads_per_row, *scales, **extra)
+        self.state, self.dendritic_state, self.adaptation_state = outs
         self.last_backend = backend
         return self.state
 
@@ -700,31 +715,32 @@ class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
         native = isinstance(self.extension, NativeExtension)
         sample = self._policy_tick()
         matrix = native and self._path == "matrix"
-        if self._pending is not None:
-            # pending[parity] holds the last tick's scatter (or zeros); the other is zero.
-            pending_in, pending_out = self._pending[self._parity], self._pending[1 - self._parity]
-            if matrix:
-                extra = {"pending": (pending_in, None), "delta": self._delta,
-                         "advance_only": True}
-            else:
-                extra = {"pending": (pending_in, pending_out)}
-            if sample:
-                extra["activity"] = self._activity
-        elif matrix:
-            extra = {"delta": self._delta, "advance_only": True}
-        elif native:
-            extra = {"delta": self._delta}
-        else:
-            extra = {}
         out_weight = self._source_major() if not matrix else None
-        if out_weight is not None:
-            extra["out_weight"] = out_weight
-        self.state, self.dendritic_state, self.adaptation_state, self.emitted_state = (
-            self.extension.dendritic_event(
-                self.state, self.dendritic_state, self.adaptation_state, self._parameters(),
-                self._current, self.emitted_state, self.theta,
-                self.topology.out_rowptr, self.topology.dst, self.topology.out_weight_index,
-                self.topology.in_weight, u, us, v, vs, **extra))
+        topology, params = self.topology, self._parameters()
+        if native:
+            # One launch with pending buffers: pending[parity] holds the last tick's
+            # scatter (or zeros) and the other is zero; the advance-only form (matrix
+            # propagation) folds pending[parity] and writes the deltas instead.
+            tick = self._prepared
+            fixed = (self.theta, topology.out_rowptr, topology.dst, topology.out_weight_index,
+                     topology.in_weight)
+            if tick is None or not tick.matches(self.state, params, *fixed,
+                                                pending=self._pending, activity=self._activity):
+                tick = self._prepared = PreparedEvent(self.extension, self.state, params, *fixed,
+                                                      delta=self._delta, pending=self._pending,
+                                                      activity=self._activity)
+            outs = tick(self.state, self.dendritic_state, self.adaptation_state,
+                        self.emitted_state, self._current, u, us, v, vs,
+                        parity=self._parity if self._pending is not None else None,
+                        advance_only=matrix, sample=sample, out_weight=out_weight)
+        else:
+            extra = {"out_weight": out_weight} if out_weight is not None else {}
+            outs = self.extension.dendritic_event(
+                self.state, self.dendritic_state, self.adaptation_state, params,
+                self._current, self.emitted_state, self.theta, topology.out_rowptr,
+                topology.dst, topology.out_weight_index, topology.in_weight, u, us, v, vs,
+                **extra)
+        self.state, self.dendritic_state, self.adaptation_state, self.emitted_state = outs
         if matrix:
             # current += W @ delta over the destination-major CSR: the matrix
             # propagation of the emitted deltas (entry n*B + b of the workspace).

@@ -302,3 +302,23 @@ def test_auto_policy_samples_every_interval_and_picks_by_edge_fraction():
     fixed = _PathPolicy("matrix", 0.12, 4)
     assert fixed.choose(3, many, graph, False) == ("matrix", -1)
     assert fixed.choose(3, many, graph, True) == ("matrix", graph.n_edges)
+
+
+def test_row_plans_of_an_inference_mode_rowptr():
+    """The reference's benchmark builds its graphs under torch.inference_mode, whose
+    tensors carry no version counter: the row-plan cache keys them by identity."""
+    from neurosim_gpu.native import load_native_extension
+
+    extension = load_native_extension()
+    with torch.inference_mode():
+        graph = random_topology(40, 400, device="cpu", seed=3)
+        assert torch.is_inference(graph.in_rowptr)
+        first = extension.plan_tensors(graph.in_rowptr, 1)
+    assert extension.plan_tensors(graph.in_rowptr, 1) is first
+    bounds, blocks, capacity = first
+    assert blocks >= 1 and capacity > 0 and bounds.numel() == 2 * (blocks + 1)
+    # A versioned rowptr edited in place gets a new plan.
+    rowptr = graph.in_rowptr.clone()
+    before = extension.plan_tensors(rowptr, 1)
+    rowptr.add_(0)
+    assert extension.plan_tensors(rowptr, 1) is not before

@@ -153,6 +153,55 @@ def test_returned_states_stay_valid_after_later_ticks(gpu):
     assert torch.equal(first, saved)
 
 
+@pytest.mark.parametrize("batch", [1, 4])
+def test_runtimes_built_under_inference_mode(gpu, batch):
+    """The reference's benchmark builds graph, model and runtimes inside
+    torch.inference_mode (benchmarks/compartmental.py:57-70), so none of its
+    tensors carry a version counter.  Every native kernel and propagation must
+    run there and agree with the torch runtimes within that benchmark's own
+    tolerances (rtol 2e-4, atol 2e-5 matrix; atol 2e-3 PELS at theta .02)."""
+    import math
+    import warnings
+    from neurosim_gpu import DendriticDynamics, DendriticPELSRuntime, MatrixRollout
+
+    n, candidates, ticks = 4096, 65_536, 40
+    print(f"case inference-mode runtimes N={n} candidates={candidates} B={batch}", flush=True)
+    kernels = ("rows", "panels") if batch == 1 else ("rows", "bands")
+    with torch.inference_mode(), warnings.catch_warnings(record=True) as caught:
+        warnings.simplefilter("always")
+        graph = random_topology(n, candidates, device=gpu, seed=23)
+        soma = Dynamics(torch.full((n,), .72, device=gpu), torch.full((n,), .8, device=gpu))
+        model = DendriticDynamics.from_time_constants(soma, dt=1., tau_dendrite=4.,
+                                                      tau_adaptation=25.)
+        initial = torch.full((batch, n), .2, device=gpu)
+        matrix = {k: NativeDendriticMatrixRuntime(graph, model, initial.clone(), kernel=k)
+                  for k in kernels}
+        pels = {p: NativeDendriticPELSRuntime(graph, model, initial.clone(), theta=.02,
+                                              propagation=p) for p in ("event", "matrix", "auto")}
+        reference = DendriticMatrixRuntime(graph, model, initial.clone())
+        reference_pels = DendriticPELSRuntime(graph, model, initial.clone(), theta=.02,
+                                              propagation="matrix")
+        for t in range(ticks):
+            drive = .2 + .1 * math.sin(t * .11)
+            for runtime in (*matrix.values(), *pels.values(), reference, reference_pels):
+                runtime.step(drive, dendritic_drive=.1)
+        rollout = MatrixRollout(matrix[kernels[-1]], 20, drive=.2, dendritic_drive=.1)
+        rollout.run()
+        assert bool(torch.isfinite(rollout.state).all())
+    # The slot-order weight copy of panels and bands cannot see in-place edits of
+    # an unversioned in_weight: the runtime says so once.
+    assert any("inference_mode" in str(w.message) for w in caught)
+    for name, runtime in matrix.items():
+        assert runtime.kernel == name
+        for f in FIELDS:
+            torch.testing.assert_close(getattr(runtime, f), getattr(reference, f),
+                                       rtol=2e-4, atol=2e-5)
+    for name, runtime in pels.items():
+        for f in FIELDS:
+            torch.testing.assert_close(getattr(runtime, f), getattr(reference_pels, f),
+                                       rtol=0, atol=2e-3)
+
+
 def test_cli_native_matrix_and_pels(gpu, tmp_path):
     from neurosim_gpu.simulate import parser, run
 
