@@ -1358,6 +1358,43 @@ class PreparedEvent:
         return outs
 
 
+class PreparedAccumulate:
+    """``out += W @ source`` (ns_csr_spmm with accumulate) with every argument
+    validated once: a source plane, float32 CSR weights with their row plan and
+    the accumulated output, all fixed tensors (the PELS runtime's delta
+    workspace and current).  ``matches`` says whether the given tensors are
+    still those objects at those addresses; a call only launches."""
+
+    def __init__(self, extension: "NativeExtension", source: torch.Tensor, rowptr, col, weight,
+                 out: torch.Tensor):
+        _check_state(source)
+        args = _SpmmArgs()
+        args.source = _plane(source, source, "source")
+        args.matrix = extension._csr(source, rowptr, col, weight, None, None)
+        batch, n = source.shape
+        args.n_neurons, args.batch = n, batch
+        bounds, blocks, capacity = extension.plan_tensors(rowptr, batch)
+        args.plan = _RowPlan(bounds.data_ptr(), blocks, capacity, 0)
+        _check_float(out, source, "accumulated output")
+        if out.shape != source.shape:
+            raise RuntimeError("the accumulated output must be [B,N]")
+        args.out = _out(out)
+        args.accumulate = 1
+        self.lib, self.args, self._ref = extension.lib, args, ctypes.byref(args)
+        self.device = source.device
+        self._tensors = (source, rowptr, col, weight, out)
+        self._pointers = tuple(t.data_ptr() for t in self._tensors)
+        self._bounds = bounds
+
+    def matches(self, source, rowptr, col, weight, out) -> bool:
+        given = (source, rowptr, col, weight, out)
+        return (all(a is b for a, b in zip(given, self._tensors))
+                and tuple(t.data_ptr() for t in given) == self._pointers)
+
+    def __call__(self) -> None:
+        _raise_on(self.lib.ns_csr_spmm(self._ref, current_stream(self.device)), self.lib)
+
+
 @lru_cache(maxsize=1)
 def load_native_extension(verbose: bool = False) -> NativeExtension:
     """The process-wide native extension (library loaded once, never rebuilt)."""

@@ -30,7 +30,8 @@ import torch
 
 from .compartmental import DendriticDynamics, DendriticMatrixRuntime, DendriticPELSRuntime
 from .native import (BAND_WIDTH, EVENT_ACTIVITY_SLOTS, EVENT_ACTIVITY_STRIDE, BandLayout,
-                     NativeExtension, PanelLayout, PreparedEvent, PreparedTick, encode_weights,
+                     NativeExtension, PanelLayout, PreparedAccumulate, PreparedEvent,
+                     PreparedTick, encode_weights,
                      load_native_extension, new_planes, panel_geometry)
 from .topology import SparseTopology
 
@@ -615,6 +616,7 @@ class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
         device = initial_state.device
         self.source_major_weights = SourceMajorWeights(build_after=1)
         self._delta = None
+        self._accumulate = None     # the prepared current += W @ delta (matrix propagation)
         if native and one_launch:
             self._pending = torch.zeros(2, batch * n, dtype=torch.float32, device=device)
             self._parity = 0
@@ -744,11 +746,16 @@ class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
         if matrix:
             # current += W @ delta over the destination-major CSR: the matrix
             # propagation of the emitted deltas (entry n*B + b of the workspace).
-            batch, n = self.state.shape
-            delta = torch.as_strided(self._delta, (batch, n), (1, batch))
-            topology = self.topology
-            self.extension.csr_spmm(delta, topology.in_rowptr, topology.in_col,
-                                    topology.in_weight, accumulate_into=self._current)
+            product = self._accumulate
+            if product is None or not product.matches(product._tensors[0], topology.in_rowptr,
+                                                      topology.in_col, topology.in_weight,
+                                                      self._current):
+                batch, n = self.state.shape
+                delta = torch.as_strided(self._delta, (batch, n), (1, batch))
+                product = self._accumulate = PreparedAccumulate(
+                    self.extension, delta, topology.in_rowptr, topology.in_col,
+                    topology.in_weight, self._current)
+            product()
         if sample:
             # The counters reach the host behind this tick; a later policy tick
             # reads them once the copy is done, then they start again from zero.

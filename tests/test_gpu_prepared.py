@@ -174,3 +174,26 @@ def test_runtime_steps_through_the_prepared_launch_and_revalidates(gpu):
         runtime.step(0.2, dendritic_drive=0.1)
         assert runtime._prepared is not first
         assert bool(torch.isfinite(runtime.state).all())
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_prepared_accumulate_equals_csr_spmm(gpu, batch):
+    """current += W @ delta: the PELS matrix propagation's prepared launch against
+    csr_spmm(accumulate_into=...), bitwise (no atomics: one lane group per row)."""
+    print(f"case prepared accumulate B={batch}", flush=True)
+    from neurosim_gpu.native import PreparedAccumulate
+
+    case = make_case(N, M, SEED, gpu)
+    topo = case.topology
+    ext = load_native_extension()
+    delta_storage = torch.randn(batch * N, generator=torch.Generator().manual_seed(3)).to(gpu)
+    delta = torch.as_strided(delta_storage, (batch, N), (1, batch))
+    a = torch.rand(batch, N, device=gpu)
+    b = a.clone()
+    product = PreparedAccumulate(ext, delta, topo.in_rowptr, topo.in_col, topo.in_weight, b)
+    assert product.matches(delta, topo.in_rowptr, topo.in_col, topo.in_weight, b)
+    assert not product.matches(delta, topo.in_rowptr, topo.in_col, topo.in_weight, a)
+    for _ in range(3):
+        ext.csr_spmm(delta, topo.in_rowptr, topo.in_col, topo.in_weight, accumulate_into=a)
+        product()
+        assert torch.equal(a, b)
