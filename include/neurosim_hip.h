@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NS_ABI_VERSION 18
+#define NS_ABI_VERSION 19
 
 /* Return codes. */
 #define NS_OK 0
@@ -311,6 +311,12 @@ typedef struct ns_spmm_args {
   int32_t accumulate;          /* nonzero: out += W @ S (every (b, n) of `out` a distinct
                                   element) instead of out = W @ S */
   int32_t reserved;
+  const ns_panel_plan* panels; /* optional (batch 1 or 2): run the product on this
+                                  column-panel layout of the matrix (ns_plan_panels over
+                                  the same CSR; slot weights or NS_PANEL_INDEXED, as for
+                                  ns_dendritic_step), summed in panel order and added
+                                  or stored by the combine kernel; `plan` is then not
+                                  read.  NULL: row blocks. */
 } ns_spmm_args;
 
 /* Arguments of the backward of one fused matrix tick (float32 weights). */
@@ -504,9 +510,11 @@ int ns_dendritic_step_bands(const ns_step_args* args, const ns_band_plan* plan, 
  * pending_out instead of `current` (see ns_event_args). */
 int ns_dendritic_event(const ns_event_args* args, void* stream);
 
-/* CSR product J = W @ S with the tick's decoding and summation order.
+/* CSR product J = W @ S with the tick's decoding and summation order (row
+ * blocks, or column panels when `panels` is set).
  * Replaces MatrixRuntime._propagate (reference: runtime.py:78-79) for device
- * float32 operands, e.g. the persistent current W @ emitted of runtime.py:124,220. */
+ * float32 operands, e.g. the persistent current W @ emitted of runtime.py:124,220,
+ * and the matrix propagation of emitted deltas (runtime.py:233-235). */
 int ns_csr_spmm(const ns_spmm_args* args, void* stream);
 
 /* Floats of workspace ns_dendritic_step_backward needs (2*N*B). */

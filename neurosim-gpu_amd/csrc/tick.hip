@@ -527,7 +527,11 @@ extern "C" int ns_csr_spmm(const ns_spmm_args* args, void* stream) {
   if (a.n_neurons <= 0) return fail("source must be [B,N], N > 0");
   if (a.batch < 0) return fail("batch must be non-negative");
   if (a.n_neurons >= (int64_t{1} << 31)) return fail("N must be below 2^31");
-  if (int rc = check_matrix(a.matrix, a.n_neurons, a.plan, a.batch)) return rc;
+  if (a.panels) {
+    if (int rc = check_csr(a.matrix, a.n_neurons)) return rc;
+  } else if (int rc = check_matrix(a.matrix, a.n_neurons, a.plan, a.batch)) {
+    return rc;
+  }
   if (a.batch == 0) return NS_OK;  // empty planes may carry null pointers
   if (!a.source.data) return fail("source data is required");
   if (!a.out.data) return fail("an output plane is required");
@@ -536,6 +540,15 @@ extern "C" int ns_csr_spmm(const ns_spmm_args* args, void* stream) {
   if (a.accumulate && !distinct_elements(a.out.stride_b, a.out.stride_n, a.batch, a.n_neurons))
     return fail("an accumulated output plane must not overlap itself (strides %lld, %lld)",
                 (long long)a.out.stride_b, (long long)a.out.stride_n);
+  if (a.panels) {
+    // The panel kernel in product mode: per-panel sums, then the combine
+    // kernel adds them in panel order and stores (1) or adds (2) them.
+    ns_step_args step{};
+    step.n_neurons = a.n_neurons; step.batch = a.batch;
+    step.state = a.source; step.matrix = a.matrix; step.panels = a.panels;
+    step.out_state = a.out;
+    return panel_step(step, static_cast<hipStream_t>(stream), a.accumulate ? 2 : 1, true);
+  }
 
   TickArgs A{};
   A.N = a.n_neurons; A.B = a.batch; A.M = a.matrix.n_edges;

@@ -36,7 +36,7 @@ import numpy as np
 import torch
 
 _LIB_NAME = "libneurosim_hip.so"
-ABI_VERSION = 18
+ABI_VERSION = 19
 
 WEIGHT_F32, WEIGHT_F16, WEIGHT_E4M3, WEIGHT_NVFP4 = 0, 1, 2, 3
 _PLAN_CACHE = 64   # row plans kept per extension (one per live topology and batch width)
@@ -123,7 +123,8 @@ EVENT_ACTIVITY_STRIDE = 16  # NS_EVENT_ACTIVITY_STRIDE
 class _SpmmArgs(ctypes.Structure):
     _fields_ = [("n_neurons", _c_i64), ("batch", _c_i64), ("source", _Plane),
                 ("matrix", _Csr), ("plan", _RowPlan), ("out", _OutPlane),
-                ("accumulate", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+                ("accumulate", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("panels", _c_ptr)]
 
 
 class _StepGradArgs(ctypes.Structure):
@@ -954,17 +955,22 @@ class NativeExtension:
         return (*planes[:3], d_drive, d_dendritic, d_weight, d_params)
 
     def csr_spmm(self, source, rowptr, col, weight, block_scales=None, global_scale=None, *,
-                 accumulate_into=None):
+                 accumulate_into=None, panels=None):
         """W @ source as a new neuron-major [B,N] plane, or, with
         ``accumulate_into`` (a [B,N] float32 tensor on the device whose elements
-        are distinct), added into that tensor in place, which is returned."""
+        are distinct), added into that tensor in place, which is returned.
+        ``panels`` (a ``_PanelPlan`` of this CSR, batch 1 or 2) runs the product
+        on the column-panel kernel instead of row blocks."""
         _check_state(source)
         args = _SpmmArgs()
         args.source = _plane(source, source, "source")
         args.matrix = self._csr(source, rowptr, col, weight, block_scales, global_scale)
         batch, n = source.shape
         args.n_neurons, args.batch = n, batch
-        args.plan = self.plan_for(rowptr, batch)
+        if panels is not None:
+            args.panels = ctypes.addressof(panels)
+        else:
+            args.plan = self.plan_for(rowptr, batch)
         if accumulate_into is None:
             (out,) = new_planes(1, batch, n, source)
         else:
@@ -1360,21 +1366,25 @@ class PreparedEvent:
 
 class PreparedAccumulate:
     """``out += W @ source`` (ns_csr_spmm with accumulate) with every argument
-    validated once: a source plane, float32 CSR weights with their row plan and
-    the accumulated output, all fixed tensors (the PELS runtime's delta
-    workspace and current).  ``matches`` says whether the given tensors are
+    validated once: a source plane, float32 CSR weights with their row plan (or
+    a column-panel plan) and the accumulated output, all fixed tensors (the PELS
+    runtime's delta workspace and current).  ``matches`` says whether the given tensors are
     still those objects at those addresses; a call only launches."""
 
     def __init__(self, extension: "NativeExtension", source: torch.Tensor, rowptr, col, weight,
-                 out: torch.Tensor):
+                 out: torch.Tensor, panels: "_PanelPlan | None" = None):
         _check_state(source)
         args = _SpmmArgs()
         args.source = _plane(source, source, "source")
         args.matrix = extension._csr(source, rowptr, col, weight, None, None)
         batch, n = source.shape
         args.n_neurons, args.batch = n, batch
-        bounds, blocks, capacity = extension.plan_tensors(rowptr, batch)
-        args.plan = _RowPlan(bounds.data_ptr(), blocks, capacity, 0)
+        bounds = None
+        if panels is not None:
+            args.panels = ctypes.addressof(panels)
+        else:
+            bounds, blocks, capacity = extension.plan_tensors(rowptr, batch)
+            args.plan = _RowPlan(bounds.data_ptr(), blocks, capacity, 0)
         _check_float(out, source, "accumulated output")
         if out.shape != source.shape:
             raise RuntimeError("the accumulated output must be [B,N]")
@@ -1384,11 +1394,11 @@ class PreparedAccumulate:
         self.device = source.device
         self._tensors = (source, rowptr, col, weight, out)
         self._pointers = tuple(t.data_ptr() for t in self._tensors)
-        self._bounds = bounds
+        self._bounds, self.panels = bounds, panels
 
-    def matches(self, source, rowptr, col, weight, out) -> bool:
+    def matches(self, source, rowptr, col, weight, out, panels=None) -> bool:
         given = (source, rowptr, col, weight, out)
-        return (all(a is b for a, b in zip(given, self._tensors))
+        return (panels is self.panels and all(a is b for a, b in zip(given, self._tensors))
                 and tuple(t.data_ptr() for t in given) == self._pointers)
 
     def __call__(self) -> None:

@@ -36,6 +36,14 @@ from .native import (BAND_WIDTH, EVENT_ACTIVITY_SLOTS, EVENT_ACTIVITY_STRIDE, Ba
 from .topology import SparseTopology
 
 
+def _capture_error(what: str) -> RuntimeError:
+    """A derived weight array missing while the stream is being captured: built
+    here, it would be filled only when the graph replays, and the eager ticks
+    after the capture would read it unfilled."""
+    return RuntimeError(f"the {what} of this weight version is built on an eager tick; "
+                        "run one eager tick before capturing ticks into a graph")
+
+
 def _require_gpu_float32(initial_state: torch.Tensor) -> None:
     if initial_state.device.type != "cuda" or initial_state.dtype != torch.float32:
         raise ValueError("native compartment runtime requires CUDA float32")
@@ -129,6 +137,8 @@ class SourceMajorWeights:
             self._key, self._source, self._seen, self._values = key, weight, 0, None
         self._seen += 1
         if self._seen >= self.build_after and self._values is None:
+            if torch.cuda.is_current_stream_capturing():
+                return None          # built by an eager request (see _capture_error)
             with torch.no_grad():
                 self._values = torch.index_select(weight.detach(), 0, out_weight_index)
         return self._values
@@ -338,6 +348,10 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         use_bands = kernel == "bands" or (
             kernel == "auto" and native and bands_pay_off(topology.n_neurons, batch))
         self.kernel = "panels" if use_panels else "bands" if use_bands else "rows"
+        if self.kernel == "rows" and native and batch > 0:
+            # A row plan reads rowptr on the host (a synchronisation): made now, not on
+            # a tick that may be captured into a graph.
+            self.extension.plan_tensors(topology.in_rowptr, batch)
         if panel_pairs is None:
             panel_pairs = weight_format == "nvfp4"
         self._panels = (PanelLayout(topology, batch, initial_state.device,
@@ -393,6 +407,13 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         ``key`` changes.  The weight payload is held with the plan, so the
         identity in the key stays its own."""
         if self._panel_struct_key != key:
+            if torch.cuda.is_current_stream_capturing():
+                if layout is self._panels and self.checkpoint_precision == "fp32":
+                    # Float32 panels read in_weight in place until an eager tick copies it.
+                    if self._indexed_struct is None:
+                        self._indexed_struct = self._panels.indexed_plan_struct()
+                    return self._indexed_struct
+                raise _capture_error("slot-order weight copy")
             block = scales[0] if len(scales) == 2 else None
             slots, slot_scales = layout.slot_weights(key, weight, block)
             self._panel_struct = layout.plan_struct(slots, slot_scales)
@@ -472,6 +493,8 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         if self.weight_format is None and self.weight_dtype == torch.float32:
             return weight, (), "native"
         if self._packed_weight_version != self.topology.weight_version:
+            if torch.cuda.is_current_stream_capturing():
+                raise _capture_error(f"{self.weight_format or 'fp16'} weight payload")
             with torch.no_grad():
                 if self.weight_format is None:
                     self._packed_weight = (weight.detach().to(torch.float16),)
@@ -589,6 +612,13 @@ class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
     Float32 atomics make the scatter's summation order, and therefore the last
     bits of the current, run-dependent.  Statistics and autograd requests use
     the reference step.
+
+    ``kernel`` picks the kernel of the matrix propagation's product: "rows"
+    (CSR row blocks), "panels" (the column-panel kernel in product mode, batch
+    1 or 2; its layout is built at construction) or "auto" (panels where they
+    pay off, as for NativeDendriticMatrixRuntime).  The panel product reads the
+    float32 weights through the slots' CSR edge numbers on the first matrix
+    tick of a weight version and from a slot-order copy after that.
     """
 
     @property
@@ -598,10 +628,13 @@ class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
     def __init__(self, topology: SparseTopology, dynamics: DendriticDynamics,
                  initial_state: torch.Tensor, *, theta: float | torch.Tensor,
                  extension=None, one_launch: bool = True, propagation: str = "event",
-                 event_edge_fraction: float = 0.12, policy_interval: int = 16) -> None:
+                 event_edge_fraction: float = 0.12, policy_interval: int = 16,
+                 kernel: str = "auto") -> None:
         _require_gpu_float32(initial_state)
         if propagation not in ("event", "matrix", "auto"):
             raise ValueError("native PELS propagation must be 'event', 'matrix' or 'auto'")
+        if kernel not in ("auto", "rows", "panels"):
+            raise ValueError("kernel must be 'auto', 'rows' or 'panels'")
         self._pending = None
         self.extension = extension if extension is not None else load_native_extension()
         native = isinstance(self.extension, NativeExtension)
@@ -629,11 +662,44 @@ class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
             slots = EVENT_ACTIVITY_SLOTS * EVENT_ACTIVITY_STRIDE
             self._activity = torch.zeros(slots, dtype=torch.int64, device=device)
             self._activity_host = torch.zeros(slots, dtype=torch.int64, pin_memory=True)
+        # The matrix propagation's product kernel and, for panels, its layout.
+        if kernel == "panels" and (batch not in (1, 2) or not native):
+            raise ValueError("the panel kernel needs batch 1 or 2 and the native extension")
+        use_panels = native and propagation != "event" and (
+            kernel == "panels" or (kernel == "auto" and batch in (1, 2)
+                                   and panels_pay_off(topology, batch)))
+        self.kernel = "panels" if use_panels else "rows"
+        self._product_panels = PanelLayout(topology, batch, device) if use_panels else None
+        self._product_key = self._product_source = None
+        self._product_seen, self._product_struct, self._product_indexed = 0, None, None
 
     @property
     def selected_path(self) -> str:
         """The propagation the next native tick takes ("event" or "matrix")."""
         return self._path
+
+    def _product_plan(self):
+        """Panel plan of ``in_weight`` for the matrix propagation: the indexed plan
+        (CSR edge numbers in the slots) on the first matrix tick of a weight
+        version and inside graph captures until the copy exists, the slot-order
+        copy from the second eager tick on.  A version is the topology's weight
+        version and the tensor's identity and in-place version."""
+        layout, weight = self._product_panels, self.topology.in_weight
+        key = (self.topology.weight_version,) + _weight_key(weight)
+        if key != self._product_key or self._product_source is not weight:
+            self._product_key, self._product_source = key, weight
+            self._product_seen, self._product_struct = 0, None
+        self._product_seen += 1
+        if self._product_struct is None:
+            # Under graph capture the copy is not built: its gather would only run
+            # at replay, while the eager ticks after the capture would read it.
+            if self._product_seen < 2 or torch.cuda.is_current_stream_capturing():
+                if self._product_indexed is None:
+                    self._product_indexed = layout.indexed_plan_struct()
+                return self._product_indexed
+            slots, _ = layout.slot_weights(("pels",) + key, weight.detach(), None)
+            self._product_struct = layout.plan_struct(slots, None)
+        return self._product_struct
 
     def _policy_tick(self) -> bool:
         """For "auto": apply a finished sample at a policy tick and say whether
@@ -746,15 +812,16 @@ class NativeDendriticPELSRuntime(_NativeCompartments, DendriticPELSRuntime):
         if matrix:
             # current += W @ delta over the destination-major CSR: the matrix
             # propagation of the emitted deltas (entry n*B + b of the workspace).
+            panels = self._product_plan() if self._product_panels is not None else None
             product = self._accumulate
             if product is None or not product.matches(product._tensors[0], topology.in_rowptr,
                                                       topology.in_col, topology.in_weight,
-                                                      self._current):
+                                                      self._current, panels):
                 batch, n = self.state.shape
                 delta = torch.as_strided(self._delta, (batch, n), (1, batch))
                 product = self._accumulate = PreparedAccumulate(
                     self.extension, delta, topology.in_rowptr, topology.in_col,
-                    topology.in_weight, self._current)
+                    topology.in_weight, self._current, panels)
             product()
         if sample:
             # The counters reach the host behind this tick; a later policy tick

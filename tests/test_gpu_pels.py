@@ -30,7 +30,10 @@ def state_error(native, oracle) -> float:
 MODES = {"one_launch": dict(one_launch=True), "two_launch": dict(one_launch=False),
          "matrix": dict(propagation="matrix"),
          "matrix_two_launch": dict(propagation="matrix", one_launch=False),
-         "auto": dict(propagation="auto", policy_interval=2)}
+         "auto": dict(propagation="auto", policy_interval=2),
+         # the matrix propagation's product on the column-panel kernel (batch 1 or 2)
+         "matrix_panels": dict(propagation="matrix", kernel="panels"),
+         "auto_panels": dict(propagation="auto", policy_interval=2, kernel="panels")}
 
 
 @pytest.mark.parametrize("mode", list(MODES))
@@ -56,9 +59,11 @@ def test_nonzero_theta_emission_and_weight_mutation(gpu, mode):
     from oracle import topology as otop
 
     case = make_case(97, 600, 83, gpu, kind="reference")
-    state = torch.full((3, 97), 0.2)
+    batch = 2 if MODES[mode].get("kernel") == "panels" else 3
+    state = torch.full((batch, 97), 0.2)
     native = NativeDendriticPELSRuntime(case.topology, case.model, state.to(gpu), theta=0.02,
                                         **MODES[mode])
+    assert native.kernel == MODES[mode].get("kernel", "rows")
     oracle = ort.PelsOracle(case.graph, case.params, state, theta=0.02)
     for t in range(50):
         if t == 25:
@@ -102,15 +107,18 @@ def test_idle_updates_traces_and_retains_returned_state(gpu):
     assert not torch.equal(first_adaptation, native.adaptation_state)
 
 
-@pytest.mark.parametrize("propagation", ["event", "matrix", "auto"])
+@pytest.mark.parametrize("propagation,kernel", [("event", "auto"), ("matrix", "auto"),
+                                                ("auto", "auto"), ("matrix", "panels"),
+                                                ("auto", "panels")])
 @pytest.mark.parametrize("theta", [0.0, 0.02])
-def test_cfg4_event_path_warmup_then_withdrawn(gpu, theta, propagation):
+def test_cfg4_event_path_warmup_then_withdrawn(gpu, theta, propagation, kernel):
     """N=50000, M~1M, B=1: 512 ticks drive .2/.1, then 4096 ticks with inputs withdrawn."""
-    print(f"case cfg4 N=50000 M=1000000 theta={theta} propagation={propagation}", flush=True)
+    print(f"case cfg4 N=50000 M=1000000 theta={theta} propagation={propagation} "
+          f"kernel={kernel}", flush=True)
     case = make_case(50_000, 1_000_000, 0, gpu)
     native = NativeDendriticPELSRuntime(case.topology, case.model,
                                         torch.zeros(1, 50_000, device=gpu), theta=theta,
-                                        propagation=propagation)
+                                        propagation=propagation, kernel=kernel)
     oracle = ort.PelsOracle(case.graph, case.params, torch.zeros(1, 50_000), theta=theta)
     bar = 1e-5 if theta == 0 else 1e-3
     worst = worst_current = 0.0
@@ -134,7 +142,8 @@ def test_cfg4_event_path_warmup_then_withdrawn(gpu, theta, propagation):
             else:
                 # theta = 0: every pair is active, so emitted tracks the state itself
                 assert max_err(native.emitted_state, native.state) <= 1e-6
-    print(f"cfg4 theta={theta} {propagation}: state {worst:.3e} current {worst_current:.3e} "
+    print(f"cfg4 theta={theta} {propagation} ({native.kernel} product): state {worst:.3e} "
+          f"current {worst_current:.3e} "
           f"emit-mask mismatches {mismatches}/{checked}; ticks by path {paths}")
     if propagation == "auto":
         # theta = 0: every pair is active (|0| >= 0), so after the first sample every
@@ -268,6 +277,16 @@ def test_propagation_modes_are_checked(gpu):
     with pytest.raises(ValueError, match="event_edge_fraction"):
         NativeDendriticPELSRuntime(case.topology, case.model, torch.zeros(1, 97, device=gpu),
                                    theta=0.0, propagation="auto", event_edge_fraction=1.5)
+    with pytest.raises(ValueError, match="'auto', 'rows' or 'panels'"):
+        NativeDendriticPELSRuntime(case.topology, case.model, torch.zeros(1, 97, device=gpu),
+                                   theta=0.0, propagation="matrix", kernel="bands")
+    with pytest.raises(ValueError, match="batch 1 or 2"):
+        NativeDendriticPELSRuntime(case.topology, case.model, torch.zeros(3, 97, device=gpu),
+                                   theta=0.0, propagation="matrix", kernel="panels")
+    scatter = NativeDendriticPELSRuntime(case.topology, case.model,
+                                         torch.zeros(1, 97, device=gpu), theta=0.0,
+                                         kernel="panels")
+    assert scatter.kernel == "rows"      # the event path multiplies nothing: no layout
 
 
 @pytest.mark.parametrize("batch,theta", [(1, 0.0), (1, 0.02), (3, 0.01), (2, 2.0)])
