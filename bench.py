@@ -96,8 +96,17 @@ def copy_calibration(mib: int = 256, repeats: int = 10) -> None:
 
 
 def launches_per_tick(runtime) -> int:
-    """Kernel launches of one tick: two on column panels whose row ranges are
-    finished by the combine kernel, one otherwise."""
+    """Kernel launches of one eager tick, counted as the kernel nodes of a graph
+    capturing it (the runtime's states are put back afterwards).  Where the HIP
+    runtime cannot be queried, the count the layout implies: two on column
+    panels finished by the combine kernel, one otherwise."""
+    graph, saved = captured_steps(runtime, [(0.2, 0.1)], STATE_FIELDS, keep_graph=True)
+    for f, value in zip(STATE_FIELDS, saved):
+        setattr(runtime, f, value)
+    counted = graph_nodes(graph)
+    del graph
+    if counted is not None:
+        return counted["kernels"]
     panels = getattr(runtime, "_panels", None)
     return 2 if panels is not None and panels.n_panels > 1 and panels.combine_launch else 1
 
