@@ -943,12 +943,15 @@ class NativeExtension:
                                   else _OutPlane(None, 0, 0))
         d_weight = torch.empty_like(weight) if need_weight else None
         args.d_weight = d_weight.data_ptr() if d_weight is not None and weight.numel() else None
-        d_params = [torch.empty(n, dtype=torch.float32, device=state.device) if want else None
-                    for want in need_params]
-        for i, value in enumerate(d_params):
-            args.d_params[i] = value.data_ptr() if value is not None else None
-        workspace = torch.empty(int(self.lib.ns_step_backward_workspace_floats(n, batch)),
-                                dtype=torch.float32, device=state.device)
+        # The wanted parameter gradients and the workspace share one allocation.
+        wanted = [i for i, want in enumerate(need_params) if want]
+        work = int(self.lib.ns_step_backward_workspace_floats(n, batch))
+        block = torch.empty(len(wanted) * n + work, dtype=torch.float32, device=state.device)
+        d_params = [None] * 6
+        for k, i in enumerate(wanted):
+            d_params[i] = block[k * n:(k + 1) * n]
+            args.d_params[i] = d_params[i].data_ptr()
+        workspace = block[len(wanted) * n:]
         args.workspace = workspace.data_ptr() if workspace.numel() else None
         stream = torch.cuda.current_stream(state.device).cuda_stream
         _raise_on(self.lib.ns_dendritic_step_backward(ctypes.byref(args), stream), self.lib)
@@ -1086,14 +1089,14 @@ def _consecutive(struct_type, names: tuple, size: int) -> int:
 # struct.pack_into each: five input planes (data, two strides, scalar), and
 # three or four output planes (data, two strides).
 _PLANES5 = struct.Struct("<" + "Qqqf4x" * 5)
-_OUTS3 = struct.Struct("<" + "Qqq" * 3)
 _OUTS4 = struct.Struct("<" + "Qqq" * 4)
 _CURRENT_EMITTED = struct.Struct("<Qqq" + "Qqqf4x")
 _EVENT_TAIL = struct.Struct("<QQQQiiQ")
 assert ctypes.sizeof(_Plane) == 32 and ctypes.sizeof(_OutPlane) == 24
 _IN_NAMES = ("state", "dendrite", "adaptation", "drive", "dendritic_drive")
 _STEP_IN = _consecutive(_StepArgs, _IN_NAMES, 32)
-_STEP_OUT = _consecutive(_StepArgs, ("out_state", "out_dendrite", "out_adaptation"), 24)
+_STEP_OUT = _consecutive(_StepArgs, ("out_state", "out_dendrite", "out_adaptation",
+                                     "out_current"), 24)
 _EVENT_IN = _consecutive(_EventArgs, _IN_NAMES, 32)
 _EVENT_OUT = _consecutive(_EventArgs, ("out_state", "out_dendrite", "out_adaptation",
                                        "out_emitted"), 24)
@@ -1103,6 +1106,18 @@ _EVENT_TAIL_AT = _consecutive(_EventArgs, ("delta", "pending_in", "pending_out",
 if (_EventArgs.flags.offset != _EVENT_TAIL_AT + 32
         or _EventArgs.activity.offset != _EVENT_TAIL_AT + 40):
     raise RuntimeError("_EventArgs: flags and activity must follow out_weight")
+_PLANES3 = struct.Struct("<" + "Qqqf4x" * 3)
+_OUTS5 = struct.Struct("<" + "Qqq" * 5)
+_POINTERS11 = struct.Struct("<" + "Q" * 11)
+_GRAD_IN = _consecutive(_StepGradArgs, _IN_NAMES, 32)
+_GRAD_UP = _consecutive(_StepGradArgs, ("grad_state", "grad_dendrite", "grad_adaptation"), 32)
+_GRAD_OUT = _consecutive(_StepGradArgs, ("d_state", "d_dendrite", "d_adaptation", "d_drive",
+                                         "d_dendritic_drive"), 24)
+_GRAD_POINTERS = _StepGradArgs.d_weight.offset
+if [getattr(_StepGradArgs, f).offset - _GRAD_POINTERS
+        for f in ("d_params", "workspace", "current", "out_weight", "transposed_panels")] \
+        != [8, 56, 64, 72, 80]:
+    raise RuntimeError("_StepGradArgs: the output pointers must be consecutive")
 
 
 def _plane_words(value: torch.Tensor, state: torch.Tensor, what: str) -> tuple:
@@ -1178,8 +1193,11 @@ class PreparedTick:
         return self._addresses(params, rowptr, col, weight) == self._pointers
 
     def __call__(self, state, dendrite, adaptation, drive, drive_scalar, dendritic_drive,
-                 dendritic_scalar) -> tuple:
-        """One tick; drives are validated [B,N] views or None with a scalar."""
+                 dendritic_scalar, current: bool = False) -> tuple:
+        """One tick; drives are validated [B,N] views or None with a scalar.
+        Returns the three new planes, and with ``current`` a fourth, j = W @ s
+        (neuron-major, from the same allocation), as a recorded tick's backward
+        reads it."""
         last = self._last
         if (last is not None and state is last[0] and dendrite is last[1]
                 and adaptation is last[2] and state.data_ptr() == last[3][0]
@@ -1202,10 +1220,12 @@ class PreparedTick:
                            *_drive_words(drive, drive_scalar, state),
                            *_drive_words(dendritic_drive, dendritic_scalar, state))
         batch, n = self.batch, self.n
-        storage = torch.empty((3, n, batch), dtype=torch.float32, device=self.device)
+        storage = torch.empty((4 if current else 3, n, batch), dtype=torch.float32,
+                              device=self.device)
         base, size = storage.data_ptr(), 4 * n * batch
         out = (base, 1, batch, base + size, 1, batch, base + 2 * size, 1, batch)
-        _OUTS3.pack_into(args, _STEP_OUT, *out)
+        _OUTS4.pack_into(args, _STEP_OUT, *out,
+                         *((base + 3 * size, 1, batch) if current else (0, 0, 0)))
         stream = current_stream(self.device)
         if self.bands is not None:
             code = self.lib.ns_dendritic_step_bands(self._ref, self._bands_ref, stream)
@@ -1216,6 +1236,117 @@ class PreparedTick:
         self._last = (outs[0], outs[1], outs[2],
                       (out[0], 1, batch, 0.0, out[3], 1, batch, 0.0, out[6], 1, batch, 0.0))
         return outs
+
+
+class PreparedBackward:
+    """The backward of a recorded matrix tick (ns_dendritic_step_backward) with
+    its fixed arguments validated once: the parameter vectors, the float32 CSR
+    with its row plan and the source-major view.  Each call validates the
+    forward's state planes, drives, upstream gradients, the forward's current
+    and the optional source-major weights, allocates the gradient planes (one
+    allocation), the weight gradient and the parameter gradients with the
+    workspace (one allocation), writes the per-call words and launches.  The
+    results equal ``NativeExtension.dendritic_step_backward`` on the same inputs."""
+
+    def __init__(self, extension: "NativeExtension", state: torch.Tensor, params, rowptr, col,
+                 weight, out_rowptr, dst, weight_index):
+        _check_state(state)
+        batch, n = state.shape
+        args = _StepGradArgs()
+        args.n_neurons, args.batch = n, batch
+        args.params = _params(params, state)
+        if weight.dtype != torch.float32:
+            raise RuntimeError("the tick backward needs float32 weights")
+        args.matrix = extension._csr(state, rowptr, col, weight, None, None)
+        bounds, blocks, capacity = extension.plan_tensors(rowptr, batch)
+        args.plan = _RowPlan(bounds.data_ptr(), blocks, capacity, 0)
+        for index in (out_rowptr, dst, weight_index):
+            _index(index, state)
+        if out_rowptr.numel() != n + 1 or dst.numel() != weight.numel() or \
+                weight_index.numel() != weight.numel():
+            raise RuntimeError("invalid source-major topology geometry")
+        args.out_rowptr, args.dst = out_rowptr.data_ptr(), dst.data_ptr()
+        args.out_weight_index = weight_index.data_ptr()
+        self.lib, self.args, self._ref = extension.lib, args, ctypes.byref(args)
+        self.batch, self.n, self.shape, self.device = batch, n, state.shape, state.device
+        self.params = tuple(params)
+        self._work = int(extension.lib.ns_step_backward_workspace_floats(n, batch))
+        self._tensors = (rowptr, col, weight, out_rowptr, dst, weight_index)
+        self._bounds = bounds
+
+    def matches(self, state, params, rowptr, col, weight, out_rowptr, dst, weight_index) -> bool:
+        """Whether the given tensors are those prepared: the same objects, or (as
+        autograd's saved tensors may be) tensors over the same memory with the same
+        layout."""
+        given = tuple(params) + (rowptr, col, weight, out_rowptr, dst, weight_index)
+        mine = self.params + self._tensors
+        if state.shape != self.shape or len(given) != len(mine):
+            return False
+        return all(a is b or (a.data_ptr() == b.data_ptr() and a.dtype == b.dtype
+                              and a.shape == b.shape and a.stride() == b.stride())
+                   for a, b in zip(given, mine))
+
+    def __call__(self, state, dendrite, adaptation, drive, drive_scalar, dendritic_drive,
+                 dendritic_scalar, grad_state, grad_dendrite, grad_adaptation, *,
+                 need_drive=False, need_dendritic=False, need_weight=False,
+                 need_params=(False,) * 6, out_weight=None, current=None,
+                 transposed_panels=None):
+        _check_state(state)
+        if state.shape != self.shape:
+            raise RuntimeError("state/current/drive shape mismatch")
+        batch, n, weight = self.batch, self.n, self._tensors[2]
+        args = self.args
+        _PLANES5.pack_into(args, _GRAD_IN,
+                           *_plane_words(state, state, "state"), 0.0,
+                           *_plane_words(dendrite, state, "dendrite"), 0.0,
+                           *_plane_words(adaptation, state, "adaptation"), 0.0,
+                           *_drive_words(drive, drive_scalar, state),
+                           *_drive_words(dendritic_drive, dendritic_scalar, state))
+        _PLANES3.pack_into(args, _GRAD_UP, *_drive_words(grad_state, 0.0, state),
+                           *_drive_words(grad_dendrite, 0.0, state),
+                           *_drive_words(grad_adaptation, 0.0, state))
+        out_weight_ptr = 0
+        if out_weight is not None:
+            _check_float(out_weight, state, "source-major weights")
+            if out_weight.numel() != weight.numel() or not out_weight.is_contiguous():
+                raise RuntimeError("source-major weights must be a contiguous [M] vector")
+            out_weight_ptr = out_weight.data_ptr() if out_weight.numel() else 0
+        current_ptr = 0
+        if current is not None:
+            _check_float(current, state, "current")
+            if current.shape != state.shape or current.stride() != (1, batch):
+                raise RuntimeError("current must be a neuron-major [B,N] plane")
+            current_ptr = current.data_ptr()
+        count = 3 + int(need_drive) + int(need_dendritic)
+        storage = torch.empty((count, n, batch), dtype=torch.float32, device=self.device)
+        base, size = storage.data_ptr(), 4 * n * batch
+        words = []
+        for k in range(5):
+            present = k < 3 or (k == 3 and need_drive) or (k == 4 and need_dendritic)
+            index = k if k < 4 else count - 1
+            words += (base + index * size, 1, batch) if present else (0, 0, 0)
+        _OUTS5.pack_into(args, _GRAD_OUT, *words)
+        planes = storage.transpose(1, 2).unbind(0)
+        d_weight = torch.empty_like(weight) if need_weight else None
+        wanted = [i for i, want in enumerate(need_params) if want]
+        block = torch.empty(len(wanted) * n + self._work, dtype=torch.float32,
+                            device=self.device)
+        d_params = [None] * 6
+        param_ptrs = [0] * 6
+        for k, i in enumerate(wanted):
+            d_params[i] = block[k * n:(k + 1) * n]
+            param_ptrs[i] = d_params[i].data_ptr()
+        workspace_ptr = block.data_ptr() + 4 * len(wanted) * n if self._work else 0
+        _POINTERS11.pack_into(args, _GRAD_POINTERS,
+                              d_weight.data_ptr() if d_weight is not None and weight.numel() else 0,
+                              *param_ptrs, workspace_ptr, current_ptr, out_weight_ptr,
+                              ctypes.addressof(transposed_panels) if transposed_panels is not None
+                              else 0)
+        _raise_on(self.lib.ns_dendritic_step_backward(self._ref, current_stream(self.device)),
+                  self.lib)
+        d_drive = planes[3] if need_drive else None
+        d_dendritic = planes[count - 1] if need_dendritic else None
+        return (planes[0], planes[1], planes[2], d_drive, d_dendritic, d_weight, d_params)
 
 
 class PreparedEvent:

@@ -30,9 +30,9 @@ import torch
 
 from .compartmental import DendriticDynamics, DendriticMatrixRuntime, DendriticPELSRuntime
 from .native import (BAND_WIDTH, EVENT_ACTIVITY_SLOTS, EVENT_ACTIVITY_STRIDE, BandLayout,
-                     NativeExtension, PanelLayout, PreparedAccumulate, PreparedEvent,
-                     PreparedTick, encode_weights,
-                     load_native_extension, new_planes, panel_geometry)
+                     NativeExtension, PanelLayout, PreparedAccumulate, PreparedBackward,
+                     PreparedEvent, PreparedTick, encode_weights,
+                     load_native_extension, panel_geometry)
 from .topology import SparseTopology
 
 
@@ -56,8 +56,11 @@ class _NativeCompartments:
         self.last_backend = "unstepped"
         # The eager tick's launch arguments, validated once and reused while the
         # parameters, weights and layout stay the same objects (PreparedTick,
-        # PreparedEvent).
-        self._prepared = None
+        # PreparedEvent), and those of a tick recorded for autograd.
+        self._prepared = self._prepared_recorded = None
+        # The backward's prepared launch, shared by the ticks recorded here (a
+        # one-element holder, since the backward runs after the forward returns).
+        self._prepared_backward = [None]
 
     def _parameters(self) -> list[torch.Tensor]:
         model = self.compartment_dynamics
@@ -188,13 +191,12 @@ class _NativeTick(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, info, state, dendrite, adaptation, weight, drive, dendritic_drive, *params):
-        extension, topology, us, vs, width, extra, _, _ = info
-        # j = W @ s kept for the backward, which then needs no product of its own
-        current = new_planes(1, state.shape[0], state.shape[1], state)[0]
-        outs = extension.dendritic_step(state, dendrite, adaptation, list(params),
-                                        topology.in_rowptr, topology.in_col, weight,
-                                        drive, us, dendritic_drive, vs, width, **extra,
-                                        current_out=current)
+        _, _, us, vs, tick, _, _, _ = info
+        # The launch arguments were prepared (and validated) for this weight, plan
+        # and these parameters; j = W @ s is kept for the backward, which then
+        # needs no product of its own.
+        *outs, current = tick(state, dendrite, adaptation, drive, us, dendritic_drive, vs,
+                              current=True)
         ctx.current = current
         ctx.info = info
         ctx.has_drive = (drive is not None, dendritic_drive is not None)
@@ -206,7 +208,7 @@ class _NativeTick(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_state, grad_dendrite, grad_adaptation):
-        extension, topology, us, vs, _, _, source_major, transposed = ctx.info
+        extension, topology, us, vs, _, source_major, transposed, cache = ctx.info
         saved = list(ctx.saved_tensors)
         state, dendrite, adaptation, weight = saved[:4]
         params = saved[4:10]
@@ -217,12 +219,16 @@ class _NativeTick(torch.autograd.Function):
         panels = transposed.plan(weight) if transposed is not None else None
         out_weight = (None if panels is not None
                       else source_major.get(weight, topology.out_weight_index))
+        fixed = (topology.in_rowptr, topology.in_col, weight, topology.out_rowptr,
+                 topology.dst, topology.out_weight_index)
+        prepared = cache[0]
+        if prepared is None or not prepared.matches(state, params, *fixed):
+            prepared = cache[0] = PreparedBackward(extension, state, params, *fixed)
         (d_state, d_dendrite, d_adaptation, d_drive, d_dendritic, d_weight,
-         d_params) = extension.dendritic_step_backward(
-            state, dendrite, adaptation, params, topology.in_rowptr, topology.in_col, weight,
-            drive, us, dendritic_drive, vs, topology.out_rowptr, topology.dst,
-            topology.out_weight_index, grad_state, grad_dendrite, grad_adaptation,
-            need_drive=bool(needs[5]), need_dendritic=bool(needs[6]), need_weight=bool(needs[4]),
+         d_params) = prepared(
+            state, dendrite, adaptation, drive, us, dendritic_drive, vs, grad_state,
+            grad_dendrite, grad_adaptation, need_drive=bool(needs[5]),
+            need_dendritic=bool(needs[6]), need_weight=bool(needs[4]),
             need_params=tuple(bool(x) for x in needs[7:13]),
             out_weight=out_weight, current=ctx.current, transposed_panels=panels)
         ctx.current = None
@@ -561,16 +567,22 @@ class NativeDendriticMatrixRuntime(_NativeCompartments, DendriticMatrixRuntime):
         """A float32 tick recorded for autograd, native forward and backward."""
         u, us = self._drive(drive)
         v, vs = self._drive(dendritic_drive)
-        weight = self.topology.in_weight
+        topology, weight, params = self.topology, self.topology.in_weight, self._parameters()
         extra = {}
         plan = self._recorded_panel_plan(weight)
         if plan is not None:
             extra["panels"] = plan
-        info = (self.extension, self.topology, us, vs, self.threads_per_row, extra,
-                self.source_major_weights, self._transposed_layout())
+        tick = self._prepared_recorded
+        if tick is None or not tick.matches(self.state, params, topology.in_rowptr,
+                                            topology.in_col, weight, **extra):
+            tick = self._prepared_recorded = PreparedTick(
+                self.extension, self.state, params, topology.in_rowptr, topology.in_col,
+                weight, **extra)
+        info = (self.extension, topology, us, vs, tick, self.source_major_weights,
+                self._transposed_layout(), self._prepared_backward)
         self.state, self.dendritic_state, self.adaptation_state = _NativeTick.apply(
             info, self.state, self.dendritic_state, self.adaptation_state, weight, u, v,
-            *self._parameters())
+            *params)
         self.last_backend = "native-autograd"
         return self.state
 

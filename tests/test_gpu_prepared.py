@@ -197,3 +197,65 @@ def test_prepared_accumulate_equals_csr_spmm(gpu, batch):
         ext.csr_spmm(delta, topo.in_rowptr, topo.in_col, topo.in_weight, accumulate_into=a)
         product()
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("batch,drives,upstream,extras", [
+    (1, "scalar", "all", "none"), (2, "tensor", "all", "current"),
+    (1, "tensor", "state_only", "out_weight"), (2, "scalar", "all", "panels"),
+    (3, "tensor", "state_only", "current")])
+def test_prepared_backward_equals_dendritic_step_backward(gpu, batch, drives, upstream, extras):
+    """The recorded tick's backward through PreparedBackward against the validated
+    call, bitwise (every backward kernel is deterministic)."""
+    print(f"case prepared backward B={batch} drives={drives} upstream={upstream} "
+          f"extras={extras}", flush=True)
+    from neurosim_gpu.native import PreparedBackward
+    from neurosim_gpu.native_compartmental import TransposedPanels
+
+    case = make_case(N, M, SEED, gpu)
+    topo = case.topology
+    runtime = NativeDendriticMatrixRuntime(topo, case.model, torch.zeros(batch, N, device=gpu),
+                                           kernel="rows")
+    ext, params = load_native_extension(), runtime._parameters()
+    gen = torch.Generator().manual_seed(batch)
+    planes = clone_planes([torch.rand(batch, N, generator=gen).to(gpu) for _ in range(3)])
+    if drives == "tensor":
+        u = column_drive(batch).to(gpu).expand(batch, N)
+        v = torch.rand(batch, N, generator=gen).to(gpu)
+        us = vs = 0.0
+        need_drive = need_dendritic = True
+    else:
+        u = v = None
+        us, vs = 0.2, 0.1
+        need_drive = need_dendritic = False
+    grads = [torch.randn(batch, N, generator=gen).to(gpu) for _ in range(3)]
+    if upstream == "state_only":
+        grads[1] = grads[2] = None
+    extra = {}
+    if extras == "current":
+        current = clone_planes([torch.rand(batch, N, generator=gen).to(gpu)])[0]
+        extra["current"] = current
+    elif extras == "out_weight":
+        extra["out_weight"] = topo.in_weight[topo.out_weight_index.long()].contiguous()
+    elif extras == "panels":
+        layout = TransposedPanels(topo, batch, gpu, max_panel_width=1024)
+        assert layout.plan(topo.in_weight) is None      # the copy is made on the second request
+        extra["transposed_panels"] = layout.plan(topo.in_weight)
+    fixed = (topo.in_rowptr, topo.in_col, topo.in_weight, topo.out_rowptr, topo.dst,
+             topo.out_weight_index)
+    flags = dict(need_drive=need_drive, need_dendritic=need_dendritic, need_weight=True,
+                 need_params=(True, False, True, True, False, True))
+    expected = ext.dendritic_step_backward(*planes, params, fixed[0], fixed[1], fixed[2], u, us,
+                                           v, vs, fixed[3], fixed[4], fixed[5], *grads,
+                                           **flags, **extra)
+    prepared = PreparedBackward(ext, planes[0], params, *fixed)
+    assert prepared.matches(planes[0], params, *fixed)
+    for _ in range(2):
+        got = prepared(*planes, u, us, v, vs, *grads, **flags, **extra)
+        for a, b in zip(expected[:6], got[:6]):
+            assert (a is None) == (b is None)
+            if a is not None:
+                assert torch.equal(a, b)
+        for a, b in zip(expected[6], got[6]):
+            assert (a is None) == (b is None)
+            if a is not None:
+                assert torch.equal(a, b)
