@@ -1085,14 +1085,19 @@ def _consecutive(struct_type, names: tuple, size: int) -> int:
     return offsets[0]
 
 
-# Per-tick words of the step and event argument structs, written with one
-# struct.pack_into each: five input planes (data, two strides, scalar), and
-# three or four output planes (data, two strides).
+# The per-tick words of the step, event and step-backward argument structs are
+# written with one struct.pack_into per run of consecutive fields: input planes
+# (data, two strides, scalar: 32 bytes), output planes (data, two strides: 24
+# bytes) and pointers.  The offsets below are checked against the ctypes layouts.
 _PLANES5 = struct.Struct("<" + "Qqqf4x" * 5)
+_PLANES3 = struct.Struct("<" + "Qqqf4x" * 3)
 _OUTS4 = struct.Struct("<" + "Qqq" * 4)
+_OUTS5 = struct.Struct("<" + "Qqq" * 5)
+_POINTERS11 = struct.Struct("<" + "Q" * 11)
 _CURRENT_EMITTED = struct.Struct("<Qqq" + "Qqqf4x")
 _EVENT_TAIL = struct.Struct("<QQQQiiQ")
-assert ctypes.sizeof(_Plane) == 32 and ctypes.sizeof(_OutPlane) == 24
+if ctypes.sizeof(_Plane) != 32 or ctypes.sizeof(_OutPlane) != 24:
+    raise RuntimeError("plane structs must be 32 and 24 bytes")
 _IN_NAMES = ("state", "dendrite", "adaptation", "drive", "dendritic_drive")
 _STEP_IN = _consecutive(_StepArgs, _IN_NAMES, 32)
 _STEP_OUT = _consecutive(_StepArgs, ("out_state", "out_dendrite", "out_adaptation",
@@ -1106,9 +1111,6 @@ _EVENT_TAIL_AT = _consecutive(_EventArgs, ("delta", "pending_in", "pending_out",
 if (_EventArgs.flags.offset != _EVENT_TAIL_AT + 32
         or _EventArgs.activity.offset != _EVENT_TAIL_AT + 40):
     raise RuntimeError("_EventArgs: flags and activity must follow out_weight")
-_PLANES3 = struct.Struct("<" + "Qqqf4x" * 3)
-_OUTS5 = struct.Struct("<" + "Qqq" * 5)
-_POINTERS11 = struct.Struct("<" + "Q" * 11)
 _GRAD_IN = _consecutive(_StepGradArgs, _IN_NAMES, 32)
 _GRAD_UP = _consecutive(_StepGradArgs, ("grad_state", "grad_dendrite", "grad_adaptation"), 32)
 _GRAD_OUT = _consecutive(_StepGradArgs, ("d_state", "d_dendrite", "d_adaptation", "d_drive",
