@@ -532,3 +532,49 @@ def test_accumulated_spmm_output_must_not_overlap_itself(lib):
     args.accumulate = 1
     rc = lib.ns_csr_spmm(ctypes.byref(args), None)
     assert rc == 1 and "must not overlap itself" in lib.ns_last_error().decode()
+
+
+def test_packed_argument_words_land_in_their_fields():
+    """The prepared launches write per-tick words with struct.pack_into at fixed
+    offsets; reading the ctypes fields back pins those layouts."""
+    import neurosim_gpu.native as nv
+
+    def planes(count, start):
+        words = []
+        for k in range(count):
+            words += [start + 100 * k, -(k + 1), k + 7, float(k) + 0.5]
+        return words
+
+    step = nv._StepArgs()
+    nv._PLANES5.pack_into(step, nv._STEP_IN, *planes(5, 1000))
+    nv._OUTS4.pack_into(step, nv._STEP_OUT, *(v for k in range(4) for v in (2000 + k, 1, k + 3)))
+    for k, name in enumerate(nv._IN_NAMES):
+        plane = getattr(step, name)
+        assert (plane.data, plane.stride_b, plane.stride_n, plane.scalar) == \
+            (1000 + 100 * k, -(k + 1), k + 7, k + 0.5)
+    for k, name in enumerate(("out_state", "out_dendrite", "out_adaptation", "out_current")):
+        plane = getattr(step, name)
+        assert (plane.data, plane.stride_b, plane.stride_n) == (2000 + k, 1, k + 3)
+
+    event = nv._EventArgs()
+    nv._PLANES5.pack_into(event, nv._EVENT_IN, *planes(5, 3000))
+    nv._CURRENT_EMITTED.pack_into(event, nv._EVENT_CURRENT, 4000, 2, 3, 4100, 5, 6, 1.5)
+    nv._EVENT_TAIL.pack_into(event, nv._EVENT_TAIL_AT, 11, 12, 13, 14, 1, 0, 15)
+    nv._OUTS4.pack_into(event, nv._EVENT_OUT, *(v for k in range(4) for v in (5000 + k, 1, 2)))
+    assert event.state.data == 3000 and event.dendritic_drive.scalar == 4.5
+    assert (event.current, event.current_stride_b, event.current_stride_n) == (4000, 2, 3)
+    assert (event.emitted.data, event.emitted.stride_n, event.emitted.scalar) == (4100, 6, 1.5)
+    assert (event.delta, event.pending_in, event.pending_out, event.out_weight) == (11, 12, 13, 14)
+    assert (event.flags, event.activity) == (1, 15)
+    assert event.out_emitted.data == 5003
+
+    grad = nv._StepGradArgs()
+    nv._PLANES5.pack_into(grad, nv._GRAD_IN, *planes(5, 6000))
+    nv._PLANES3.pack_into(grad, nv._GRAD_UP, *planes(3, 7000))
+    nv._OUTS5.pack_into(grad, nv._GRAD_OUT, *(v for k in range(5) for v in (8000 + k, 1, 9)))
+    nv._POINTERS11.pack_into(grad, nv._GRAD_POINTERS, *range(9000, 9011))
+    assert grad.adaptation.data == 6200 and grad.grad_adaptation.data == 7200
+    assert grad.d_dendritic_drive.data == 8004
+    assert grad.d_weight == 9000 and list(grad.d_params) == list(range(9001, 9007))
+    assert (grad.workspace, grad.current, grad.out_weight, grad.transposed_panels) == \
+        (9007, 9008, 9009, 9010)
