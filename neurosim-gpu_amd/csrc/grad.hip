@@ -253,6 +253,9 @@ extern "C" int ns_dendritic_step_backward(const ns_step_grad_args* args, void* s
     transposed.state = ns_plane{gj, 1, batch, 0.0f};
     transposed.matrix.n_rows = n; transposed.matrix.n_edges = a.matrix.n_edges;
     transposed.matrix.format = NS_WEIGHT_F32;
+    // An indexed plan (NS_PANEL_INDEXED) reads each slot's weight from the CSR
+    // weights through the slot's edge number.
+    transposed.matrix.weight = a.matrix.weight;
     transposed.panels = a.transposed_panels;
     transposed.out_state = a.d_state;
     if (int rc = panel_step(transposed, s, 2, false)) return rc;

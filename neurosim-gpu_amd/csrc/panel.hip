@@ -814,6 +814,8 @@ int panel_step(const ns_step_args& a, hipStream_t stream, int product, bool laun
   const bool indexed = (pl.flags & NS_PANEL_INDEXED) != 0;
   if (indexed && a.matrix.format != NS_WEIGHT_F32)
     return fail("an indexed panel plan reads float32 CSR weights");
+  if (indexed && a.matrix.n_edges > 0 && !a.matrix.weight)
+    return fail("an indexed panel plan needs the CSR weights");
   // The products always finish in the second kernel.
   const bool one_launch = !product && pl.n_panels > 1 && !(pl.flags & NS_PANEL_COMBINE_LAUNCH);
   if (one_launch) {

@@ -151,13 +151,15 @@ class TransposedPanels:
     """Column-panel layout of the transposed matrix, for the backward's W^T @ g.
 
     Its rows are the sources (``out_rowptr``, ``dst``: the source-major view)
-    and its slots name CSR positions through ``out_weight_index``, so the slot
-    weights are gathered from the CSR-order weights directly.  That gather is
-    one random read per edge, as costly as the out-edge walk it replaces, so
-    it is made on the second request for one weight version (backpropagation
-    through several ticks, or repeated passes on fixed weights); the first
-    request returns None and the backward walks the out-edges.  Built on the
-    host from the source-major view (set-up only, like the forward's layout)."""
+    and its slots name CSR positions through ``out_weight_index``.  On the
+    first request for a weight version the plan is indexed (NS_PANEL_INDEXED):
+    the kernel reads each slot's weight from the CSR-order weights through
+    that position, so a weight version used once (an optimizer step before
+    every backward) needs no copy.  The slot-order copy, one random read per
+    edge, is made on the second request (backpropagation through several
+    ticks, or repeated passes on fixed weights), and streamed after that.
+    Built on the host from the source-major view (set-up only, like the
+    forward's layout)."""
 
     def __init__(self, topology, batch: int, device, *, max_panel_width: int | None = None) -> None:
         view = SimpleNamespace(n_neurons=topology.n_neurons, n_edges=topology.n_edges,
@@ -169,16 +171,21 @@ class TransposedPanels:
         self.layout.perm = torch.where(perm >= 0, owi[perm.clamp(min=0).long()],
                                        perm).to(torch.int32).contiguous()
         self._key, self._source, self._seen = None, None, 0
+        self._indexed = None
 
     def plan(self, weight: torch.Tensor):
-        """The plan struct with ``weight`` (float32, CSR order) in slot order,
-        or None on the first request for this weight version."""
+        """The plan struct for ``weight`` (float32, CSR order): on the first
+        request for a weight version the indexed plan, whose slots carry CSR
+        edge numbers so the kernel reads ``weight`` in place; from the second on,
+        ``weight`` gathered into slot order once."""
         key = _weight_key(weight)
         if key != self._key or self._source is not weight:
             self._key, self._source, self._seen = key, weight, 0
         self._seen += 1
         if self._seen < 2:
-            return None
+            if self._indexed is None:
+                self._indexed = self.layout.indexed_plan_struct()
+            return self._indexed
         slots, _ = self.layout.slot_weights(key, weight, None)
         return self.layout.plan_struct(slots, None)
 

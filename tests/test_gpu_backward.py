@@ -191,6 +191,47 @@ def test_transposed_product_on_panels_matches_the_oracle(gpu, ticks, batch, widt
     compare(native, {k: v.detach().double().cpu() for k, v in walked.items()}, rtol=1e-5)
 
 
+@pytest.mark.parametrize("batch", [1, 2])
+def test_first_backward_of_a_weight_version_reads_the_weights_in_place(gpu, batch):
+    """One recorded tick per weight version (an optimizer step before every pass):
+    the transposed product runs on the indexed plan, reading the CSR weights
+    through the slots' edge numbers, where it used to walk the out-edges.  The
+    gradients match the oracle and equal bitwise those of a second backward of the
+    same version, which streams the slot-order copy."""
+    print(f"case backward indexed transposed plan batch={batch}", flush=True)
+    g = graph(3000, 90_000, 17)
+    inputs = inputs_for(g, batch, 60 + batch)
+    kw = dict(scalar_drives=False, expanded=False, kernel="panels", panel_width=1000)
+    first, rt = run(NativeDendriticMatrixRuntime, g, inputs, torch.float32, gpu, 1, **kw)
+    assert rt._transposed is not None and rt._transposed._seen == 1
+    assert rt._transposed.layout._slot_weights is None      # the indexed plan ran
+    compare(first, oracle_gradients(g, inputs, 1, scalar_drives=False, expanded=False))
+
+    def again():
+        """The same tick and loss once more, on the same weights (leaves reset)."""
+        topo, mdl = rt.topology, rt.compartment_dynamics
+        for t in [topo.in_weight, *params_of(mdl)]:
+            base(t).grad = None
+        state0 = leaf(inputs["state"], torch.float32, gpu)
+        rt.state = state0
+        rt.dendritic_state = leaf(inputs["dendrite"], torch.float32, gpu)
+        rt.adaptation_state = leaf(inputs["adaptation"], torch.float32, gpu)
+        drive = leaf(inputs["drive"], torch.float32, gpu)
+        dendritic = leaf(inputs["dendritic"], torch.float32, gpu)
+        rt.step(drive, dendritic_drive=dendritic)
+        r = {k: torch.tensor(v, dtype=torch.float32, device=gpu)
+             for k, v in inputs["probe"].items()}
+        loss = (rt.state * r["s"]).sum() + (rt.dendritic_state * r["d"]).sum() + \
+            (rt.adaptation_state * r["a"]).sum()
+        loss.backward()
+        return {"weight": topo.in_weight.grad, "state": state0.grad}
+
+    second = again()
+    assert rt._transposed.layout._slot_weights is not None  # the slot-order copy ran
+    for name in second:
+        assert torch.equal(first[name], second[name]), name
+
+
 def test_backward_is_repeatable(gpu):
     print("case backward repeatable", flush=True)
     g = graph(2000, 60_000, 3)

@@ -238,8 +238,12 @@ def test_prepared_backward_equals_dendritic_step_backward(gpu, batch, drives, up
         extra["out_weight"] = topo.in_weight[topo.out_weight_index.long()].contiguous()
     elif extras == "panels":
         layout = TransposedPanels(topo, batch, gpu, max_panel_width=1024)
-        assert layout.plan(topo.in_weight) is None      # the copy is made on the second request
+        from neurosim_gpu.native import PANEL_INDEXED
+
+        # The first request gives the indexed plan, the second the slot-order copy.
+        assert layout.plan(topo.in_weight).flags & PANEL_INDEXED
         extra["transposed_panels"] = layout.plan(topo.in_weight)
+        assert not extra["transposed_panels"].flags & PANEL_INDEXED
     fixed = (topo.in_rowptr, topo.in_col, topo.in_weight, topo.out_rowptr, topo.dst,
              topo.out_weight_index)
     flags = dict(need_drive=need_drive, need_dendritic=need_dendritic, need_weight=True,
