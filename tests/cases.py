@@ -8,6 +8,7 @@ equality is re-checked for the arrays the kernels read.
 
 from __future__ import annotations
 
+import sys
 from dataclasses import dataclass
 
 import numpy as np
@@ -76,3 +77,9 @@ def max_err(a: torch.Tensor, b: torch.Tensor) -> float:
 def column_drive(batch: int, seed: int = 1) -> torch.Tensor:
     """Per-column drive U(0, 0.4) of shape [B, 1] from a CPU generator."""
     return torch.rand((batch, 1), generator=torch.Generator().manual_seed(seed)) * 0.4
+
+
+def progress(message: str) -> None:
+    """A line on the process's real stderr, past pytest's capture: long host
+    phases of a GPU test (graph builds, oracle runs) show that they advance."""
+    print(f"[progress] {message}", file=sys.__stderr__, flush=True)

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from cases import column_drive, make_case, max_err, model_to, standard_model
+from cases import column_drive, make_case, max_err, model_to, progress, standard_model
 from oracle import precision as op
 from oracle import runtime as ort
 from oracle import topology as otop
@@ -312,25 +312,41 @@ def test_cfg3_large_1000_ticks(gpu, large_case, fmt):
     assert worst <= 1e-5 and worst_rollout <= 1e-5
 
 
-def test_cfg5_scaleout_fp8_against_an_independent_graph(gpu):
-    """N=1000000, M~100M, B=16, drive [16,1] U(0,.4) seed 1, fp8 weights.
-
-    The oracle builds its own graph from the same draws (oracle.topology, numpy
-    coalescing); the product's CPU build and its GPU build (ns_build_topology) must
-    both equal it bitwise.  Then 10 eager ticks against the oracle's float32 run on
-    the decoded weights, every tick, and the timed path: a graph of 100 captured
-    ticks replayed from the same zero state, against the oracle at tick 100."""
-    print("case cfg5 N=1000000 M=100M B=16 fp8 ticks=10 eager + 100 graph", flush=True)
-    n, batch = 1_000_000, 16
+@pytest.fixture(scope="module")
+def cfg5(gpu):
+    """N=1000000, M~100M candidates (seed 0): the oracle's own graph from the
+    draws (oracle.topology, numpy coalescing), the product's CPU build and its
+    GPU build (ns_build_topology).  Several minutes of host work in all, so each
+    phase reports on the real stderr."""
+    n = 1_000_000
+    progress("cfg5: oracle graph from 100M candidate draws (numpy coalescing)")
     graph = otop.random_graph(n, 100_000_000, seed=0)
+    progress("cfg5: the product's CPU build")
     topology_cpu = random_topology(n, 100_000_000, device="cpu", seed=0)
+    progress("cfg5: the product's GPU build")
     topology = random_topology(n, 100_000_000, device="cpu", seed=0, build_device=gpu)
+    progress(f"cfg5: {graph.n_edges} edges built three ways")
+    return graph, topology_cpu, topology
+
+
+def test_cfg5_three_constructions_of_the_scaleout_graph_are_bitwise_equal(cfg5):
+    graph, topology_cpu, topology = cfg5
     for name in ("src", "dst", "weight", "out_rowptr", "in_rowptr", "in_col", "in_weight",
                  "out_weight_index"):
         assert np.array_equal(getattr(topology_cpu, name).numpy(), getattr(graph, name)), name
         assert torch.equal(getattr(topology, name).cpu(), getattr(topology_cpu, name)), name
-    del topology_cpu
-    print(f"cfg5 graph: {graph.n_edges} edges, three constructions bitwise equal", flush=True)
+
+
+def test_cfg5_scaleout_fp8_against_an_independent_graph(gpu, cfg5):
+    """N=1000000, M~100M, B=16, drive [16,1] U(0,.4) seed 1, fp8 weights, on the
+    GPU build of the graph; the oracle runs on its own construction (bitwise
+    the same arrays, previous test).  10 eager ticks against the oracle's float32
+    run on the decoded weights, every tick, and the timed path: a graph of 100
+    captured ticks replayed from the same zero state, against the oracle at tick
+    100."""
+    print("case cfg5 N=1000000 M=100M B=16 fp8 ticks=10 eager + 100 graph", flush=True)
+    graph, _, topology = cfg5
+    n, batch = 1_000_000, 16
     model, params = standard_model(n)
     native = NativeDendriticMatrixRuntime(topology, model_to(model, gpu),
                                           torch.zeros(batch, n, device=gpu), weight_format="fp8")
@@ -346,8 +362,10 @@ def test_cfg5_scaleout_fp8_against_an_independent_graph(gpu):
             oracle.step(drive, 0.1)
             worst = max(worst, errors(native, oracle))
         rollout.run()
-        for _ in range(90):
+        for k in range(90):
             oracle.step(drive, 0.1)
+            if k % 30 == 29:
+                progress(f"cfg5: oracle tick {k + 11} of 100")
         worst_rollout = errors(rollout, oracle)
     print(f"cfg5 fp8 max abs error: eager ticks 1-10 {worst:.3e}, "
           f"graph of 100 ticks {worst_rollout:.3e}", flush=True)
