@@ -43,6 +43,16 @@ N, EDGES, BATCH, CHUNK, INTERVAL = 1024, 16_384, 4, 32, 256
 BAR = 1e-5
 
 
+@pytest.fixture(autouse=True)
+def one_host_thread():
+    """The oracle's ticks on a 4096-neuron union are faster on one host thread;
+    the thread count is restored for the tests that follow."""
+    previous = torch.get_num_threads()
+    torch.set_num_threads(1)
+    yield
+    torch.set_num_threads(previous)
+
+
 def build(scenario: str, seed: int, gpu):
     """The native case (every mode) and the oracle over the modes' decoded weights."""
     p = scenario_parameters(scenario)
@@ -100,7 +110,6 @@ def against_native_fp32(case: DriftCase) -> dict:
 def test_drift_in_every_weight_mode_against_the_oracle(gpu, scenario, seed, ticks):
     print(f"case drift {scenario} seed {seed}: N={N} candidate edges={EDGES} B={BATCH} "
           f"ticks={ticks} modes={MODES}", flush=True)
-    torch.set_num_threads(1)
     case, oracle = build(scenario, seed, gpu)
     worst = {mode: 0.0 for mode in MODES}
     drift = {mode: 0.0 for mode in MODES[1:]}
@@ -129,7 +138,6 @@ def test_recurrent_stress_drift(gpu, seed):
     ticks, oracle_cap, agree_ticks = 100_000, 20_000, 50
     print(f"case drift recurrent_stress seed {seed}: N={N} candidate edges={EDGES} "
           f"B={BATCH} ticks={ticks}", flush=True)
-    torch.set_num_threads(1)
     case, oracle = build("recurrent_stress", seed, gpu)
     levels = (1e-4, 1e-2)
     first_max = {mode: {lv: None for lv in levels} for mode in MODES}
