@@ -1207,6 +1207,8 @@ class PreparedTick:
             words = last[3]
         else:
             _check_state(state)
+            if state.device != self.device:
+                raise RuntimeError("all tensors must be on the state's CUDA device")
             if state.shape != self.shape:
                 raise RuntimeError("state/current/drive shape mismatch")
             if self.bands is not None and not (
@@ -1294,6 +1296,8 @@ class PreparedBackward:
                  need_params=(False,) * 6, out_weight=None, current=None,
                  transposed_panels=None):
         _check_state(state)
+        if state.device != self.device:
+            raise RuntimeError("all tensors must be on the state's CUDA device")
         if state.shape != self.shape:
             raise RuntimeError("state/current/drive shape mismatch")
         batch, n, weight = self.batch, self.n, self._tensors[2]
@@ -1438,6 +1442,8 @@ class PreparedEvent:
             words = last[4]
         else:
             _check_state(state)
+            if state.device != self.device:
+                raise RuntimeError("all tensors must be on the state's CUDA device")
             if state.shape != self.shape:
                 raise RuntimeError("state/current/drive shape mismatch")
             words = (_plane_words(state, state, "state") + (0.0,)
