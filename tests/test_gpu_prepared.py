@@ -36,11 +36,12 @@ def clone_planes(planes):
 
 @pytest.mark.parametrize("kernel,batch", [("rows", 1), ("rows", 3), ("panels", 1),
                                           ("panels", 2), ("bands", 4), ("bands", 8)])
-@pytest.mark.parametrize("fmt", ["fp32", "fp8", "nvfp4"])
+@pytest.mark.parametrize("fmt", ["fp32", "fp16", "fp8", "nvfp4"])
 def test_prepared_tick_equals_dendritic_step(gpu, kernel, batch, fmt):
     print(f"case prepared tick kernel={kernel} B={batch} fmt={fmt}", flush=True)
     case = make_case(N, M, SEED, gpu)
-    options = {} if fmt == "fp32" else {"weight_format": fmt}
+    options = ({} if fmt == "fp32" else {"weight_dtype": torch.float16} if fmt == "fp16"
+               else {"weight_format": fmt})
     if kernel == "panels":
         options.update(panel_width=1024, panel_tiles=5)
     runtime = NativeDendriticMatrixRuntime(case.topology, case.model,
