@@ -260,8 +260,56 @@ __global__ __launch_bounds__(kThreads) void tick_kernel(TickArgs A) {
   for (int r = tid; r <= nrows; r += kThreads) srow[r] = A.rowptr[r0 + r];
 
   // Phase 1: decode, gather, multiply, stage in LDS.
+  bool paired = false;
+  if constexpr (BT == 8 && kPasses == 1) {
+    // Eight columns of neuron-major s: an edge's source row is 32 bytes.  The
+    // two lanes of a pair take the pair's eight edges together, each loading one
+    // 16-byte half of every edge's row, so one load instruction reads 32 rows
+    // whole and the L2 sees one request per row rather than up to two (the
+    // lanes trade column indices and weights with shuffles).  The products and
+    // their LDS places are those of the per-lane path below, so the sums are
+    // bitwise the same.  N=50k, M=1M, B=8: 14.8 to 13.7 us per tick.
+    if (A.s_vec4 && b0 + 8 <= A.B) {
+      paired = true;
+      const bool have = base + tid * 4 < e1;
+      int c_own[4], c_par[4];
+      float w_own[4], w_par[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        c_own[k] = have ? cq[0][k] : 0;
+        w_own[k] = have ? wq[0][k] : 0.0f;
+        c_par[k] = __shfl_xor(c_own[k], 1, 64);
+        w_par[k] = __shfl_xor(w_own[k], 1, 64);
+      }
+      const int h = tid & 1;                         // the half of the row this lane loads
+      const int pair0 = base + (tid & ~1) * 4;       // the pair's first edge
+      v4f g[8];
+      float w[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        // Edges 0-3 are the even lane's quad, 4-7 the odd lane's.
+        const int e = pair0 + i;
+        const int c = i < 4 ? (h ? c_par[i] : c_own[i]) : (h ? c_own[i - 4] : c_par[i - 4]);
+        w[i] = i < 4 ? (h ? w_par[i] : w_own[i]) : (h ? w_own[i - 4] : w_par[i - 4]);
+        g[i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        if (e >= e0 && e < e1)
+          g[i] = *reinterpret_cast<const v4f*>(A.s.data + static_cast<int64_t>(c) * A.s.sn +
+                                               (b0 + 4 * h));
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        v4f lo, hi;
+        lo.x = w[0] * g[0][t]; lo.y = w[1] * g[1][t]; lo.z = w[2] * g[2][t]; lo.w = w[3] * g[3][t];
+        hi.x = w[4] * g[4][t]; hi.y = w[5] * g[5][t]; hi.z = w[6] * g[6][t]; hi.w = w[7] * g[7][t];
+        float* const at = prod + (4 * h + t) * kStride + (pair0 - base);
+        *reinterpret_cast<v4f*>(at) = lo;
+        *reinterpret_cast<v4f*>(at + 4) = hi;
+      }
+    }
+  }
 #pragma unroll
   for (int p = 0; p < kPasses; ++p) {
+    if (paired) break;
     const int q = base + (p * kThreads + tid) * 4;
     if (q < e1) {
       float g[4][BT];
