@@ -21,7 +21,9 @@ headline graph's weights, one recorded tick plus its native backward on
 the headline graph next to autograd through the torch step, and headline
 ticks with a new weight version before each, and the reference's own benchmark
 protocol (five shapes, eager ticks, its published RTX 5070 figures beside each
-row, kernels per tick counted in a captured graph).  ``host`` names the CPU model,
+row, kernels per tick counted in a captured graph), and the reference's
+reduced-weight-storage protocol (two B=8 shapes, fp32/fp16/fp8/NVFP4, eager ticks and
+each mode's trajectory error against fp32, its published figures beside).  ``host`` names the CPU model,
 torch and HIP versions; ``cpu_baseline`` also gives the one-thread figure.
 
     python bench.py [--gpus 1] [--steps 1000] [--warmup 50]
@@ -33,7 +35,9 @@ import argparse
 import dataclasses
 import gc
 import json
+import math
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -761,7 +765,6 @@ def measure_protocol(device, iterations: int = 100, repeats: int = 7) -> dict:
     propagation="auto" (a fifth runtime in the same rotation), each native
     runtime's kernels per tick, counted in a captured graph of one tick, and its
     ms per tick when the same inputs run as graph replays of ``iterations`` ticks."""
-    import math
     import random
     from neurosim_gpu import DendriticMatrixRuntime, DendriticPELSRuntime
 
@@ -872,6 +875,142 @@ def measure_protocol(device, iterations: int = 100, repeats: int = 7) -> dict:
             "published_kernels_per_tick": PROTOCOL_PUBLISHED_KERNELS, "cases": cases}
 
 
+PRECISION_MODES = ("fp32", "fp16", "fp8", "nvfp4")
+PRECISION_CASES = (("small", 1024, 16_384, 8), ("large", 50_000, 1_000_000, 8))
+# results/precision_native.json (NVIDIA GeForce RTX 5070 Laptop GPU): per mode the
+# median GPU and wall ms per tick, the weight payload bytes and the state's peak
+# |error| against the fp32 runtime over the 72 probe ticks.
+PRECISION_PUBLISHED = {
+    "small": {"edges": 16_273,
+              "fp32": (0.02098, 0.02208, 65_092, 0.0), "fp16": (0.01871, 0.02554, 32_546, 1.648e-5),
+              "fp8": (0.02004, 0.02057, 16_277, 2.105e-3), "nvfp4": (0.02124, 0.02487, 9_159, 5.629e-3)},
+    "large": {"edges": 999_787,
+              "fp32": (0.44973, 0.45098, 3_999_148, 0.0), "fp16": (0.44543, 0.44796, 1_999_574, 1.745e-5),
+              "fp8": (0.44356, 0.44461, 999_791, 2.382e-3), "nvfp4": (0.49787, 0.49992, 562_385, 8.233e-3)},
+}
+
+
+def measure_precision_native(device, iterations: int = 60, repeats: int = 5, warmup: int = 12) -> dict:
+    """The reference's reduced-weight-storage benchmark on this GPU, its published figures beside.
+
+    benchmarks/precision_native.py: per workload random_topology(n, candidates,
+    seed=23, weight_scale=.15) drawn on the GPU, batch 8, initial state .25, the
+    model of benchmarks/precision_compartmental.py:33-41 (alpha .72, gain .8,
+    retentions exp(-1/4) and exp(-1/20), coupling .45, adaptation strength .15, all
+    per-neuron vectors), drive .16 + .04 (t mod 7)/6 and dendritic drive .025.  For
+    each of ``repeats`` orders of the four weight modes (shuffled, seed 19) a fresh
+    native matrix runtime takes one tick, ``warmup - 1`` more and then ``iterations``
+    timed eager ticks (HIP events and the host clock); medians are kept.  Then fresh
+    fp32 and mode runtimes step in lockstep for ``warmup + iterations`` ticks and the
+    peak and mean |mode - fp32| of every state field are recorded.  The graph differs
+    from the reference's (another device generator draws it), so the error figures
+    compare as statistics, not tick by tick."""
+    import random
+
+    def drive_at(tick: int) -> float:
+        return 0.16 + 0.04 * ((tick % 7) / 6.0)
+
+    options = {"fp32": {}, "fp16": {"weight_dtype": torch.float16},
+               "fp8": {"weight_format": "fp8"}, "nvfp4": {"weight_format": "nvfp4"}}
+    shuffle = random.Random(19)
+    orders = []
+    for _ in range(repeats):
+        order = list(PRECISION_MODES)
+        shuffle.shuffle(order)
+        orders.append(order)
+    workloads = {}
+    with torch.no_grad():
+        for name, n, candidates, batch in PRECISION_CASES:
+            log(f"precision_native: {name} N={n} candidates={candidates} B={batch}")
+            graph = random_topology(n, candidates, device=device, seed=23, weight_scale=0.15)
+            initial = torch.full((batch, n), 0.25, device=device)
+
+            def full(value):
+                return torch.full((n,), value, device=device)
+
+            model = DendriticDynamics(Dynamics(full(.72), full(.8)), full(math.exp(-1 / 4)),
+                                      full(math.exp(-1 / 20)), full(.45), full(.15))
+
+            def fresh(mode):
+                return NativeDendriticMatrixRuntime(graph, model, initial.clone(), **options[mode])
+
+            samples = {mode: {"gpu": [], "wall": [], "resident": []} for mode in PRECISION_MODES}
+            meta = {}
+            for order in orders:
+                for mode in order:
+                    torch.cuda.synchronize()
+                    before = torch.cuda.memory_allocated()
+                    runner = fresh(mode)
+                    runner.step(drive_at(0), dendritic_drive=.025)
+                    torch.cuda.synchronize()
+                    samples[mode]["resident"].append(torch.cuda.memory_allocated() - before)
+                    for t in range(1, warmup):
+                        runner.step(drive_at(t), dendritic_drive=.025)
+                    start = torch.cuda.Event(enable_timing=True)
+                    end = torch.cuda.Event(enable_timing=True)
+                    torch.cuda.synchronize()
+                    wall = time.perf_counter()
+                    start.record()
+                    for t in range(iterations):
+                        runner.step(drive_at(warmup + t), dendritic_drive=.025)
+                    end.record()
+                    end.synchronize()
+                    samples[mode]["wall"].append((time.perf_counter() - wall) * 1000 / iterations)
+                    samples[mode]["gpu"].append(start.elapsed_time(end) / iterations)
+                    meta[mode] = {"execution": runner.last_backend, "kernel": runner.kernel,
+                                  "weight_storage_bytes": runner.weight_storage_bytes}
+                    del runner
+            published = PRECISION_PUBLISHED[name]
+            rows = {}
+            for mode in PRECISION_MODES:
+                gpu = statistics.median(samples[mode]["gpu"])
+                wall = statistics.median(samples[mode]["wall"])
+                reference, candidate = fresh("fp32"), fresh(mode)
+                peaks = {f: [] for f in STATE_FIELDS}
+                means = {f: [] for f in STATE_FIELDS}
+                for t in range(warmup + iterations):
+                    for runner in (reference, candidate):
+                        runner.step(drive_at(t), dendritic_drive=.025)
+                    for f in STATE_FIELDS:
+                        error = (getattr(candidate, f) - getattr(reference, f)).abs()
+                        peaks[f].append(error.max())
+                        means[f].append(error.mean())
+                trajectory = {f: {"max_abs_error": float(torch.stack(peaks[f]).max()),
+                                  "mean_abs_error": float(torch.stack(means[f]).mean()),
+                                  "final_max_abs_error": float(peaks[f][-1])}
+                              for f in STATE_FIELDS}
+                del reference, candidate
+                pub_gpu, pub_wall, pub_bytes, pub_error = published[mode]
+                rows[mode] = {"median_gpu_ms_per_tick": round(gpu, 5),
+                              "median_wall_ms_per_tick": round(wall, 5), **meta[mode],
+                              "resident_extra_bytes_after_first_tick":
+                                  statistics.median(samples[mode]["resident"]),
+                              "trajectory_error_vs_fp32": trajectory,
+                              "published_rtx5070": {"median_gpu_ms_per_tick": pub_gpu,
+                                                    "median_wall_ms_per_tick": pub_wall,
+                                                    "weight_storage_bytes": pub_bytes,
+                                                    "state_max_abs_error": pub_error},
+                              "rtx5070_over_this_gpu_wall": round(pub_wall / wall, 2)}
+            for mode in PRECISION_MODES:
+                rows[mode]["speedup_wall_vs_fp32"] = round(
+                    rows["fp32"]["median_wall_ms_per_tick"] / rows[mode]["median_wall_ms_per_tick"], 3)
+            workloads[name] = {"n": n, "candidate_edges": candidates, "edges": graph.n_edges,
+                               "published_edges": published["edges"], "batch": batch,
+                               "modes": rows}
+            log(f"precision_native {name}: " + ", ".join(
+                f"{mode} {rows[mode]['median_wall_ms_per_tick']} ms" for mode in PRECISION_MODES))
+            del graph, model, initial
+            gc.collect()
+            torch.cuda.empty_cache()
+    return {"protocol": "benchmarks/precision_native.py: seed 23 (GPU generator), weight scale "
+                        ".15, B=8, initial .25, drive .16+.04*(t mod 7)/6, dendritic .025, "
+                        f"{warmup} warm-up ticks, {repeats} x {iterations} eager ticks per mode "
+                        "in shuffled orders (seed 19), medians; trajectory error over "
+                        f"{warmup + iterations} ticks against the fp32 runtime",
+            "published": "results/precision_native.json, NVIDIA GeForce RTX 5070 Laptop GPU",
+            "workloads": workloads}
+
+
 def main() -> None:
     cli = argparse.ArgumentParser(description=__doc__)
     cli.add_argument("--gpus", type=int, default=1)
@@ -886,7 +1025,7 @@ def main() -> None:
     cli.add_argument("--copy-calibration", action="store_true",
                      help="only run 256 MiB device copies (PMC byte-counter calibration)")
     cli.add_argument("--configs",
-                     default="encode,backward,weights,batched,pels,scaleout,protocol",
+                     default="encode,backward,weights,batched,pels,scaleout,protocol,precision",
                      help="other workloads to time after the headline one ('none' for none)")
     args = cli.parse_args()
     if args.gpus != 1:
@@ -987,6 +1126,8 @@ def main() -> None:
             extra[name] = measure_scaleout(device, not args.no_cpu_baseline)
         elif name == "protocol":
             extra[name] = measure_protocol(device)
+        elif name == "precision":
+            extra[name] = measure_precision_native(device)
         else:
             cli.error(f"unknown config {name}")
         log(f"{name}: {extra[name]}")

@@ -322,3 +322,21 @@ def test_row_plans_of_an_inference_mode_rowptr():
     before = extension.plan_tensors(rowptr, 1)
     rowptr.add_(0)
     assert extension.plan_tensors(rowptr, 1) is not before
+
+
+@pytest.mark.parametrize("edges,published", [
+    (16_273, {"fp32": 65_092, "fp16": 32_546, "fp8": 16_277, "nvfp4": 9_159}),
+    (999_787, {"fp32": 3_999_148, "fp16": 1_999_574, "fp8": 999_791, "nvfp4": 562_385})])
+def test_weight_storage_bytes_equal_the_published_payloads(edges, published):
+    """results/precision_native.json:362,417,472,527 (and the small workload's rows)
+    give each mode's logical payload for the reference's two graphs; the property
+    reads only the edge count and the mode, so it is checked without a GPU."""
+    from types import SimpleNamespace
+    from neurosim_gpu import NativeDendriticMatrixRuntime
+
+    modes = {"fp32": (torch.float32, None), "fp16": (torch.float16, None),
+             "fp8": (torch.float32, "fp8"), "nvfp4": (torch.float32, "nvfp4")}
+    for mode, (dtype, fmt) in modes.items():
+        runtime = SimpleNamespace(topology=SimpleNamespace(n_edges=edges),
+                                  weight_dtype=dtype, weight_format=fmt)
+        assert NativeDendriticMatrixRuntime.weight_storage_bytes.fget(runtime) == published[mode]
