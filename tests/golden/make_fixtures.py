@@ -12,10 +12,12 @@ compact fixtures next to this script:
   and the 4096-tick population-mean soma traces of both rows (row 0 keeps
   its inputs, row 1 has both drives withdrawn).
 * drift.npz + drift_summary.json <- results/precision_drift.json.gz: the
-  100,000-tick schedule of 429 sample ticks, and for seed 11 of each scenario
-  (native backend) the per-sample RMSE and max-abs curves of fp16/fp8/NVFP4
-  against FP32 for the three states, with the summary figures the reference
-  computed from them.
+  100,000-tick schedule of 429 sample ticks; for every scenario and seed
+  (11, 23, 47; native backend) the graph's edge count, the per-sample RMSE,
+  max-abs and bias curves of fp16/fp8/NVFP4 against FP32 for the three
+  states, the mean and standard deviation of the FP32 run's states, and the
+  max-abs difference between its native and torch FP32 runs; and
+  for seed 11 the summary figures the reference computed from the curves.
 
 Usage: python tests/golden/make_fixtures.py [/root/reference]
 """
@@ -63,19 +65,32 @@ def main(reference: Path) -> None:
     with gzip.open(reference / "results/precision_drift.json.gz", "rt") as handle:
         drift = json.load(handle)
     modes, fields = ("fp16", "fp8", "nvfp4"), ("state", "dendritic_state", "adaptation_state")
-    kept = [case for case in drift["cases"] if case["seed"] == 11 and case["backend"] == "native"]
+    kept = [case for case in drift["cases"] if case["backend"] == "native"]
     arrays = {"ticks": np.asarray([s["tick"] for s in kept[0]["samples"]], dtype=np.int64)}
     summary = {"steps": drift["protocol"]["steps"],
                "sample_interval": drift["protocol"]["sample_interval"], "cases": {}}
+    edges = {}
     for case in kept:
         assert [s["tick"] for s in case["samples"]] == arrays["ticks"].tolist()
-        for stat in ("rmse", "max_abs"):
-            arrays[f"{case['scenario']}_{stat}"] = np.asarray(
+        key = f"{case['scenario']}_s{case['seed']}"
+        edges[case["seed"]] = case["edges"]
+        for stat in ("rmse", "max_abs", "bias"):
+            arrays[f"{key}_{stat}"] = np.asarray(
                 [[[s["precisions"][m][f][stat] for s in case["samples"]] for f in fields]
                  for m in modes], dtype=np.float64)
-        summary["cases"][case["scenario"]] = {
-            m: {f: {k: v for k, v in case["summary"][m][f].items() if k != "final"}
-                for f in fields} for m in modes}
+        for stat in ("mean", "std"):
+            arrays[f"{key}_fp32_{stat}"] = np.asarray(
+                [[s["reference"][f][stat] for s in case["samples"]] for f in fields],
+                dtype=np.float64)
+        # The reference's control: its native FP32 run against its torch FP32 run.
+        arrays[f"{key}_control_max_abs"] = np.asarray(
+            [[s["fp32_other_backend"][f]["max_abs"] for s in case["samples"]] for f in fields],
+            dtype=np.float64)
+        if case["seed"] == 11:
+            summary["cases"][case["scenario"]] = {
+                m: {f: {k: v for k, v in case["summary"][m][f].items() if k != "final"}
+                    for f in fields} for m in modes}
+    arrays["edges"] = np.asarray(sorted(edges.items()), dtype=np.int64)
     np.savez_compressed(HERE / "drift.npz", **arrays)
     (HERE / "drift_summary.json").write_text(json.dumps(summary, indent=1) + "\n")
 

@@ -32,7 +32,7 @@ REF_MODES = ("fp16", "fp8", "nvfp4")
 
 
 def reference_samples(scenario: str) -> list[dict]:
-    rmse, max_abs = ARRAYS[f"{scenario}_rmse"], ARRAYS[f"{scenario}_max_abs"]
+    rmse, max_abs = ARRAYS[f"{scenario}_s11_rmse"], ARRAYS[f"{scenario}_s11_max_abs"]
     return [{mode: {field: {"rmse": float(rmse[m, f, i]), "max_abs": float(max_abs[m, f, i])}
                     for f, field in enumerate(drift.FIELDS)}
              for m, mode in enumerate(REF_MODES)}

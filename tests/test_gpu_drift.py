@@ -22,9 +22,16 @@ computed once on the CPU in float32, so both sides read the same values.
   max-abs and RMS difference from the oracle cross 1e-4 and 1e-2, and asserts
   finite states inside the model's bounds at every sample of 100,000 ticks,
   plus agreement within 1e-5 over the first 50 ticks.
+* Against the reference's own published run: drawn on this GPU, the drift
+  graphs are the reference's (same edge counts), so every sample's figures
+  (the fp32 run's mean and standard deviation, each mode's RMS, max-abs and
+  mean difference from fp32) must equal those in results/precision_drift.json
+  within twice the reference's own native-vs-torch float32 gap plus 1e-6.
 """
 
 from __future__ import annotations
+
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -173,3 +180,80 @@ def test_recurrent_stress_drift(gpu, seed):
                       f"rms {first_rms[m][1e-4]} / {first_rms[m][1e-2]}" for m in MODES)
           + f"; worst over the first {agree_ticks} ticks {early_worst:.2e}", flush=True)
     assert early_worst <= BAR, (seed, early_worst)
+
+
+PUBLISHED = np.load(Path(__file__).resolve().parent / "golden" / "drift.npz")
+ROUNDING = 1e-6
+CHAOS_LIMIT = 1e-5
+
+
+def sample_figures(case: DriftCase) -> np.ndarray:
+    """At the current tick, as the reference's snapshot computes them
+    (benchmarks/precision_drift.py:160-185): per state field the fp32 run's mean and
+    population standard deviation, and per lowered mode and field the RMS, max-abs
+    and mean of (mode - fp32).  One host transfer; shape [2 + 9, 3]: fp32 mean and
+    std, then (rmse, max_abs, bias) per mode."""
+    values = torch.stack([torch.stack(case.states(mode)) for mode in MODES])  # [4, 3, B, N]
+    dims = (-2, -1)
+    base = values[0]
+    errors = values[1:] - base
+    rows = [base.mean(dim=dims), base.std(dim=dims, unbiased=False)]
+    for m in range(len(MODES) - 1):
+        rows += [errors[m].square().mean(dim=dims).sqrt(), errors[m].abs().amax(dim=dims),
+                 errors[m].mean(dim=dims)]
+    return torch.stack(rows).double().cpu().numpy()
+
+
+@pytest.mark.parametrize("scenario,seed", [
+    ("stable_drive", 11), ("slow_adaptation", 11), ("stable_drive", 23),
+    ("slow_adaptation", 23), ("stable_drive", 47), ("slow_adaptation", 47),
+    ("recurrent_stress", 11), ("recurrent_stress", 23), ("recurrent_stress", 47)])
+def test_drift_equals_the_published_native_run(gpu, scenario, seed):
+    """The reference drew its drift graphs with random_topology(1024, 16384, seed)
+    on its GPU (benchmarks/precision_drift.py:231-236); this GPU's generator draws
+    the same graphs (the edge counts equal the published ones, 16,243 / 16,273 /
+    16,267, and so do the figures below).  The native run here and the reference's
+    native run (results/precision_drift.json, backend "native") then see the same
+    graph, model, drives and schedule and differ only in float32 rounding.
+
+    The reference also published how far its native float32 run lies from its torch
+    float32 run at each sample ("fp32_other_backend"): 5e-7 after one tick, up to
+    1.8e-6 (stable_drive) and 3.2e-6 (slow_adaptation), since its kernel is built
+    with fast math, while the native run here stays within 1.6e-7 of the torch
+    order (the oracle tests above).  So at every sample tick the fp32 run's mean and
+    standard deviation, and each lowered mode's RMS, max-abs and mean difference
+    from fp32, must equal the published figures within twice that control's max-abs
+    plus 1e-6: over all 100,000 ticks of the two contractive scenarios, and in the
+    chaotic recurrent_stress for as long as the control stays below 1e-5 (its first
+    20-50 ticks).  After that a rounding difference grows there, in each weight
+    mode at its own rate, until the runs decorrelate."""
+    print(f"case drift vs published {scenario} seed {seed}: graph drawn on the GPU",
+          flush=True)
+    case = DriftCase(scenario, seed, neurons=N, edges=EDGES, batch=BATCH, chunk=CHUNK,
+                     device=gpu, draw_device=gpu)
+    assert case.edges() == dict(PUBLISHED["edges"].tolist())[seed]
+    key = f"{scenario}_s{seed}"
+    schedule = PUBLISHED["ticks"].tolist()
+    assert schedule == sample_ticks(100_000, INTERVAL)
+    control = PUBLISHED[f"{key}_control_max_abs"].max(axis=0)
+    expected = np.concatenate([PUBLISHED[f"{key}_fp32_mean"][None], PUBLISHED[f"{key}_fp32_std"][None],
+                               np.stack([PUBLISHED[f"{key}_{stat}"] for stat in
+                                         ("rmse", "max_abs", "bias")], axis=1).reshape(9, 3, -1)])
+    worst, worst_ratio, compared = 0.0, 0.0, 0
+    for index, target in enumerate(schedule):
+        if control[index] > CHAOS_LIMIT:
+            assert scenario == "recurrent_stress", (scenario, seed, target, control[index])
+            break
+        while case.tick < target:
+            case.advance(min(CHUNK, target - case.tick))
+        difference = float(np.abs(sample_figures(case) - expected[:, :, index]).max())
+        bar = 2 * control[index] + ROUNDING
+        assert difference <= bar, (scenario, seed, target, difference, bar)
+        worst = max(worst, difference)
+        worst_ratio = max(worst_ratio, difference / bar)
+        compared = target
+        if case.tick and case.tick % 25_000 == 0:
+            print(f"  tick {case.tick}: worst difference from the published figures "
+                  f"{worst:.2e}", flush=True)
+    print(f"drift vs published {scenario} seed {seed} ({case.edges()} edges): worst difference "
+          f"{worst:.2e} over ticks 0-{compared}, at most {worst_ratio:.2f} of the bar", flush=True)
