@@ -398,6 +398,8 @@ def measure_backward(topology, model, repeats: int = 10) -> dict:
             runtime.state.sum().backward()
 
         try:
+            # The first two passes of a weight version build its slot-order and
+            # transposed copies.
             for _ in range(2):
                 once()
         except RuntimeError as error:
@@ -417,6 +419,9 @@ def measure_backward(topology, model, repeats: int = 10) -> dict:
         # time the GPU work.
         gc.collect()
         gc.freeze()
+        # The collection leaves the GPU idle for tens of milliseconds, and the
+        # first pass after such a pause runs 1.5-2x slower: one more untimed pass.
+        once()
         passes = []
         for _ in range(repeats):
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -432,6 +437,7 @@ def measure_backward(topology, model, repeats: int = 10) -> dict:
         else:
             out[f"{name}_ms_per_tick"] = round(ms / ticks, 4)
         out[f"{name}_slowest_pass_ms"] = round(max(passes), 4)
+        out[f"{name}_passes_ms"] = [round(p, 3) for p in passes]
         weight.grad = None
         for p in params:
             p.grad = None
