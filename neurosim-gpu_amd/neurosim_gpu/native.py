@@ -30,6 +30,7 @@ import threading
 import weakref
 from collections import OrderedDict
 from functools import lru_cache
+from operator import is_
 from pathlib import Path
 
 import numpy as np
@@ -371,10 +372,26 @@ def _params(values, state: torch.Tensor):
     return vectors
 
 
+def _new_outputs(count: int, batch: int, n: int, device) -> tuple:
+    """``count`` fresh neuron-major [batch, n] planes from one allocation, and
+    that allocation's address.  At batch 1 a neuron-major plane is a row, so the
+    planes are the rows of a [count, 1, n] block (no transposed view needed)."""
+    if batch == 1:
+        storage = torch.empty((count, 1, n), dtype=torch.float32, device=device)
+        return storage.unbind(0), storage.data_ptr()
+    storage = torch.empty((count, n, batch), dtype=torch.float32, device=device)
+    return storage.transpose(1, 2).unbind(0), storage.data_ptr()
+
+
+def _neuron_major(plane: torch.Tensor) -> bool:
+    """Element (b, n) of a [B,N] plane at offset n * B + b (at B=1 any row)."""
+    batch = plane.size(0)
+    return plane.stride(1) == batch and (batch == 1 or plane.stride(0) == 1)
+
+
 def new_planes(count: int, batch: int, n: int, like: torch.Tensor) -> list[torch.Tensor]:
     """``count`` fresh [B,N] planes stored neuron-major in one allocation."""
-    storage = torch.empty((count, n, batch), dtype=torch.float32, device=like.device)
-    return [storage[i].T for i in range(count)]
+    return list(_new_outputs(count, batch, n, like.device)[0])
 
 
 def panel_geometry(batch: int) -> tuple[int, int]:
@@ -927,7 +944,7 @@ class NativeExtension:
             args.transposed_panels = ctypes.addressof(transposed_panels)
         if current is not None:
             _check_float(current, state, "current")
-            if current.shape != state.shape or current.stride() != (1, batch):
+            if current.shape != state.shape or not _neuron_major(current):
                 raise RuntimeError("current must be a neuron-major [B,N] plane")
             args.current = current.data_ptr()
         args.grad_state = _drive(grad_state, 0.0, state)
@@ -1122,6 +1139,9 @@ if [getattr(_StepGradArgs, f).offset - _GRAD_POINTERS
     raise RuntimeError("_StepGradArgs: the output pointers must be consecutive")
 
 
+_data_ptr = torch.Tensor.data_ptr
+
+
 def _plane_words(value: torch.Tensor, state: torch.Tensor, what: str) -> tuple:
     """(data, stride_b, stride_n) of a validated [B,N] float32 plane."""
     _check_float(value, state, what)
@@ -1170,29 +1190,24 @@ class PreparedTick:
         self.bands, self._bands_ref = bands, (ctypes.byref(bands) if bands is not None else None)
         self.batch, self.n, self.shape, self.device = batch, n, state.shape, state.device
         self.params = tuple(params)
-        self._fixed = (rowptr, col, weight, block_scales, global_scale, panels, bands)
-        self._pointers = self._addresses(self.params, rowptr, col, weight)
+        self._fixed = (rowptr, col, weight, block_scales, global_scale, panels, bands,
+                       *self.params)
+        self._addressed = (*self.params, rowptr, col, weight)
+        self._pointers = tuple(map(_data_ptr, self._addressed))
         self._bounds = bounds
         self._last = None     # (s', d', a', their nine words)
 
-    @staticmethod
-    def _addresses(params, rowptr, col, weight) -> tuple:
-        return tuple(p.data_ptr() for p in params) + (rowptr.data_ptr(), col.data_ptr(),
-                                                      weight.data_ptr())
-
     def matches(self, state, params, rowptr, col, weight, block_scales=None, global_scale=None,
                 panels=None, bands=None) -> bool:
-        fixed = self._fixed
-        if not (rowptr is fixed[0] and col is fixed[1] and weight is fixed[2]
-                and block_scales is fixed[3] and global_scale is fixed[4] and panels is fixed[5]
-                and bands is fixed[6] and len(params) == 6):
-            return False
-        if any(a is not b for a, b in zip(params, self.params)):
+        """The same tensor objects (and layouts) as prepared, still at the same
+        addresses (an assignment to ``.data`` keeps the object, not the address)."""
+        given = (rowptr, col, weight, block_scales, global_scale, panels, bands, *params)
+        if len(given) != 13 or not all(map(is_, given, self._fixed)):
             return False
         last = self._last
         if (last is None or state is not last[0]) and state.shape != self.shape:
             return False
-        return self._addresses(params, rowptr, col, weight) == self._pointers
+        return tuple(map(_data_ptr, self._addressed)) == self._pointers
 
     def __call__(self, state, dendrite, adaptation, drive, drive_scalar, dendritic_drive,
                  dendritic_scalar, current: bool = False) -> tuple:
@@ -1224,9 +1239,8 @@ class PreparedTick:
                            *_drive_words(drive, drive_scalar, state),
                            *_drive_words(dendritic_drive, dendritic_scalar, state))
         batch, n = self.batch, self.n
-        storage = torch.empty((4 if current else 3, n, batch), dtype=torch.float32,
-                              device=self.device)
-        base, size = storage.data_ptr(), 4 * n * batch
+        outs, base = _new_outputs(4 if current else 3, batch, n, self.device)
+        size = 4 * n * batch
         out = (base, 1, batch, base + size, 1, batch, base + 2 * size, 1, batch)
         _OUTS4.pack_into(args, _STEP_OUT, *out,
                          *((base + 3 * size, 1, batch) if current else (0, 0, 0)))
@@ -1236,7 +1250,6 @@ class PreparedTick:
         else:
             code = self.lib.ns_dendritic_step(self._ref, stream)
         _raise_on(code, self.lib)
-        outs = storage.transpose(1, 2).unbind(0)
         self._last = (outs[0], outs[1], outs[2],
                       (out[0], 1, batch, 0.0, out[3], 1, batch, 0.0, out[6], 1, batch, 0.0))
         return outs
@@ -1320,7 +1333,7 @@ class PreparedBackward:
         current_ptr = 0
         if current is not None:
             _check_float(current, state, "current")
-            if current.shape != state.shape or current.stride() != (1, batch):
+            if current.shape != state.shape or not _neuron_major(current):
                 raise RuntimeError("current must be a neuron-major [B,N] plane")
             current_ptr = current.data_ptr()
         count = 3 + int(need_drive) + int(need_dendritic)
@@ -1407,8 +1420,9 @@ class PreparedEvent:
         self.args, self._ref = args, ctypes.byref(args)
         self.batch, self.n, self.shape, self.device = batch, n, state.shape, state.device
         self.params = tuple(params)
-        self._fixed = (theta, rowptr, dst, weight_index, weight, pending, activity)
-        self._pointers = tuple(t.data_ptr() for t in self.params + self._fixed[:5])
+        self._fixed = (theta, rowptr, dst, weight_index, weight, pending, activity, *self.params)
+        self._addressed = (*self.params, theta, rowptr, dst, weight_index, weight)
+        self._pointers = tuple(map(_data_ptr, self._addressed))
         self._delta = delta
         self._pending = ((pending[0].data_ptr(), pending[1].data_ptr())
                          if pending is not None else None)
@@ -1419,17 +1433,13 @@ class PreparedEvent:
 
     def matches(self, state, params, theta, rowptr, dst, weight_index, weight, pending=None,
                 activity=None) -> bool:
-        fixed = self._fixed
-        if not (theta is fixed[0] and rowptr is fixed[1] and dst is fixed[2]
-                and weight_index is fixed[3] and weight is fixed[4] and pending is fixed[5]
-                and activity is fixed[6] and len(params) == 6):
-            return False
-        if any(a is not b for a, b in zip(params, self.params)):
+        given = (theta, rowptr, dst, weight_index, weight, pending, activity, *params)
+        if len(given) != 13 or not all(map(is_, given, self._fixed)):
             return False
         last = self._last
         if (last is None or state is not last[0]) and state.shape != self.shape:
             return False
-        return tuple(t.data_ptr() for t in self.params + fixed[:5]) == self._pointers
+        return tuple(map(_data_ptr, self._addressed)) == self._pointers
 
     def __call__(self, state, dendrite, adaptation, emitted, current, drive, drive_scalar,
                  dendritic_drive, dendritic_scalar, *, parity=None, advance_only=False,
@@ -1490,13 +1500,12 @@ class PreparedEvent:
                               self._out_weight[1], EVENT_ADVANCE_ONLY if advance_only else 0,
                               0, self._activity if sample else 0)
         batch, n = self.batch, self.n
-        storage = torch.empty((4, n, batch), dtype=torch.float32, device=self.device)
-        base, size = storage.data_ptr(), 4 * n * batch
+        outs, base = _new_outputs(4, batch, n, self.device)
+        size = 4 * n * batch
         out = (base, 1, batch, base + size, 1, batch, base + 2 * size, 1, batch,
                base + 3 * size, 1, batch)
         _OUTS4.pack_into(args, _EVENT_OUT, *out)
         _raise_on(self.lib.ns_dendritic_event(self._ref, current_stream(self.device)), self.lib)
-        outs = storage.transpose(1, 2).unbind(0)
         self._last = (outs[0], outs[1], outs[2], outs[3],
                       (out[0], 1, batch, 0.0, out[3], 1, batch, 0.0, out[6], 1, batch, 0.0),
                       (out[9], 1, batch, 0.0))
