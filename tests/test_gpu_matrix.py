@@ -370,3 +370,34 @@ def test_cfg5_scaleout_fp8_against_an_independent_graph(gpu, cfg5):
     print(f"cfg5 fp8 max abs error: eager ticks 1-10 {worst:.3e}, "
           f"graph of 100 ticks {worst_rollout:.3e}", flush=True)
     assert worst <= 1e-5 and worst_rollout <= 1e-5
+
+
+@pytest.mark.parametrize("fmt", ["fp32", "nvfp4"])
+@pytest.mark.parametrize("batch", [4, 5, 6, 7, 8, 9, 12, 17, 20, 33])
+def test_row_blocks_at_every_column_tile(gpu, batch, fmt):
+    """The row-block kernel's column tiles (4, 8 or 16 columns, the last one of a
+    batch partial) against the oracle, at B=8 with the paired 32-byte row gathers.
+    A twin runtime whose states are copied row-major before every tick gathers
+    element by element instead (no 16-byte row loads, no pairs); the products and
+    their order are the same, so its states must be bitwise those of the first."""
+    print(f"case row blocks B={batch} fmt={fmt}", flush=True)
+    n, m = 600, 9000
+    case = make_case(n, m, 5, gpu)
+    options = {} if fmt == "fp32" else {"weight_format": fmt}
+    neuron_major, row_major = (
+        NativeDendriticMatrixRuntime(case.topology, case.model, torch.zeros(batch, n, device=gpu),
+                                     kernel="rows", **options) for _ in range(2))
+    weight = (case.graph.in_weight if fmt == "fp32"
+              else op.quantize_dequantize(case.graph.in_weight, fmt))
+    oracle = ort.MatrixOracle(case.graph, case.params, torch.zeros(batch, n), in_weight=weight)
+    drive = column_drive(batch)
+    for t in range(20):
+        neuron_major.step(drive.to(gpu), dendritic_drive=0.1)
+        for f in FIELDS:
+            setattr(row_major, f, getattr(row_major, f).contiguous())
+        row_major.step(drive.to(gpu), dendritic_drive=0.1)
+        oracle.step(drive, 0.1)
+        for f in FIELDS:
+            assert torch.equal(getattr(neuron_major, f), getattr(row_major, f)), (batch, fmt, t, f)
+    assert neuron_major.state.stride(0) == 1 or batch == 1
+    assert errors(neuron_major, oracle) <= 1e-5
