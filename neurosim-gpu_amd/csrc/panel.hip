@@ -472,7 +472,7 @@ __global__ __launch_bounds__(kPanelThreads) void panel_tick_kernel(PanelArgs A) 
   __builtin_assume(lane32 < 64u);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const_i32_ptr tile = (const_i32_ptr)(A.tiles + 4 * static_cast<int64_t>(blockIdx.x));
-  const int panel = tile[0], row0 = tile[1];
+  const int panel = tile[0];
   const int64_t base = static_cast<int64_t>(panel) * A.width;
   const int len = static_cast<int>(min<int64_t>(A.width, A.N - base));
   const float gscale =
