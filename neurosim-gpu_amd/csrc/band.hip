@@ -257,7 +257,7 @@ __global__ __launch_bounds__(kBandWaves * 64) void band_tick_kernel(BandArgs A) 
 #pragma unroll
   for (int j = 0; j < 4 * G; ++j) acc[j] = 0.0f;
 
-  BandBlock cur{0, 0, 0, 0, 0};
+  BandBlock cur{};
   BandSlot here[D];
   uint32_t row = kBandNoRow | (kBandNoRow << kBandRowBits);
   if (b_begin < b_end) {
