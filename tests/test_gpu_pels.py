@@ -226,17 +226,21 @@ def test_one_launch_graph_replay_matches_eager(gpu):
         assert max_err(rolled.persistent_current, eager.persistent_current) <= 1e-5, replay
 
 
+@pytest.mark.parametrize("batch", [3, 8, 64])
 @pytest.mark.parametrize("one_launch", [True, False])
 @pytest.mark.parametrize("theta", [0.0, 0.01])
-def test_hub_sources_scatter_many_rounds(gpu, one_launch, theta):
-    """Sources with thousands of out-edges next to ordinary ones, B=3: one
+def test_hub_sources_scatter_many_rounds(gpu, one_launch, theta, batch):
+    """Sources with thousands of out-edges next to ordinary ones: one
     wavefront's emitters then span dozens of 64-edge rounds, and an edge's
-    emitter is found among neighbours of very different degree."""
+    emitter is found among neighbours of very different degree.  At B=8 and 64
+    the scatter takes each source's emitting columns together (B=3 walks pair by
+    pair); the columns get different drives and initial states, so a source
+    emits in some columns and not in others."""
     from oracle import topology as otop
     from neurosim_gpu import SparseTopology, topology_to
     from cases import model_to, standard_model
 
-    print(f"case pels hubs theta={theta} one_launch={one_launch}", flush=True)
+    print(f"case pels hubs theta={theta} one_launch={one_launch} B={batch}", flush=True)
     n = 3000
     rng = np.random.default_rng(21)
     hubs = [(5, 2900), (6, 1500), (64, 2999), (2999, 2000)]
@@ -251,14 +255,15 @@ def test_hub_sources_scatter_many_rounds(gpu, one_launch, theta):
     topology = topology_to(SparseTopology.from_edges(n, torch.from_numpy(src), torch.from_numpy(dst),
                                                      torch.from_numpy(weight)), gpu)
     model, params = standard_model(n)
-    state = torch.full((3, n), 0.1)
+    columns = torch.linspace(0.0, 1.0, batch)[:, None]
+    state = 0.1 + 0.05 * columns.expand(batch, n).contiguous()
     native = NativeDendriticPELSRuntime(topology, model_to(model, gpu), state.to(gpu), theta=theta,
                                         one_launch=one_launch)
     oracle = ort.PelsOracle(graph, params, state, theta=theta)
     matrix = ort.csr_matrix(graph)
     for tick in range(40):
-        drive = 0.3 if tick < 25 else 0.05
-        native.step(drive, dendritic_drive=0.1)
+        drive = (0.3 if tick < 25 else 0.05) * (0.5 + columns)
+        native.step(drive.to(gpu), dendritic_drive=0.1)
         oracle.step(drive, 0.1)
     exact = ort.propagate(matrix, native.emitted_state.cpu())
     bar = 1e-5 if theta == 0 else 1e-3
