@@ -226,16 +226,16 @@ def test_one_launch_graph_replay_matches_eager(gpu):
         assert max_err(rolled.persistent_current, eager.persistent_current) <= 1e-5, replay
 
 
-@pytest.mark.parametrize("batch", [3, 8, 64])
+@pytest.mark.parametrize("batch", [2, 3, 4, 8, 64])
 @pytest.mark.parametrize("one_launch", [True, False])
 @pytest.mark.parametrize("theta", [0.0, 0.01])
 def test_hub_sources_scatter_many_rounds(gpu, one_launch, theta, batch):
     """Sources with thousands of out-edges next to ordinary ones: one
     wavefront's emitters then span dozens of 64-edge rounds, and an edge's
-    emitter is found among neighbours of very different degree.  At B=8 and 64
-    the scatter takes each source's emitting columns together (B=3 walks pair by
-    pair); the columns get different drives and initial states, so a source
-    emits in some columns and not in others."""
+    emitter is found among neighbours of very different degree.  At B = 2, 4, 8
+    and 64 the scatter takes each source's emitting columns together (B=3 walks
+    pair by pair); the columns get different drives and initial states, so a
+    source emits in some columns and not in others."""
     from oracle import topology as otop
     from neurosim_gpu import SparseTopology, topology_to
     from cases import model_to, standard_model
