@@ -159,12 +159,13 @@ def test_cfg4_event_path_warmup_then_withdrawn(gpu, theta, propagation, kernel):
     assert mismatches <= 1e-3 * max(checked, 1)
 
 
-@pytest.mark.parametrize("batch", [1, 3])
+@pytest.mark.parametrize("batch", [1, 3, 8])
 def test_one_launch_pending_reads_and_assignments(gpu, batch):
     """Reads of the persistent current fold the outstanding pending buffer; an
     assignment replaces the current and discards it.  Either way the run goes on
     matching the oracle and the two-launch tick (which gathers its weights
-    through out_weight_index instead of streaming the source-major copy)."""
+    through out_weight_index instead of streaming the source-major copy, and
+    here scatters into an assigned row-major current as well)."""
     case = make_case(2000, 40_000, 7, gpu)
     matrix = ort.csr_matrix(case.graph)
     state = torch.full((batch, 2000), 0.1)
@@ -184,6 +185,8 @@ def test_one_launch_pending_reads_and_assignments(gpu, batch):
         if tick % 11 == 5:
             # the exact current, assigned while a scatter is outstanding
             native.persistent_current = exact.to(gpu)
+            # a row-major current for the two-launch tick to scatter into
+            two.persistent_current = ort.propagate(matrix, two.emitted_state.cpu()).to(gpu)
         if tick % 11 == 6:
             assert max_err(native.persistent_current, exact) <= 1e-5
     assert state_error(native, oracle) <= 1e-3
