@@ -85,7 +85,7 @@ typedef struct ns_csr {
 typedef struct ns_row_plan {
   const int32_t* bounds;       /* device int32[2*(n_blocks+1)] */
   int64_t n_blocks;
-  int32_t block_edges;         /* edge capacity the plan was built for */
+  int32_t block_edges;         /* edges per block the plan was built for (<= ns_block_edges) */
   int32_t reserved;
 } ns_row_plan;
 
@@ -406,8 +406,9 @@ int ns_abi_version(void);
 const char* ns_last_error(void);
 
 /* Edge capacity of one row block used by the tick kernels for batch width
- * `batch` (a plan passed to ns_dendritic_step/ns_csr_spmm must have been built
- * with exactly this capacity). */
+ * `batch`: a plan passed to ns_dendritic_step/ns_csr_spmm must have been built
+ * with at most this many edges per block (a multiple of 4, at least 8).
+ * Smaller blocks give small graphs more workgroups. */
 int32_t ns_block_edges(int64_t batch);
 
 /* Host-side planner: splits rows [0,N) of a host copy of `rowptr` into blocks

@@ -466,9 +466,9 @@ int check_matrix(const ns_csr& m, int64_t n, const ns_row_plan& plan, int64_t ba
   if (int rc = check_csr(m, n)) return rc;
   if (!plan.bounds || plan.n_blocks < 1) return fail("a row plan is required");
   if (plan.n_blocks > 0x7FFFFFFF) return fail("row plan has too many blocks");
-  if (plan.block_edges != capacity_for(batch))
-    return fail("row plan was built for block capacity %d, batch %lld needs %d",
-                plan.block_edges, (long long)batch, capacity_for(batch));
+  if (plan.block_edges < 8 || plan.block_edges % 4 || plan.block_edges > capacity_for(batch))
+    return fail("row plan was built for %d edges per block, batch %lld takes a multiple of 4 "
+                "from 8 to %d", plan.block_edges, (long long)batch, capacity_for(batch));
   return NS_OK;
 }
 

@@ -301,23 +301,43 @@ def build_topology(n_neurons: int, src: torch.Tensor, dst: torch.Tensor,
     return out
 
 
+def row_block_edges(batch: int, n_edges: int, units: int) -> int:
+    """Edges per row block: the kernels' capacity for ``batch``, halved while the
+    graph would give fewer than two blocks per compute unit, down to 1024 edges at
+    batch 1 or 2 (one full pass of a workgroup's lanes) and 256 from batch 4.
+    Graph-replayed ticks measured with each size (rows kernel, µs): N=4096,
+    M=65k: B=1 5.00 at 2048 edges, 4.37 at 1024; B=8 8.85 at 1024, 5.89 at 256;
+    N=1024, M=16k, B=16: 16.6 at 1024, 8.4 at 256; N=20k, M=400k, B=8: 9.0 at
+    1024, 8.3 at 512; N=50k, M=1M: B=1 7.97 at 2048, 7.88 at 1024, B=8 13.5 at
+    1024, 15.2 at 512; N=166k, M=2M, B=1: 13.4 at 2048, 13.7 at 1024."""
+    edges = int(load_library().ns_block_edges(int(batch)))
+    floor = 1024 if batch <= 2 else 256
+    while edges > floor and n_edges < 2 * units * edges:
+        edges //= 2
+    return edges
+
+
 def plan_row_blocks(rowptr: torch.Tensor, batch: int, device: torch.device) -> tuple[torch.Tensor, int, int]:
     """Row blocks for the tick kernels, built on the host and placed on ``device``.
 
-    Returns (bounds int32 device tensor [2*(blocks+1)], blocks, block capacity).
+    Returns (bounds int32 device tensor [2*(blocks+1)], blocks, edges per block:
+    ``row_block_edges`` for the graph, at most ``ns_block_edges(batch)``).
     Reads rowptr once on the host (a synchronisation), so call it at set-up.
     """
     lib = load_library()
-    capacity = int(lib.ns_block_edges(int(batch)))
     host = np.ascontiguousarray(rowptr.detach().to("cpu", torch.int32).numpy())
     n = host.size - 1
+    device = torch.device(device)
+    units = (torch.cuda.get_device_properties(device).multi_processor_count
+             if device.type == "cuda" else 256)
+    block_edges = row_block_edges(batch, int(host[-1]) if n >= 0 else 0, units)
     count = _c_i64(0)
-    _raise_on(lib.ns_plan_row_blocks(host.ctypes.data, n, capacity, None, 0,
+    _raise_on(lib.ns_plan_row_blocks(host.ctypes.data, n, block_edges, None, 0,
                                      ctypes.byref(count)), lib)
     bounds = np.empty(2 * (count.value + 1), dtype=np.int32)
-    _raise_on(lib.ns_plan_row_blocks(host.ctypes.data, n, capacity, bounds.ctypes.data,
+    _raise_on(lib.ns_plan_row_blocks(host.ctypes.data, n, block_edges, bounds.ctypes.data,
                                      bounds.size, ctypes.byref(count)), lib)
-    return torch.from_numpy(bounds).to(device), int(count.value), capacity
+    return torch.from_numpy(bounds).to(device), int(count.value), block_edges
 
 
 def _check_float(value: torch.Tensor, state: torch.Tensor, what: str) -> None:
@@ -695,7 +715,8 @@ class NativeExtension:
 
     # -- row plans ---------------------------------------------------------
     def plan_tensors(self, rowptr: torch.Tensor, batch: int) -> tuple[torch.Tensor, int, int]:
-        """Cached (bounds, blocks, capacity) of ``rowptr`` for batch width ``batch``."""
+        """Cached (bounds, blocks, edges per block) of ``rowptr`` for batch width
+        ``batch`` (cached per kernel capacity, which the batch width sets)."""
         capacity = int(self.lib.ns_block_edges(int(batch)))
         key = id(rowptr)
         with self._lock:

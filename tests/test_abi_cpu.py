@@ -128,9 +128,10 @@ def test_step_validation_messages(lib):
     args, keep = fake_step_args()
     args.n_neurons = 0
     assert "N > 0" in call(lib, args)[1]
-    args, keep = fake_step_args()
-    args.plan.block_edges = 1024
-    assert "capacity" in call(lib, args)[1]
+    for edges in (4096, 1022, 4):   # above the kernels' capacity, unaligned, too small
+        args, keep = fake_step_args()
+        args.plan.block_edges = edges
+        assert "edges per block" in call(lib, args)[1]
     args, keep = fake_step_args()
     args.out_dendrite = native._OutPlane(args.state.data, 8, 1)
     assert "overlap" in call(lib, args)[1]
@@ -578,3 +579,22 @@ def test_packed_argument_words_land_in_their_fields():
     assert grad.d_weight == 9000 and list(grad.d_params) == list(range(9001, 9007))
     assert (grad.workspace, grad.current, grad.out_weight, grad.transposed_panels) == \
         (9007, 9008, 9009, 9010)
+
+
+def test_row_block_size_follows_the_graph():
+    """Small graphs get smaller row blocks (at least two per compute unit where
+    the floor allows); large ones keep the kernels' capacity."""
+    cap = {b: native.load_library().ns_block_edges(b) for b in (1, 2, 4, 8, 16)}
+    assert native.row_block_edges(1, 65_401, 256) == 1024          # floor at batch 1-2
+    assert native.row_block_edges(2, 65_401, 256) == 1024
+    assert native.row_block_edges(1, 999_828, 256) == 1024
+    assert native.row_block_edges(1, 1_999_924, 256) == cap[1]      # 2048
+    assert native.row_block_edges(8, 65_401, 256) == 256            # floor from batch 4
+    assert native.row_block_edges(16, 16_273, 256) == 256
+    assert native.row_block_edges(8, 399_806, 256) == 512
+    assert native.row_block_edges(8, 999_828, 256) == cap[8]        # 1024
+    assert native.row_block_edges(16, 99_994_973, 256) == cap[16]
+    for b in cap:
+        for m in (0, 1, 10**3, 10**5, 10**7):
+            edges = native.row_block_edges(b, m, 256)
+            assert 8 <= edges <= cap[b] and edges % 4 == 0
