@@ -736,8 +736,8 @@ class NativeExtension:
         return plan
 
     def plan_for(self, rowptr: torch.Tensor, batch: int) -> _RowPlan:
-        bounds, blocks, capacity = self.plan_tensors(rowptr, batch)
-        return _RowPlan(bounds.data_ptr(), blocks, capacity, 0)
+        bounds, blocks, block_edges = self.plan_tensors(rowptr, batch)
+        return _RowPlan(bounds.data_ptr(), blocks, block_edges, 0)
 
     # -- weights -----------------------------------------------------------
     @staticmethod
@@ -1070,8 +1070,8 @@ class TickLauncher:
         elif panels is not None:
             args.panels = ctypes.addressof(panels)
         else:
-            bounds, blocks, capacity = extension.plan_tensors(rowptr, batch)
-            args.plan = _RowPlan(bounds.data_ptr(), blocks, capacity, 0)
+            bounds, blocks, block_edges = extension.plan_tensors(rowptr, batch)
+            args.plan = _RowPlan(bounds.data_ptr(), blocks, block_edges, 0)
         self.args = args
         self.bands = bands
         self.batch, self.n = batch, n
@@ -1205,8 +1205,8 @@ class PreparedTick:
         if panels is not None:
             args.panels = ctypes.addressof(panels)
         elif bands is None:
-            bounds, blocks, capacity = extension.plan_tensors(rowptr, batch)
-            args.plan = _RowPlan(bounds.data_ptr(), blocks, capacity, 0)
+            bounds, blocks, block_edges = extension.plan_tensors(rowptr, batch)
+            args.plan = _RowPlan(bounds.data_ptr(), blocks, block_edges, 0)
         self.args, self._ref = args, ctypes.byref(args)
         self.bands, self._bands_ref = bands, (ctypes.byref(bands) if bands is not None else None)
         self.batch, self.n, self.shape, self.device = batch, n, state.shape, state.device
@@ -1296,8 +1296,8 @@ class PreparedBackward:
         if weight.dtype != torch.float32:
             raise RuntimeError("the tick backward needs float32 weights")
         args.matrix = extension._csr(state, rowptr, col, weight, None, None)
-        bounds, blocks, capacity = extension.plan_tensors(rowptr, batch)
-        args.plan = _RowPlan(bounds.data_ptr(), blocks, capacity, 0)
+        bounds, blocks, block_edges = extension.plan_tensors(rowptr, batch)
+        args.plan = _RowPlan(bounds.data_ptr(), blocks, block_edges, 0)
         for index in (out_rowptr, dst, weight_index):
             _index(index, state)
         if out_rowptr.numel() != n + 1 or dst.numel() != weight.numel() or \
@@ -1552,8 +1552,8 @@ class PreparedAccumulate:
         if panels is not None:
             args.panels = ctypes.addressof(panels)
         else:
-            bounds, blocks, capacity = extension.plan_tensors(rowptr, batch)
-            args.plan = _RowPlan(bounds.data_ptr(), blocks, capacity, 0)
+            bounds, blocks, block_edges = extension.plan_tensors(rowptr, batch)
+            args.plan = _RowPlan(bounds.data_ptr(), blocks, block_edges, 0)
         _check_float(out, source, "accumulated output")
         if out.shape != source.shape:
             raise RuntimeError("the accumulated output must be [B,N]")
